@@ -1,0 +1,198 @@
+/*
+ * sa_amd.h - C ABI of the MI355X (gfx950) streaming-attention library.
+ *
+ * Every entry point takes plain device pointers and sizes, runs asynchronously
+ * on the HIP stream it is given (NULL = the default stream), and returns an
+ * sa_status.  No C++ type and no exception crosses this boundary.  The C++
+ * mirror of the reference API (attention.h, tensor_cpp/kv_cache.h,
+ * tensor_cpp/ops.h, tensor_cpp/qwen3_ops.h) is built on top of these calls.
+ *
+ * Layouts are row-major.  "token-major" means [seq][token][head][head_dim],
+ * which is what a Q/K/V projection writes before any transpose.
+ */
+#ifndef SA_AMD_H
+#define SA_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SA_PAGE_TOKENS 64      /* tokens per KV-cache page */
+#define SA_MAX_HEAD_DIM 256
+
+typedef enum sa_status {
+    SA_OK = 0,
+    SA_EINVAL = -1,   /* bad argument (null pointer, unsupported size, ...) */
+    SA_ENOMEM = -2,   /* device allocation failed / workspace too small      */
+    SA_EFULL = -3,    /* KV cache has no room for the requested tokens       */
+    SA_EHIP = -4,     /* a HIP runtime call failed                           */
+    SA_ERANGE = -5    /* index (layer, sequence, length) out of range        */
+} sa_status;
+
+typedef enum sa_dtype {
+    SA_DTYPE_F32 = 0,
+    SA_DTYPE_BF16 = 1
+} sa_dtype;
+
+typedef void* sa_stream_t;   /* a hipStream_t */
+
+/* Message describing the last failure on the calling thread ("" if none). */
+const char* sa_last_error(void);
+
+/* ------------------------------------------------------------------------
+ * Single-query streaming attention (split-KV online softmax + LSE merge).
+ *
+ * Replaces the compute of streaming_attention_serial / _omp / _mpi_simple and
+ * naive_attention_serial / _omp (reference attention/src/attention.h:27-208,
+ * attention/src/streaming_serial.cpp:20-71, attention/src/streaming_omp.cpp:99-154).
+ * O = softmax(scale * Q K^T) V with Q [d], K and V [T][d], O [d], all fp32 on
+ * the device.  The reference API is unscaled: pass scale = 1.
+ * block_size must be > 0; it is the reference's streaming block and does not
+ * change the result beyond rounding.  T <= 0 writes a zero output.
+ * ws must hold sa_stream_attn_ws_bytes(T, d) bytes (NULL allowed when that is 0).
+ * ------------------------------------------------------------------------ */
+size_t sa_stream_attn_ws_bytes(int T, int d);
+sa_status sa_stream_attn_f32(const float* Q, const float* K, const float* V,
+                             int T, int d, int block_size, float scale,
+                             float* O, void* ws, size_t ws_bytes,
+                             sa_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Dense multi-head single-query (decode) attention with grouped KV heads.
+ *
+ * Replaces the compute of ops::self_attention_streaming and of the decode
+ * (q_len = 1) case of ops::self_attention (reference tensor_cpp/src/ops.cpp:964-1017
+ * and :514-641), without materialising repeat_kv (qwen3_ops.cpp:194-234):
+ * query head h reads KV head h / (n_q_heads / n_kv_heads).
+ * q [batch][n_q_heads][d], k and v [batch][n_kv_heads][T][d], out like q; fp32.
+ * out = softmax(scale * q k^T) v  (the mathematically correct decode; the
+ * reference's streaming decode multiplies the output by scale instead, see
+ * compat_scale_on_output in tensor_cpp/ops.h).
+ * ------------------------------------------------------------------------ */
+size_t sa_decode_dense_ws_bytes(int batch, int n_q_heads, int T, int d);
+sa_status sa_decode_dense_f32(const float* q, const float* k, const float* v,
+                              int batch, int n_q_heads, int n_kv_heads, int T, int d,
+                              float scale, float* out, void* ws, size_t ws_bytes,
+                              sa_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Paged KV cache (64-token pages, int32 block tables, fp32 or bf16 storage).
+ *
+ * Replaces tensor_cpp::qwen3::KVCache (reference
+ * tensor_cpp/include/tensor_cpp/kv_cache.h:27-238).  Storage per layer:
+ * K pool and V pool of [num_pages][num_kv_heads][64][head_dim].
+ * Sequence s owns pages block_table[s][0..]; token t of s lives in page
+ * block_table[s][t / 64], row t % 64.  seq_len[s] is the committed length:
+ * appends write at positions seq_len[s] + i and become visible to later
+ * steps only after sa_kvcache_commit (append-then-commit, as the reference's
+ * update()/increment_seq_len()).
+ * ------------------------------------------------------------------------ */
+typedef struct sa_kv_desc {
+    int num_layers;
+    int num_kv_heads;
+    int head_dim;           /* 64, 128 or 256 */
+    int max_seqs;
+    int max_pages_per_seq;
+    int num_pages;          /* pages in the pool shared by all sequences */
+    sa_dtype kv_dtype;
+} sa_kv_desc;
+
+typedef struct sa_kvcache sa_kvcache;
+
+sa_status sa_kvcache_create(const sa_kv_desc* desc, sa_kvcache** out);
+sa_status sa_kvcache_destroy(sa_kvcache* cache);
+/* All sequences back to length 0, pages returned to the pool, storage zeroed. */
+sa_status sa_kvcache_reset(sa_kvcache* cache, sa_stream_t stream);
+/* Make room for n_tokens tokens in total in sequence seq, taking pages from
+ * the free list in order.  SA_EFULL if the pool or the table row is exhausted. */
+sa_status sa_kvcache_reserve(sa_kvcache* cache, int seq, int n_tokens);
+/* Give sequence seq an explicit page list (replaces its current pages). */
+sa_status sa_kvcache_set_pages(sa_kvcache* cache, int seq, const int32_t* pages,
+                               int n_pages);
+/* Set the committed length of seq (host and device), within its reserved pages. */
+sa_status sa_kvcache_set_len(sa_kvcache* cache, int seq, int len, sa_stream_t stream);
+/* Committed length of seq as tracked on the host, or -1. */
+int sa_kvcache_len(const sa_kvcache* cache, int seq);
+/* Add n to the committed length of seqs[0..n_seqs) (host ids; NULL = 0..n_seqs-1). */
+sa_status sa_kvcache_commit(sa_kvcache* cache, const int32_t* seqs, int n_seqs, int n,
+                            sa_stream_t stream);
+/* Device pointers into the cache, for callers that drive kernels themselves. */
+void* sa_kvcache_k_pool(sa_kvcache* cache, int layer);
+void* sa_kvcache_v_pool(sa_kvcache* cache, int layer);
+int32_t* sa_kvcache_block_table(sa_kvcache* cache);   /* [max_seqs][max_pages_per_seq] */
+int32_t* sa_kvcache_seq_lens(sa_kvcache* cache);      /* [max_seqs] committed lengths */
+size_t sa_kvcache_bytes(const sa_kvcache* cache);
+
+/* ------------------------------------------------------------------------
+ * RoPE tables, built exactly as the reference: inv_freq[i] = 1/theta^(i/D),
+ * cos/sin[pos][i] = cos/sin(float(pos) * inv_freq[i]) in fp32
+ * (reference tensor_cpp/src/qwen3_ops.cpp:70-104).  d_cos and d_sin are
+ * device buffers of max_pos * head_dim/2 floats.
+ * ------------------------------------------------------------------------ */
+sa_status sa_rope_table_init(float* d_cos, float* d_sin, int max_pos, int head_dim,
+                             float theta, sa_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Fused per-head q/k RMSNorm + rotate-half RoPE + K/V append.
+ *
+ * Replaces the QK-norm loops, the RoPE at position current_seq_len + s, the
+ * concat and KVCache::update of the reference decoder layer (reference
+ * tensor_cpp/src/qwen3_ops.cpp:697-861, kv_cache.h:94-130).
+ * q [n_seq][S][n_q_heads][D], k and v [n_seq][S][n_kv_heads][D], fp32,
+ * token-major.  seq_ids: device [n_seq] cache rows, or NULL for 0..n_seq-1.
+ * Token s of sequence i is written at position seq_len[seq_ids[i]] + s.
+ * q_norm_w / k_norm_w: [D] RMSNorm weights, or NULL to skip the norm
+ * (y = x / sqrt(mean(x^2) + eps) * w).  rope_cos / rope_sin: tables from
+ * sa_rope_table_init with rope_max_pos rows, or NULL to skip RoPE.
+ * q may be NULL (K/V append only); otherwise q_out receives the normed and
+ * rotated q in q's layout.  The caller must have reserved the pages.
+ * ------------------------------------------------------------------------ */
+sa_status sa_qknorm_rope_append(sa_kvcache* cache, int layer,
+                                const float* q, const float* k, const float* v,
+                                int n_seq, int S, const int32_t* seq_ids, int n_q_heads,
+                                const float* q_norm_w, const float* k_norm_w, float eps,
+                                const float* rope_cos, const float* rope_sin, int rope_max_pos,
+                                float* q_out, sa_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Paged GQA decode attention (split-KV online softmax + LSE merge).
+ *
+ * Replaces repeat_kv + ops::self_attention_streaming / self_attention on the
+ * cache path (reference tensor_cpp/src/qwen3_ops.cpp:863-909).  Each sequence
+ * i attends over its first seq_len[seq_ids[i]] + n_pending tokens, where
+ * n_pending counts tokens appended but not yet committed (1 in a decode
+ * step).  q [n_seq][n_q_heads][D] fp32, out likewise.
+ * ws must hold sa_paged_decode_ws_bytes(...) bytes.
+ * ------------------------------------------------------------------------ */
+size_t sa_paged_decode_ws_bytes(const sa_kvcache* cache, int n_seq, int n_q_heads);
+sa_status sa_paged_decode(const sa_kvcache* cache, int layer, const float* q,
+                          int n_seq, const int32_t* seq_ids, int n_q_heads, int n_pending,
+                          float scale, float* out, void* ws, size_t ws_bytes,
+                          sa_stream_t stream);
+
+/* Dense copy of a sequence's first len tokens: k_out, v_out [n_kv_heads][len][D]
+ * fp32 (serves KVCache::get_cached_keys / get_cached_values, kv_cache.h:161-237). */
+sa_status sa_kvcache_gather(const sa_kvcache* cache, int layer, int seq, int len,
+                            float* k_out, float* v_out, sa_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Causal prefill attention on MFMA.
+ *
+ * Replaces ops::self_attention_streaming_blockwise[_avx2] (reference
+ * tensor_cpp/src/ops.cpp:1027-1112, :1383-1599) without repeat_kv.
+ * q [batch][n_q_heads][L][D], k and v [batch][n_kv_heads][L][D] in dtype
+ * (fp32 or bf16); out [batch][n_q_heads][L][D] fp32.  Query i attends to keys
+ * 0..i with scores scale * q.k; accumulation is fp32.
+ * ------------------------------------------------------------------------ */
+sa_status sa_prefill_causal(const void* q, const void* k, const void* v, sa_dtype dtype,
+                            int batch, int n_q_heads, int n_kv_heads, int L, int D,
+                            float scale, float* out, sa_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SA_AMD_H */

@@ -1,0 +1,278 @@
+"""ctypes bindings of the CPU oracle (liboracle.so) and of the reference built
+from its own sources (_ref/libsa_ref.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, as the checker or the timed CPU baseline.  All
+arrays are numpy float32, C-contiguous.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+ORACLE_DIR = Path(__file__).resolve().parent
+ORACLE_LIB = ORACLE_DIR / "liboracle.so"
+REF_LIB = ORACLE_DIR / "_ref" / "libsa_ref.so"
+
+_P = C.c_void_p
+_I = C.c_int
+_F = C.c_float
+_D = C.c_double
+
+_ORACLE_SIGS = {
+    "or_streaming_serial": (None, [_P, _P, _P, _I, _I, _I, _P]),
+    "or_naive_serial": (None, [_P, _P, _P, _I, _I, _P]),
+    "or_streaming_omp": (None, [_P, _P, _P, _I, _I, _I, _I, _P]),
+    "or_l2_error": (_F, [_P, _P, _I]),
+    "or_max_error": (_F, [_P, _P, _I]),
+    "or_rms_norm_rows": (None, [_P, _P, _I, _I, _F, _I, _P]),
+    "or_rope_tables": (None, [_I, _I, _F, _P, _P]),
+    "or_apply_rope": (None, [_P, _I, _I, _P, _P, _P, _P]),
+    "or_decode_gqa": (None, [_P, _P, _P, _I, _I, _I, _I, _I, _F, _P]),
+    "or_decode_streaming_compat": (None, [_P, _P, _P, _I, _I, _I, _I, _F, _I, _P]),
+    "or_prefill_blockwise": (None, [_P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _P, _I, _P]),
+    "or_sdpa_f64": (None, [_P, _P, _P, _I, _I, _I, _D, _I, _I, _P]),
+}
+
+_REF_SIGS = {
+    "ref_streaming_serial": (None, [_P, _P, _P, _I, _I, _I, _P]),
+    "ref_naive_serial": (None, [_P, _P, _P, _I, _I, _P]),
+    "ref_streaming_omp": (None, [_P, _P, _P, _I, _I, _I, _I, _P]),
+    "ref_naive_omp": (None, [_P, _P, _P, _I, _I, _I, _P]),
+    "ref_l2_error": (_F, [_P, _P, _I]),
+    "ref_max_error": (_F, [_P, _P, _I]),
+    "ref_rope_freqs": (None, [_I, _I, _F, _P, _P]),
+    "ref_apply_rope": (None, [_P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P]),
+    "ref_repeat_kv": (None, [_P, _I, _I, _I, _I, _I, _P]),
+    "ref_self_attention": (None, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P]),
+    "ref_self_attention_streaming": (None, [_P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _P]),
+    "ref_blockwise": (None, [_P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _I, _P]),
+    "ref_layer_attention": (_I, [_I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _F, _I, _I, _I, _P, _P]),
+}
+
+
+def _bind(path: Path, sigs: dict) -> C.CDLL:
+    lib = C.CDLL(str(path))
+    for name, (res, args) in sigs.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags.c_contiguous, "arrays must be C-contiguous"
+    return a.ctypes.data
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class Oracle:
+    """The C restatement of the reference (oracle.c)."""
+
+    def __init__(self, path: Path = ORACLE_LIB):
+        if not path.exists():
+            raise RuntimeError(f"{path} missing: run `make -C oracle oracle`")
+        self.lib = _bind(path, _ORACLE_SIGS)
+
+    def streaming_serial(self, Q, K, V, block):
+        Q, K, V = _f32(Q), _f32(K), _f32(V)
+        T, d = (K.shape[0], K.shape[1]) if K.ndim == 2 else (0, Q.size)
+        O = np.empty(d, np.float32)
+        self.lib.or_streaming_serial(_p(Q), _p(K), _p(V), T, d, block, _p(O))
+        return O
+
+    def naive_serial(self, Q, K, V):
+        Q, K, V = _f32(Q), _f32(K), _f32(V)
+        T, d = K.shape
+        O = np.empty(d, np.float32)
+        self.lib.or_naive_serial(_p(Q), _p(K), _p(V), T, d, _p(O))
+        return O
+
+    def streaming_omp(self, Q, K, V, block, nthreads=0):
+        Q, K, V = _f32(Q), _f32(K), _f32(V)
+        T, d = K.shape
+        O = np.empty(d, np.float32)
+        self.lib.or_streaming_omp(_p(Q), _p(K), _p(V), T, d, block, nthreads, _p(O))
+        return O
+
+    def l2_error(self, a, b):
+        a, b = _f32(a).ravel(), _f32(b).ravel()
+        return float(self.lib.or_l2_error(_p(a), _p(b), a.size))
+
+    def max_error(self, a, b):
+        a, b = _f32(a).ravel(), _f32(b).ravel()
+        return float(self.lib.or_max_error(_p(a), _p(b), a.size))
+
+    def rms_norm_rows(self, x, w, eps=1e-6, eps_outside=False):
+        x, w = _f32(x), _f32(w)
+        D = x.shape[-1]
+        y = np.empty_like(x)
+        self.lib.or_rms_norm_rows(_p(x), _p(w), x.size // D, D, eps, int(eps_outside), _p(y))
+        return y
+
+    def rope_tables(self, max_pos, D, theta=1e6):
+        c = np.empty((max_pos, D // 2), np.float32)
+        s = np.empty_like(c)
+        self.lib.or_rope_tables(max_pos, D, theta, _p(c), _p(s))
+        return c, s
+
+    def apply_rope(self, x, pos, cos, sin):
+        """x [..., D] rows; pos int array with one entry per row."""
+        x = _f32(x)
+        D = x.shape[-1]
+        rows = x.size // D
+        pos = np.ascontiguousarray(np.broadcast_to(pos, (rows,)), dtype=np.int32)
+        y = np.empty_like(x)
+        self.lib.or_apply_rope(_p(x), rows, D, _p(pos), _p(_f32(cos)), _p(_f32(sin)), _p(y))
+        return y
+
+    def decode_gqa(self, q, k, v, scale):
+        q, k, v = _f32(q), _f32(k), _f32(v)
+        B, Hq, D = q.shape
+        Hkv, L = k.shape[1], k.shape[2]
+        out = np.empty_like(q)
+        self.lib.or_decode_gqa(_p(q), _p(k), _p(v), B, Hq, Hkv, L, D, scale, _p(out))
+        return out
+
+    def decode_streaming_compat(self, q, k, v, scale, block=64):
+        q, k, v = _f32(q), _f32(k), _f32(v)
+        B, H, D = q.shape
+        L = k.shape[2]
+        out = np.empty_like(q)
+        self.lib.or_decode_streaming_compat(_p(q), _p(k), _p(v), B, H, L, D, scale, block, _p(out))
+        return out
+
+    def prefill_blockwise(self, q, k, v, scale, kv_block=64, rows=None):
+        q, k, v = _f32(q), _f32(k), _f32(v)
+        B, Hq, L, D = q.shape
+        Hkv = k.shape[1]
+        out = np.zeros_like(q)
+        r = None if rows is None else np.ascontiguousarray(rows, dtype=np.int32)
+        self.lib.or_prefill_blockwise(_p(q), _p(k), _p(v), B, Hq, Hkv, L, D, scale, kv_block,
+                                      None if r is None else _p(r), 0 if r is None else r.size, _p(out))
+        return out
+
+    def sdpa_f64(self, q, k, v, scale, causal=False, pos0=0):
+        """q [nq, D], k/v [L, D] -> fp64 [nq, D]."""
+        q, k, v = _f32(q), _f32(k), _f32(v)
+        nq, D = q.shape
+        L = k.shape[0]
+        out = np.empty((nq, D), np.float64)
+        self.lib.or_sdpa_f64(_p(q), _p(k), _p(v), nq, L, D, float(scale), int(causal), pos0, _p(out))
+        return out
+
+
+class Reference:
+    """The reference compiled from its own sources (oracle/_ref/libsa_ref.so)."""
+
+    def __init__(self, path: Path = REF_LIB):
+        if not path.exists():
+            raise RuntimeError(f"{path} missing: run `make -C oracle ref` where the reference is mounted")
+        self.lib = _bind(path, _REF_SIGS)
+
+    @staticmethod
+    def available(path: Path = REF_LIB) -> bool:
+        return path.exists()
+
+    def streaming_serial(self, Q, K, V, block):
+        Q, K, V = _f32(Q), _f32(K), _f32(V)
+        T, d = K.shape
+        O = np.empty(d, np.float32)
+        self.lib.ref_streaming_serial(_p(Q), _p(K), _p(V), T, d, block, _p(O))
+        return O
+
+    def naive_serial(self, Q, K, V):
+        Q, K, V = _f32(Q), _f32(K), _f32(V)
+        T, d = K.shape
+        O = np.empty(d, np.float32)
+        self.lib.ref_naive_serial(_p(Q), _p(K), _p(V), T, d, _p(O))
+        return O
+
+    def streaming_omp(self, Q, K, V, block, nthreads=0):
+        Q, K, V = _f32(Q), _f32(K), _f32(V)
+        T, d = K.shape
+        O = np.empty(d, np.float32)
+        self.lib.ref_streaming_omp(_p(Q), _p(K), _p(V), T, d, block, nthreads, _p(O))
+        return O
+
+    def naive_omp(self, Q, K, V, nthreads=0):
+        Q, K, V = _f32(Q), _f32(K), _f32(V)
+        T, d = K.shape
+        O = np.empty(d, np.float32)
+        self.lib.ref_naive_omp(_p(Q), _p(K), _p(V), T, d, nthreads, _p(O))
+        return O
+
+    def l2_error(self, a, b):
+        a, b = _f32(a).ravel(), _f32(b).ravel()
+        return float(self.lib.ref_l2_error(_p(a), _p(b), a.size))
+
+    def max_error(self, a, b):
+        a, b = _f32(a).ravel(), _f32(b).ravel()
+        return float(self.lib.ref_max_error(_p(a), _p(b), a.size))
+
+    def rope_freqs(self, seq_len, D, theta):
+        c = np.empty((seq_len, D // 2), np.float32)
+        s = np.empty_like(c)
+        self.lib.ref_rope_freqs(seq_len, D, theta, _p(c), _p(s))
+        return c, s
+
+    def apply_rope(self, q, k, cos, sin):
+        q, k = _f32(q), _f32(k)
+        B, Hq, S, D = q.shape
+        Hkv = k.shape[1]
+        qo, ko = np.empty_like(q), np.empty_like(k)
+        self.lib.ref_apply_rope(_p(q), _p(k), B, Hq, Hkv, S, D, _p(_f32(cos)), _p(_f32(sin)), _p(qo),
+                                _p(ko))
+        return qo, ko
+
+    def repeat_kv(self, x, n_rep):
+        x = _f32(x)
+        B, H, S, D = x.shape
+        out = np.empty((B, H * n_rep, S, D), np.float32)
+        self.lib.ref_repeat_kv(_p(x), B, H, S, D, n_rep, _p(out))
+        return out
+
+    def self_attention(self, q, k, v, scale, causal):
+        q, k, v = _f32(q), _f32(k), _f32(v)
+        B, H, Sq, D = q.shape
+        Sk = k.shape[2]
+        out = np.empty_like(q)
+        self.lib.ref_self_attention(_p(q), _p(k), _p(v), B, H, Sq, Sk, D, int(causal), scale, _p(out))
+        return out
+
+    def self_attention_streaming(self, q, k, v, scale, block=64, nthreads=0):
+        q, k, v = _f32(q), _f32(k), _f32(v)
+        B, H, D = q.shape[0], q.shape[1], q.shape[-1]
+        L = k.shape[2]
+        out = np.empty((B, H, 1, D), np.float32)
+        self.lib.ref_self_attention_streaming(_p(q), _p(k), _p(v), B, H, L, D, scale, block, nthreads,
+                                              _p(out))
+        return out
+
+    def blockwise(self, q, k, v, scale, q_block=32, kv_block=64, variant=0):
+        q, k, v = _f32(q), _f32(k), _f32(v)
+        B, H, L, D = q.shape
+        out = np.empty_like(q)
+        self.lib.ref_blockwise(_p(q), _p(k), _p(v), B, H, L, D, scale, q_block, kv_block, variant,
+                               _p(out))
+        return out
+
+    def layer_attention(self, q, k, v, wq, wk, prompt_len, eps=1e-6, max_seq=4096, avx2=False,
+                        streaming=False):
+        """q [N, Hq, D], k/v [N, Hkv, D] token rows -> (attn [N, Hq, D], qkv_eff [N, (Hq+2Hkv)*D])."""
+        q, k, v, wq, wk = _f32(q), _f32(k), _f32(v), _f32(wq), _f32(wk)
+        N, Hq, D = q.shape
+        Hkv = k.shape[1]
+        attn = np.empty((N, Hq, D), np.float32)
+        eff = np.empty((N, (Hq + 2 * Hkv) * D), np.float32)
+        rc = self.lib.ref_layer_attention(Hq, Hkv, D, prompt_len, N - prompt_len, _p(q), _p(k), _p(v),
+                                          _p(wq), _p(wk), eps, max_seq, int(avx2), int(streaming),
+                                          _p(attn), _p(eff))
+        if rc != 0:
+            raise RuntimeError("reference layer raised")
+        return attn, eff

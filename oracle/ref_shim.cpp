@@ -1,0 +1,209 @@
+// ref_shim.cpp - extern "C" entry points into the reference implementation.
+//
+// TEST INFRASTRUCTURE ONLY.  Compiled together with the reference's own
+// sources (attention/src, tensor_cpp/src) by oracle/Makefile into
+// oracle/_ref/libsa_ref.so; used by tests/golden/make_golden.py to write
+// golden vectors, by tests to pin the oracle, and by bench.py as the timed
+// CPU baseline.  Nothing here re-implements the reference: each function only
+// marshals plain arrays into the reference's API and back.
+#include <omp.h>
+
+#include <cstring>
+#include <stdexcept>
+#include <vector>
+
+#include "attention.h"
+#include "tensor_cpp/kv_cache.h"
+#include "tensor_cpp/ops.h"
+#include "tensor_cpp/qwen3_ops.h"
+#include "tensor_cpp/qwen3_ops_avx.h"
+
+using tensor_cpp::Shape;
+using tensor_cpp::Tensor;
+namespace q3 = tensor_cpp::qwen3;
+
+namespace {
+Tensor make(const float* p, std::vector<size_t> dims) {
+    size_t n = 1;
+    for (size_t d : dims) n *= d;
+    return Tensor(std::vector<float>(p, p + n), Shape(dims));
+}
+void put(const Tensor& t, float* out) { std::memcpy(out, t.data(), t.size() * sizeof(float)); }
+void put(const std::vector<float>& v, float* out) { std::memcpy(out, v.data(), v.size() * sizeof(float)); }
+}  // namespace
+
+extern "C" {
+
+void ref_streaming_serial(const float* Q, const float* K, const float* V, int T, int d, int block,
+                          float* O) {
+    put(streaming_attention_serial(Q, K, V, T, d, block), O);
+}
+
+void ref_naive_serial(const float* Q, const float* K, const float* V, int T, int d, float* O) {
+    put(naive_attention_serial(Q, K, V, T, d), O);
+}
+
+void ref_streaming_omp(const float* Q, const float* K, const float* V, int T, int d, int block,
+                       int nthreads, float* O) {
+    put(streaming_attention_omp(Q, K, V, T, d, block, nthreads), O);
+}
+
+void ref_naive_omp(const float* Q, const float* K, const float* V, int T, int d, int nthreads,
+                   float* O) {
+    put(naive_attention_omp(Q, K, V, T, d, nthreads), O);
+}
+
+float ref_l2_error(const float* a, const float* b, int n) { return compute_l2_error(a, b, n); }
+float ref_max_error(const float* a, const float* b, int n) { return compute_max_error(a, b, n); }
+
+// compute_rope_freqs(seq_len, head_dim, theta) -> cos, sin [seq_len][D/2]
+void ref_rope_freqs(int seq_len, int D, float theta, float* cos_out, float* sin_out) {
+    auto cs = q3::compute_rope_freqs(seq_len, D, theta);
+    put(cs.first, cos_out);
+    put(cs.second, sin_out);
+}
+
+// apply_rotary_pos_emb on q [B][Hq][S][D], k [B][Hkv][S][D] with cos/sin [S][D/2]
+void ref_apply_rope(const float* q, const float* k, int B, int Hq, int Hkv, int S, int D,
+                    const float* cos_t, const float* sin_t, float* q_out, float* k_out) {
+    Tensor tq = make(q, {(size_t)B, (size_t)Hq, (size_t)S, (size_t)D});
+    Tensor tk = make(k, {(size_t)B, (size_t)Hkv, (size_t)S, (size_t)D});
+    Tensor tc = make(cos_t, {(size_t)S, (size_t)D / 2});
+    Tensor ts = make(sin_t, {(size_t)S, (size_t)D / 2});
+    auto r = q3::apply_rotary_pos_emb(tq, tk, tc, ts);
+    put(r.first, q_out);
+    put(r.second, k_out);
+}
+
+void ref_repeat_kv(const float* x, int B, int Hkv, int S, int D, int n_rep, float* out) {
+    put(q3::repeat_kv(make(x, {(size_t)B, (size_t)Hkv, (size_t)S, (size_t)D}), n_rep), out);
+}
+
+// ops::self_attention on [B][H][Sq][D] x [B][H][Sk][D]; causal != 0 adds the
+// [Sk][Sk] causal mask (prefill), otherwise an all-zero [1,1,1,Sk] mask (decode).
+void ref_self_attention(const float* q, const float* k, const float* v, int B, int H, int Sq, int Sk,
+                        int D, int causal, float scale, float* out) {
+    Tensor tq = make(q, {(size_t)B, (size_t)H, (size_t)Sq, (size_t)D});
+    Tensor tk = make(k, {(size_t)B, (size_t)H, (size_t)Sk, (size_t)D});
+    Tensor tv = make(v, {(size_t)B, (size_t)H, (size_t)Sk, (size_t)D});
+    Tensor mask;
+    if (causal) {
+        mask = q3::create_causal_mask(Sk).view({1, 1, (size_t)Sk, (size_t)Sk});
+    } else {
+        mask = Tensor(std::vector<float>((size_t)Sk, 0.0f), Shape({1, 1, 1, (size_t)Sk}));
+    }
+    put(tensor_cpp::ops::self_attention(tq, tk, tv, &mask, scale), out);
+}
+
+// nthreads > 0 sets the OpenMP thread count for the call (restored afterwards).
+void ref_self_attention_streaming(const float* q, const float* k, const float* v, int B, int H, int L,
+                                  int D, float scale, int block, int nthreads, float* out) {
+    const int saved = omp_get_max_threads();
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+    Tensor tq = make(q, {(size_t)B, (size_t)H, 1, (size_t)D});
+    Tensor tk = make(k, {(size_t)B, (size_t)H, (size_t)L, (size_t)D});
+    Tensor tv = make(v, {(size_t)B, (size_t)H, (size_t)L, (size_t)D});
+    put(tensor_cpp::ops::self_attention_streaming(tq, tk, tv, scale, block), out);
+    omp_set_num_threads(saved);
+}
+
+// variant: 0 = self_attention_streaming_blockwise, 1 = _avx2, 2 = _avx2_cache_optimized
+void ref_blockwise(const float* q, const float* k, const float* v, int B, int H, int L, int D,
+                   float scale, int q_block, int kv_block, int variant, float* out) {
+    Tensor tq = make(q, {(size_t)B, (size_t)H, (size_t)L, (size_t)D});
+    Tensor tk = make(k, {(size_t)B, (size_t)H, (size_t)L, (size_t)D});
+    Tensor tv = make(v, {(size_t)B, (size_t)H, (size_t)L, (size_t)D});
+    namespace ops = tensor_cpp::ops;
+    if (variant == 1)
+        put(ops::self_attention_streaming_blockwise_avx2(tq, tk, tv, scale, q_block, kv_block), out);
+    else if (variant == 2)
+        put(ops::self_attention_streaming_blockwise_avx2_cache_optimized(tq, tk, tv, scale, q_block,
+                                                                          kv_block), out);
+    else
+        put(ops::self_attention_streaming_blockwise(tq, tk, tv, scale, q_block, kv_block), out);
+}
+
+// Drive one reference decoder layer with a KVCache through a prompt of
+// prompt_len tokens and then n_steps single-token steps, and recover the
+// attention output of every call.
+//
+// The layer is wired so that its attention output appears verbatim in its
+// output: hidden rows are [q | k | v | 0] (width W = 2*Hq*D + 2*Hkv*D), the
+// combined QKV projection is [I | 0], o_proj writes into the zero block, and
+// the MLP weights are zero.  The input RMSNorm (weight 1) rescales each row,
+// so the q/k/v the attention saw are x / sqrt(mean(x^2) + eps); they are
+// returned in qkv_eff so callers can feed the same values elsewhere.
+//
+// q_in [N][Hq*D], k_in/v_in [N][Hkv*D] with N = prompt_len + n_steps;
+// attn_out [N][Hq*D]; qkv_eff [N][(Hq+2Hkv)*D].
+// avx2 selects qwen3_decoder_layer_avx_with_cache; streaming selects
+// AttentionType::STREAMING.  Returns 0 on success, -1 on a reference exception.
+int ref_layer_attention(int Hq, int Hkv, int D, int prompt_len, int n_steps, const float* q_in,
+                        const float* k_in, const float* v_in, const float* wq, const float* wk,
+                        float eps, int max_seq, int avx2, int streaming, float* attn_out,
+                        float* qkv_eff) {
+    try {
+        const size_t qd = (size_t)Hq * D, kd = (size_t)Hkv * D;
+        const size_t proj = qd + 2 * kd;
+        const size_t W = proj + qd;
+        // Combined projection [I | 0] : [proj][W]; separate q/k/v for the AVX2 path.
+        std::vector<float> qkv(proj * W, 0.0f), qp(qd * W, 0.0f), kp(kd * W, 0.0f), vp(kd * W, 0.0f);
+        for (size_t r = 0; r < proj; ++r) qkv[r * W + r] = 1.0f;
+        for (size_t r = 0; r < qd; ++r) qp[r * W + r] = 1.0f;
+        for (size_t r = 0; r < kd; ++r) kp[r * W + qd + r] = 1.0f;
+        for (size_t r = 0; r < kd; ++r) vp[r * W + qd + kd + r] = 1.0f;
+        std::vector<float> op(W * qd, 0.0f);
+        for (size_t c = 0; c < qd; ++c) op[(proj + c) * qd + c] = 1.0f;
+        Tensor t_qkv(qkv, Shape({proj, W}));
+        Tensor t_qp(qp, Shape({qd, W})), t_kp(kp, Shape({kd, W})), t_vp(vp, Shape({kd, W}));
+        Tensor t_op(op, Shape({W, qd}));
+        Tensor ones(std::vector<float>(W, 1.0f), Shape({W}));
+        Tensor t_wq = make(wq, {(size_t)D});
+        Tensor t_wk = make(wk, {(size_t)D});
+        const size_t I = 8;
+        Tensor gate(std::vector<float>(I * W, 0.0f), Shape({I, W}));
+        Tensor up(std::vector<float>(I * W, 0.0f), Shape({I, W}));
+        Tensor down(std::vector<float>(W * I, 0.0f), Shape({W, I}));
+
+        q3::KVCache cache(1, 1, Hkv, D, max_seq);
+        auto cs = q3::compute_rope_freqs(cache.max_seq_len, D, 1000000.0f);
+        const auto type = streaming ? q3::AttentionType::STREAMING : q3::AttentionType::STANDARD;
+
+        int t0 = 0;
+        for (int call = 0; call <= n_steps; ++call) {
+            const int S = call == 0 ? prompt_len : 1;
+            std::vector<float> h((size_t)S * W, 0.0f);
+            for (int s = 0; s < S; ++s) {
+                const int t = t0 + s;
+                std::memcpy(&h[s * W], q_in + (size_t)t * qd, qd * sizeof(float));
+                std::memcpy(&h[s * W + qd], k_in + (size_t)t * kd, kd * sizeof(float));
+                std::memcpy(&h[s * W + qd + kd], v_in + (size_t)t * kd, kd * sizeof(float));
+            }
+            Tensor hidden(h, Shape({1, (size_t)S, W}));
+            Tensor normed = tensor_cpp::ops::rms_norm(hidden, &ones, eps);
+            for (int s = 0; s < S; ++s)
+                std::memcpy(qkv_eff + (size_t)(t0 + s) * proj, normed.data() + (size_t)s * W,
+                            proj * sizeof(float));
+            Tensor out;
+            if (avx2)
+                out = tensor_cpp::qwen3::avx2::qwen3_decoder_layer_avx_with_cache(
+                    hidden, &cache, 0, Hq, Hkv, D, eps, ones, t_qp, t_kp, t_vp, t_op, t_wq, t_wk, ones,
+                    gate, up, down, cs.first, cs.second, type);
+            else
+                out = q3::qwen3_decoder_layer_with_cache(hidden, &cache, 0, Hq, Hkv, D, eps, ones,
+                                                         t_qkv, t_op, t_wq, t_wk, ones, gate, up, down,
+                                                         cs.first, cs.second, type);
+            // Residual of the attention block is hidden itself: zero on the output columns.
+            for (int s = 0; s < S; ++s)
+                std::memcpy(attn_out + (size_t)(t0 + s) * qd, out.data() + (size_t)s * W + proj,
+                            qd * sizeof(float));
+            cache.increment_seq_len(S);
+            t0 += S;
+        }
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+}  // extern "C"

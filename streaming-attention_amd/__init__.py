@@ -1,0 +1,282 @@
+"""ctypes binding of libsa_amd.so, the gfx950 streaming-attention library.
+
+The directory name carries a hyphen, so load it by path:
+
+    import importlib.util, pathlib
+    spec = importlib.util.spec_from_file_location(
+        "streaming_attention_amd", "streaming-attention_amd/__init__.py",
+        submodule_search_locations=["streaming-attention_amd"])
+
+Device buffers are torch tensors (torch is used for device memory and streams
+only); every call goes through the C ABI declared in include/sa_amd.h.  There is
+no fallback: if the library is missing, `lib()` raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+LIB_PATH = PKG_DIR / "lib" / "libsa_amd.so"
+
+SA_OK = 0
+SA_EINVAL = -1
+SA_ENOMEM = -2
+SA_EFULL = -3
+SA_EHIP = -4
+SA_ERANGE = -5
+SA_DTYPE_F32 = 0
+SA_DTYPE_BF16 = 1
+PAGE_TOKENS = 64
+
+_STATUS_NAMES = {0: "SA_OK", -1: "SA_EINVAL", -2: "SA_ENOMEM", -3: "SA_EFULL",
+                 -4: "SA_EHIP", -5: "SA_ERANGE"}
+
+
+class SaError(RuntimeError):
+    def __init__(self, status: int, msg: str):
+        super().__init__(f"{_STATUS_NAMES.get(status, status)}: {msg}")
+        self.status = status
+
+
+class KvDesc(C.Structure):
+    _fields_ = [("num_layers", C.c_int), ("num_kv_heads", C.c_int), ("head_dim", C.c_int),
+                ("max_seqs", C.c_int), ("max_pages_per_seq", C.c_int), ("num_pages", C.c_int),
+                ("kv_dtype", C.c_int)]
+
+
+_P = C.c_void_p
+_I = C.c_int
+_F = C.c_float
+_SZ = C.c_size_t
+
+# name -> (restype, argtypes); mirrors include/sa_amd.h
+SIGNATURES = {
+    "sa_last_error": (C.c_char_p, []),
+    "sa_stream_attn_ws_bytes": (_SZ, [_I, _I]),
+    "sa_stream_attn_f32": (_I, [_P, _P, _P, _I, _I, _I, _F, _P, _P, _SZ, _P]),
+    "sa_decode_dense_ws_bytes": (_SZ, [_I, _I, _I, _I]),
+    "sa_decode_dense_f32": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _SZ, _P]),
+    "sa_kvcache_create": (_I, [C.POINTER(KvDesc), C.POINTER(_P)]),
+    "sa_kvcache_destroy": (_I, [_P]),
+    "sa_kvcache_reset": (_I, [_P, _P]),
+    "sa_kvcache_reserve": (_I, [_P, _I, _I]),
+    "sa_kvcache_set_pages": (_I, [_P, _I, _P, _I]),
+    "sa_kvcache_set_len": (_I, [_P, _I, _I, _P]),
+    "sa_kvcache_len": (_I, [_P, _I]),
+    "sa_kvcache_commit": (_I, [_P, _P, _I, _I, _P]),
+    "sa_kvcache_k_pool": (_P, [_P, _I]),
+    "sa_kvcache_v_pool": (_P, [_P, _I]),
+    "sa_kvcache_block_table": (_P, [_P]),
+    "sa_kvcache_seq_lens": (_P, [_P]),
+    "sa_kvcache_bytes": (_SZ, [_P]),
+    "sa_rope_table_init": (_I, [_P, _P, _I, _I, _F, _P]),
+    "sa_qknorm_rope_append": (_I, [_P, _I, _P, _P, _P, _I, _I, _P, _I, _P, _P, _F, _P, _P, _I,
+                                   _P, _P]),
+    "sa_paged_decode_ws_bytes": (_SZ, [_P, _I, _I]),
+    "sa_paged_decode": (_I, [_P, _I, _P, _I, _P, _I, _I, _F, _P, _P, _SZ, _P]),
+    "sa_kvcache_gather": (_I, [_P, _I, _I, _I, _P, _P, _P]),
+    "sa_prefill_causal": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _P]),
+}
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """Load libsa_amd.so once; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is missing: run `python streaming-attention_amd/build.py`")
+        handle = C.CDLL(str(LIB_PATH), mode=os.RTLD_NOW | os.RTLD_GLOBAL)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def check(status: int) -> None:
+    if status != SA_OK:
+        raise SaError(status, lib().sa_last_error().decode())
+
+
+def _ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream) -> int | None:
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    return stream.cuda_stream if hasattr(stream, "cuda_stream") else stream
+
+
+def _f32(t, name: str):
+    import torch
+    if t is None:
+        return None
+    if t.dtype != torch.float32 or not t.is_cuda or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous float32 CUDA tensor")
+    return t
+
+
+# ---------------------------------------------------------------- single query
+
+def stream_attn(Q, K, V, block_size: int = 64, scale: float = 1.0, out=None, ws=None, stream=None):
+    """O = softmax(scale Q K^T) V for Q [d], K/V [T, d] (fp32, device)."""
+    import torch
+    T, d = (K.shape[0], K.shape[1]) if K.dim() == 2 else (0, Q.numel())
+    out = torch.empty(d, dtype=torch.float32, device=Q.device) if out is None else out
+    need = lib().sa_stream_attn_ws_bytes(T, d)
+    if ws is None and need:
+        ws = torch.zeros(need, dtype=torch.uint8, device=Q.device)
+    check(lib().sa_stream_attn_f32(_ptr(_f32(Q, "Q")), _ptr(_f32(K, "K")), _ptr(_f32(V, "V")), T, d,
+                                   block_size, scale, _ptr(out), _ptr(ws), 0 if ws is None else ws.numel(),
+                                   _stream(stream)))
+    return out
+
+
+def decode_dense(q, k, v, scale: float, out=None, ws=None, stream=None):
+    """q [B, Hq, D], k/v [B, Hkv, T, D] -> out [B, Hq, D] (fp32)."""
+    import torch
+    B, Hq, D = q.shape
+    Hkv, T = k.shape[1], k.shape[2]
+    out = torch.empty_like(q) if out is None else out
+    need = lib().sa_decode_dense_ws_bytes(B, Hq, T, D)
+    if ws is None and need:
+        ws = torch.zeros(need, dtype=torch.uint8, device=q.device)
+    check(lib().sa_decode_dense_f32(_ptr(_f32(q, "q")), _ptr(_f32(k, "k")), _ptr(_f32(v, "v")), B, Hq,
+                                    Hkv, T, D, scale, _ptr(out), _ptr(ws),
+                                    0 if ws is None else ws.numel(), _stream(stream)))
+    return out
+
+
+# ---------------------------------------------------------------- KV cache
+
+class KVCache:
+    """Owner of an sa_kvcache handle (64-token pages, fp32 or bf16 storage)."""
+
+    def __init__(self, num_layers: int, num_kv_heads: int, head_dim: int, max_seqs: int,
+                 max_pages_per_seq: int, num_pages: int, kv_dtype: int = SA_DTYPE_F32):
+        self.desc = KvDesc(num_layers, num_kv_heads, head_dim, max_seqs, max_pages_per_seq,
+                           num_pages, kv_dtype)
+        h = C.c_void_p()
+        check(lib().sa_kvcache_create(C.byref(self.desc), C.byref(h)))
+        self.handle = h
+
+    def close(self) -> None:
+        if self.handle:
+            lib().sa_kvcache_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def reset(self, stream=None) -> None:
+        check(lib().sa_kvcache_reset(self.handle, _stream(stream)))
+
+    def reserve(self, seq: int, n_tokens: int) -> None:
+        check(lib().sa_kvcache_reserve(self.handle, seq, n_tokens))
+
+    def set_pages(self, seq: int, pages) -> None:
+        arr = (C.c_int32 * len(pages))(*[int(p) for p in pages])
+        check(lib().sa_kvcache_set_pages(self.handle, seq, arr, len(pages)))
+
+    def set_len(self, seq: int, n: int, stream=None) -> None:
+        check(lib().sa_kvcache_set_len(self.handle, seq, n, _stream(stream)))
+
+    def length(self, seq: int) -> int:
+        return lib().sa_kvcache_len(self.handle, seq)
+
+    def commit(self, n: int, seqs=None, n_seqs: int | None = None, stream=None) -> None:
+        if seqs is None:
+            check(lib().sa_kvcache_commit(self.handle, None, n_seqs or 0, n, _stream(stream)))
+        else:
+            arr = (C.c_int32 * len(seqs))(*[int(s) for s in seqs])
+            check(lib().sa_kvcache_commit(self.handle, arr, len(seqs), n, _stream(stream)))
+
+    def k_pool(self, layer: int) -> int:
+        return lib().sa_kvcache_k_pool(self.handle, layer)
+
+    def v_pool(self, layer: int) -> int:
+        return lib().sa_kvcache_v_pool(self.handle, layer)
+
+    def nbytes(self) -> int:
+        return lib().sa_kvcache_bytes(self.handle)
+
+    def append(self, layer: int, q, k, v, q_norm_w=None, k_norm_w=None, eps: float = 1e-6,
+               rope=None, q_out=None, seq_ids=None, stream=None):
+        """q [n, S, Hq, D] (or None), k/v [n, S, Hkv, D]; rope = (cos, sin) tables."""
+        n_seq, S = k.shape[0], k.shape[1]
+        Hq = 0 if q is None else q.shape[2]
+        cos, sin = (None, None) if rope is None else rope
+        max_pos = 0 if rope is None else cos.shape[0]
+        if q is not None and q_out is None:
+            import torch
+            q_out = torch.empty_like(q)
+        check(lib().sa_qknorm_rope_append(
+            self.handle, layer, _ptr(_f32(q, "q")), _ptr(_f32(k, "k")), _ptr(_f32(v, "v")), n_seq, S,
+            _ptr(seq_ids), Hq, _ptr(_f32(q_norm_w, "q_norm_w")), _ptr(_f32(k_norm_w, "k_norm_w")), eps,
+            _ptr(cos), _ptr(sin), max_pos, _ptr(q_out), _stream(stream)))
+        return q_out
+
+    def decode_ws_bytes(self, n_seq: int, n_q_heads: int) -> int:
+        return lib().sa_paged_decode_ws_bytes(self.handle, n_seq, n_q_heads)
+
+    def decode(self, layer: int, q, scale: float, n_pending: int = 0, out=None, ws=None,
+               seq_ids=None, stream=None):
+        """q [n_seq, Hq, D] -> out [n_seq, Hq, D]."""
+        import torch
+        n_seq, Hq, _ = q.shape
+        out = torch.empty_like(q) if out is None else out
+        if ws is None:
+            need = self.decode_ws_bytes(n_seq, Hq)
+            ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=q.device)
+        check(lib().sa_paged_decode(self.handle, layer, _ptr(_f32(q, "q")), n_seq, _ptr(seq_ids), Hq,
+                                    n_pending, scale, _ptr(out), _ptr(ws), ws.numel(), _stream(stream)))
+        return out
+
+    def gather(self, layer: int, seq: int, length: int, stream=None):
+        import torch
+        H, D = self.desc.num_kv_heads, self.desc.head_dim
+        k = torch.empty(H, length, D, dtype=torch.float32, device="cuda")
+        v = torch.empty_like(k)
+        check(lib().sa_kvcache_gather(self.handle, layer, seq, length, _ptr(k), _ptr(v),
+                                      _stream(stream)))
+        return k, v
+
+
+def rope_tables(max_pos: int, head_dim: int, theta: float = 1e6, device="cuda"):
+    import torch
+    cos = torch.empty(max_pos, head_dim // 2, dtype=torch.float32, device=device)
+    sin = torch.empty_like(cos)
+    check(lib().sa_rope_table_init(_ptr(cos), _ptr(sin), max_pos, head_dim, theta, _stream(None)))
+    return cos, sin
+
+
+# ---------------------------------------------------------------- prefill
+
+def prefill_causal(q, k, v, scale: float, out=None, stream=None):
+    """q [B, Hq, L, D], k/v [B, Hkv, L, D] (fp32 or bf16) -> out fp32 [B, Hq, L, D]."""
+    import torch
+    if q.dtype == torch.float32:
+        dt = SA_DTYPE_F32
+    elif q.dtype == torch.bfloat16:
+        dt = SA_DTYPE_BF16
+    else:
+        raise ValueError("q must be float32 or bfloat16")
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        if t.dtype != q.dtype or not t.is_cuda or not t.is_contiguous():
+            raise ValueError(f"{n} must be a contiguous CUDA tensor of q's dtype")
+    B, Hq, L, D = q.shape
+    Hkv = k.shape[1]
+    out = torch.empty(B, Hq, L, D, dtype=torch.float32, device=q.device) if out is None else out
+    check(lib().sa_prefill_causal(_ptr(q), _ptr(k), _ptr(v), dt, B, Hq, Hkv, L, D, scale, _ptr(out),
+                                  _stream(stream)))
+    return out

@@ -1,0 +1,592 @@
+// Split-KV single-query attention for gfx950: one kernel body serves the
+// single-head streaming attention of attention.h, dense multi-head GQA decode
+// and paged GQA decode.
+//
+// Algorithm (the reference's online softmax, reference utils/softmax_online.h:40-87,
+// plus its chunk merge, attention/src/streaming_omp.cpp:27-48):
+//   * the KV sequence of each (sequence, KV head) is cut into chunks; one
+//     workgroup (4 or 8 waves) owns a chunk and all query heads of the GQA
+//     group, so every K/V byte is read from HBM once;
+//   * a wave walks 16..64-token tiles of its chunk; each lane issues 16-byte
+//     loads so one wave-load covers 1 KiB of consecutive rows (coalesced), and
+//     the next tile's loads are in flight while the current tile is reduced;
+//   * scores are reduced across the lanes of a row with DPP / swizzle, the
+//     running max m and normaliser l are wave-uniform, and the output O is
+//     kept unnormalised (O = sum p_i V_i with p relative to m);
+//   * the waves merge through LDS; a chunk's (m, l, O) goes to the workspace
+//     and a second launch applies the log-sum-exp merge
+//     O = sum_c e^{m_c-M} O_c / sum_c e^{m_c-M} l_c; a sequence that fits one
+//     chunk is written directly and needs no merge.
+//
+// Workspace: [(m, l) per (sequence, q head, chunk)][O per (sequence, q head,
+// chunk)], fp32; nothing in it survives from one call to the next.
+#include "sa_internal.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+
+namespace sa {
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kSplitCap = 1024;     // hard cap on chunks per (sequence, KV head)
+constexpr int kSplitTarget = 256;   // default cap: keeps the final merge short
+
+template <int D, bool BF16>
+struct Geo {
+    static constexpr int kElemBytes = BF16 ? 2 : 4;
+    static constexpr int E = 16 / kElemBytes;       // elements per lane per load
+    static constexpr int LPR = D / E;               // lanes per K/V row
+    static constexpr int RPW = kWave / LPR;         // rows per wave-load
+    static constexpr int R = (RPW * 8 <= 64) ? 8 : 64 / RPW;  // loads per lane per tile
+    static constexpr int TILE = R * RPW;            // tokens per wave tile (divides 64)
+    static_assert(LPR >= 1 && LPR <= kWave, "unsupported head_dim");
+    static_assert(64 % TILE == 0, "tile must divide a page");
+};
+
+// Waves per workgroup: 8, or 4 when the per-wave LDS merge buffer would be large.
+template <int D, int NREP>
+constexpr int waves_for() { return NREP * D <= 512 ? 8 : 4; }
+
+struct DecodeArgs {
+    const float* q;          // [n_seq][n_q_heads][D]
+    const void* k;           // dense: [n_seq][n_kv][T][D]; paged: pool [pages][n_kv][64][D]
+    const void* v;
+    float* out;              // [n_seq][n_q_heads][D]
+    float* part_ml;          // [n_seq*n_q_heads][n_split][2]
+    float* part_o;           // [n_seq*n_q_heads][n_split][D]
+    const int32_t* block_table;  // paged only: [max_seqs][max_pages]
+    const int32_t* seq_lens;     // paged only: committed lengths
+    const int32_t* seq_ids;      // paged only: may be null
+    int n_kv;
+    int n_q;
+    int T;                   // dense length
+    int max_pages;
+    int n_pending;
+    int chunk;               // tokens per workgroup, multiple of 64
+    int n_split;             // chunks per (sequence, kv head) in the grid
+    float scale;
+};
+
+// Widen one 16-byte slice of a K/V row to fp32.
+template <bool BF16, class V4>
+__device__ __forceinline__ void widen(const V4& raw, float* out) {
+    if constexpr (BF16) {
+        out[0] = bf16_lo(raw.x); out[1] = bf16_hi(raw.x);
+        out[2] = bf16_lo(raw.y); out[3] = bf16_hi(raw.y);
+        out[4] = bf16_lo(raw.z); out[5] = bf16_hi(raw.z);
+        out[6] = bf16_lo(raw.w); out[7] = bf16_hi(raw.w);
+    } else {
+        out[0] = __uint_as_float(raw.x); out[1] = __uint_as_float(raw.y);
+        out[2] = __uint_as_float(raw.z); out[3] = __uint_as_float(raw.w);
+    }
+}
+
+// Reduction over the whole workgroup of W waves; every thread gets the result.
+template <class Op, int W>
+__device__ __forceinline__ float block_reduce(float v, float* scratch) {
+    v = group_reduce<Op, 1, kWave>(v);
+    const int wave = threadIdx.x / kWave;
+    __syncthreads();
+    if ((threadIdx.x & (kWave - 1)) == 0) scratch[wave] = v;
+    __syncthreads();
+    float r = scratch[0];
+#pragma unroll
+    for (int w = 1; w < W; ++w) r = Op::apply(r, scratch[w]);
+    return r;
+}
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// One tile of K/V rows in registers: R 16-byte loads of K and of V per lane.
+template <int R>
+struct TileRegs {
+    u32x4 k[R];
+    u32x4 v[R];
+};
+
+template <int D, int NREP, bool BF16, bool PAGED>
+struct TileWalker {
+    using G = Geo<D, BF16>;
+    static constexpr int ROW_BYTES = D * G::kElemBytes;
+
+    const DecodeArgs& a;
+    const char* kbase;
+    const char* vbase;
+    int cache_row, g, t_end, grp, col;
+
+    // Start of tile t0 for this lane, or false when its page is unassigned.
+    __device__ __forceinline__ bool locate(int t0, const char*& kt, const char*& vt) const {
+        if constexpr (PAGED) {
+            const int page = a.block_table[(size_t)cache_row * a.max_pages + (t0 >> 6)];
+            if (page < 0) return false;
+            const size_t off = (((size_t)page * a.n_kv + g) * 64 + (t0 & 63)) * (size_t)ROW_BYTES;
+            kt = static_cast<const char*>(a.k) + off;
+            vt = static_cast<const char*>(a.v) + off;
+        } else {
+            kt = kbase + (size_t)t0 * ROW_BYTES;
+            vt = vbase + (size_t)t0 * ROW_BYTES;
+        }
+        return true;
+    }
+
+    // Issue the loads of tile t0 (rows past t_end re-read the last valid row).
+    __device__ __forceinline__ bool load(int t0, TileRegs<G::R>& regs) const {
+        const char* kt;
+        const char* vt;
+        if (!locate(t0, kt, vt)) return false;
+        const int n_valid = t_end - t0;
+        const bool full = n_valid >= G::TILE;
+#pragma unroll
+        for (int r = 0; r < G::R; ++r) {
+            const int row = r * G::RPW + grp;
+            const int rr = full ? row : min(row, n_valid - 1);
+            regs.k[r] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4*>(kt + (size_t)rr * ROW_BYTES + col * 16));
+            regs.v[r] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4*>(vt + (size_t)rr * ROW_BYTES + col * 16));
+        }
+        return true;
+    }
+};
+
+// Fold one loaded tile into the running (m, l, O) of every head of the group.
+template <int D, int NREP, bool BF16>
+__device__ __forceinline__ void consume(const TileRegs<Geo<D, BF16>::R>& regs, int n_valid, int grp,
+                                        const float (&qv)[NREP][Geo<D, BF16>::E], float (&m)[NREP],
+                                        float (&l)[NREP], float (&o)[NREP][Geo<D, BF16>::E]) {
+    using G = Geo<D, BF16>;
+    constexpr int E = G::E, LPR = G::LPR, RPW = G::RPW, R = G::R, TILE = G::TILE;
+    float s[R][NREP];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float kf[E];
+        widen<BF16>(regs.k[r], kf);
+#pragma unroll
+        for (int h = 0; h < NREP; ++h) {
+            float acc = 0.f;
+#pragma unroll
+            for (int e = 0; e < E; ++e) acc = fmaf(qv[h][e], kf[e], acc);
+            s[r][h] = group_reduce<OpSum, 1, LPR>(acc);
+        }
+    }
+    if (n_valid < TILE) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (r * RPW + grp >= n_valid) {
+#pragma unroll
+                for (int h = 0; h < NREP; ++h) s[r][h] = -INFINITY;
+            }
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < NREP; ++h) {
+        float mt = s[0][h];
+#pragma unroll
+        for (int r = 1; r < R; ++r) mt = fmaxf(mt, s[r][h]);
+        mt = group_reduce<OpMax, LPR, kWave>(mt);
+        const float m_new = fmaxf(m[h], mt);
+        const float alpha = __builtin_amdgcn_exp2f((m[h] - m_new) * kLog2e);
+        float lsum = 0.f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            s[r][h] = __builtin_amdgcn_exp2f((s[r][h] - m_new) * kLog2e);
+            lsum += s[r][h];
+        }
+        l[h] = l[h] * alpha + lsum;
+        m[h] = m_new;
+#pragma unroll
+        for (int e = 0; e < E; ++e) o[h][e] *= alpha;
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float vf[E];
+        widen<BF16>(regs.v[r], vf);
+#pragma unroll
+        for (int h = 0; h < NREP; ++h) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) o[h][e] = fmaf(s[r][h], vf[e], o[h][e]);
+        }
+    }
+}
+
+template <int D, int NREP, bool BF16, bool PAGED, int W>
+__global__ void __launch_bounds__(W * kWave)
+split_kv_decode_kernel(DecodeArgs a) {
+    using G = Geo<D, BF16>;
+    constexpr int E = G::E, LPR = G::LPR, TILE = G::TILE;
+    constexpr int THREADS = W * kWave;
+    constexpr bool kPrefetch = NREP <= 2;
+
+    const int split = blockIdx.x;
+    const int g = blockIdx.y;      // kv head
+    const int seq = blockIdx.z;    // batch row
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int col = lane % LPR;    // 16-byte column slice of a row
+    const int grp = lane / LPR;    // row inside a wave-load
+
+    int len;
+    int cache_row = seq;
+    if constexpr (PAGED) {
+        cache_row = a.seq_ids ? a.seq_ids[seq] : seq;
+        // Never walk past the block-table row, whatever the lengths say.
+        len = min(a.seq_lens[cache_row] + a.n_pending, a.max_pages * 64);
+    } else {
+        len = a.T;
+    }
+    const int t_begin = split * a.chunk;
+    if (t_begin >= len) return;    // whole workgroup: uniform exit
+    const int t_end = min(len, t_begin + a.chunk);
+    const int n_active = (len - 1) / a.chunk + 1;   // chunks holding tokens
+
+    // q slice of every head of the group, pre-multiplied by scale.
+    float qv[NREP][E];
+#pragma unroll
+    for (int h = 0; h < NREP; ++h) {
+        const float* qp = a.q + ((size_t)seq * a.n_q + g * NREP + h) * D + col * E;
+#pragma unroll
+        for (int e = 0; e < E; e += 4) {
+            float4 t = *reinterpret_cast<const float4*>(qp + e);
+            qv[h][e] = t.x * a.scale; qv[h][e + 1] = t.y * a.scale;
+            qv[h][e + 2] = t.z * a.scale; qv[h][e + 3] = t.w * a.scale;
+        }
+    }
+
+    float m[NREP], l[NREP], o[NREP][E];
+#pragma unroll
+    for (int h = 0; h < NREP; ++h) {
+        m[h] = -INFINITY; l[h] = 0.f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) o[h][e] = 0.f;
+    }
+
+    TileWalker<D, NREP, BF16, PAGED> walk{a, nullptr, nullptr, cache_row, g, t_end, grp, col};
+    if constexpr (!PAGED) {
+        const size_t off = ((size_t)seq * a.n_kv + g) * (size_t)a.T * TileWalker<D, NREP, BF16, PAGED>::ROW_BYTES;
+        walk.kbase = static_cast<const char*>(a.k) + off;
+        walk.vbase = static_cast<const char*>(a.v) + off;
+    }
+
+    constexpr int STRIDE = W * TILE;
+    int t0 = t_begin + wave * TILE;
+    if constexpr (kPrefetch) {
+        // Two register tiles: loads of the next tile fly while this one is reduced.
+        TileRegs<G::R> ra, rb;
+        bool va = t0 < t_end && walk.load(t0, ra);
+        while (t0 < t_end) {
+            const int t1 = t0 + STRIDE;
+            const bool vb = t1 < t_end && walk.load(t1, rb);
+            if (va) consume<D, NREP, BF16>(ra, t_end - t0, grp, qv, m, l, o);
+            if (t1 >= t_end) break;
+            const int t2 = t1 + STRIDE;
+            va = t2 < t_end && walk.load(t2, ra);
+            if (vb) consume<D, NREP, BF16>(rb, t_end - t1, grp, qv, m, l, o);
+            t0 = t2;
+        }
+    } else {
+        for (; t0 < t_end; t0 += STRIDE) {
+            TileRegs<G::R> ra;
+            if (walk.load(t0, ra)) consume<D, NREP, BF16>(ra, t_end - t0, grp, qv, m, l, o);
+        }
+    }
+
+    // Sum the row groups of this wave: l and O were accumulated per group.
+#pragma unroll
+    for (int h = 0; h < NREP; ++h) {
+        l[h] = group_reduce<OpSum, LPR, kWave>(l[h]);
+#pragma unroll
+        for (int e = 0; e < E; ++e) o[h][e] = group_reduce<OpSum, LPR, kWave>(o[h][e]);
+    }
+
+    __shared__ float sh_m[W][NREP];
+    __shared__ float sh_l[W][NREP];
+    __shared__ float sh_o[W][NREP][D];
+    if (lane < LPR) {
+#pragma unroll
+        for (int h = 0; h < NREP; ++h) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) sh_o[wave][h][col * E + e] = o[h][e];
+        }
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int h = 0; h < NREP; ++h) { sh_m[wave][h] = m[h]; sh_l[wave][h] = l[h]; }
+    }
+    __syncthreads();
+
+    // Merge the waves: this chunk's (m, l, O).
+    for (int i = threadIdx.x; i < NREP * D; i += THREADS) {
+        const int h = i / D, d = i % D;
+        float mm = sh_m[0][h];
+#pragma unroll
+        for (int w = 1; w < W; ++w) mm = fmaxf(mm, sh_m[w][h]);
+        float acc = 0.f, lsum = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            // A wave that saw no tile has m = -inf and contributes nothing.
+            const float c = (sh_m[w][h] == -INFINITY) ? 0.f
+                          : __builtin_amdgcn_exp2f((sh_m[w][h] - mm) * kLog2e);
+            acc = fmaf(c, sh_o[w][h][d], acc);
+            lsum = fmaf(c, sh_l[w][h], lsum);
+        }
+        const size_t bh = (size_t)seq * a.n_q + g * NREP + h;
+        if (n_active == 1) {
+            a.out[bh * D + d] = acc / lsum;
+        } else {
+            a.part_o[(bh * a.n_split + split) * D + d] = acc;
+            if (d == 0) {
+                a.part_ml[(bh * a.n_split + split) * 2 + 0] = mm;
+                a.part_ml[(bh * a.n_split + split) * 2 + 1] = lsum;
+            }
+        }
+    }
+}
+
+// Log-sum-exp merge of the chunk partials of one (sequence, query head):
+// O = sum_c e^{m_c-M} O_c / sum_c e^{m_c-M} l_c.  A separate launch: the
+// kernel boundary publishes the partials, where an in-kernel hand-off would
+// need a device-scope fence per workgroup (measured at ~57 ns each,
+// serialised across the device).  MT threads read the partials as float4
+// columns, PARTS chunks at a time, so one round trip covers up to MT/(D/4)
+// chunks.
+template <int D, bool PAGED, int MT>
+__global__ void __launch_bounds__(MT)
+lse_merge_kernel(DecodeArgs a) {
+    constexpr int V4 = D / 4;
+    constexpr int PARTS = MT / V4;
+    const int bh = blockIdx.x;
+    const int seq = bh / a.n_q;
+    int len;
+    if constexpr (PAGED) {
+        const int row = a.seq_ids ? a.seq_ids[seq] : seq;
+        len = min(a.seq_lens[row] + a.n_pending, a.max_pages * 64);
+    } else {
+        len = a.T;
+    }
+    const int n_active = len > 0 ? (len - 1) / a.chunk + 1 : 0;
+    if (n_active <= 1) return;     // written directly by the split kernel
+    __shared__ float sh_w[kSplitCap];
+    __shared__ float4 sh_red[PARTS][V4];
+    __shared__ float sh_scr[MT / kWave];
+    const float* ml = a.part_ml + (size_t)bh * a.n_split * 2;
+    const float4* po = reinterpret_cast<const float4*>(a.part_o + (size_t)bh * a.n_split * D);
+    float mx = -INFINITY;
+    for (int c = threadIdx.x; c < n_active; c += MT) mx = fmaxf(mx, ml[2 * c]);
+    mx = block_reduce<OpMax, MT / kWave>(mx, sh_scr);
+    float ls = 0.f;
+    for (int c = threadIdx.x; c < n_active; c += MT) {
+        const float w = __builtin_amdgcn_exp2f((ml[2 * c] - mx) * kLog2e);
+        sh_w[c] = w;
+        ls = fmaf(w, ml[2 * c + 1], ls);
+    }
+    ls = block_reduce<OpSum, MT / kWave>(ls, sh_scr);   // also orders the sh_w writes
+    const int j = threadIdx.x % V4;
+    const int part = threadIdx.x / V4;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+    for (int c = part; c < n_active; c += PARTS) {
+        const float4 x = po[(size_t)c * V4 + j];
+        const float w = sh_w[c];
+        acc.x = fmaf(w, x.x, acc.x); acc.y = fmaf(w, x.y, acc.y);
+        acc.z = fmaf(w, x.z, acc.z); acc.w = fmaf(w, x.w, acc.w);
+    }
+    sh_red[part][j] = acc;
+    __syncthreads();
+    if (threadIdx.x < V4) {
+        float4 t = sh_red[0][j];
+#pragma unroll
+        for (int pp = 1; pp < PARTS; ++pp) {
+            const float4 u = sh_red[pp][j];
+            t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
+        }
+        const float inv = 1.0f / ls;
+        reinterpret_cast<float4*>(a.out + (size_t)bh * D)[j] =
+            make_float4(t.x * inv, t.y * inv, t.z * inv, t.w * inv);
+    }
+}
+
+__global__ void zero_kernel(float* p, size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0.f;
+}
+
+int env_int(const char* name, int dflt) {
+    const char* s = std::getenv(name);
+    return s ? std::atoi(s) : dflt;
+}
+
+long long round64(long long c) { return (c + 63) / 64 * 64; }
+
+// Smallest chunk ever used: every wave of an 8-wave workgroup gets a tile.
+constexpr int kMinChunk = 128;
+
+// Tokens per workgroup for a launch over total_rows (sequence x KV head x
+// token) rows whose longest sequence may reach max_len tokens: about 8
+// workgroups per CU, at most kSplitTarget chunks per sequence, at least
+// kMinChunk, a multiple of the 64-token page.  SA_DECODE_CHUNK overrides the
+// first two rules (still at most kSplitCap chunks).
+int pick_chunk(long long total_rows, long long max_len) {
+    const long long cap_floor = round64((max_len + kSplitCap - 1) / kSplitCap);
+    const int forced = env_int("SA_DECODE_CHUNK", 0);
+    if (forced > 0) return (int)std::max<long long>({round64(forced), cap_floor, (long long)kMinChunk});
+    const long long target = 8LL * device_cu_count();
+    long long c = (total_rows + target - 1) / target;
+    c = std::max<long long>({c, (long long)kMinChunk, (max_len + kSplitTarget - 1) / kSplitTarget});
+    return (int)std::min<long long>(round64(c), 1LL << 30);
+}
+
+// Upper bound of the split count any call may use for sequences up to max_len.
+long long max_splits_for(long long max_len) {
+    const long long c = std::max<long long>(kMinChunk, round64((max_len + kSplitCap - 1) / kSplitCap));
+    return (max_len + c - 1) / c;
+}
+
+size_t ws_bytes_for(long long bh, long long n_split, int d) {
+    if (n_split <= 1) return 0;
+    return (size_t)(bh * n_split * (2 + d)) * sizeof(float);
+}
+
+void carve_ws(DecodeArgs& a, void* ws, long long bh) {
+    a.part_ml = static_cast<float*>(ws);
+    a.part_o = a.part_ml + (size_t)bh * a.n_split * 2;
+}
+
+template <int D, int NREP, bool BF16, bool PAGED>
+sa_status launch_decode(const DecodeArgs& a, int n_seq, hipStream_t st) {
+    constexpr int W = waves_for<D, NREP>();
+    dim3 grid(a.n_split, a.n_kv, n_seq);
+    hipLaunchKernelGGL((split_kv_decode_kernel<D, NREP, BF16, PAGED, W>), grid, dim3(W * kWave), 0, st, a);
+    SA_CHECK_LAUNCH();
+    if (a.n_split > 1) {
+        const dim3 mgrid(n_seq * a.n_q);
+        if (a.n_split >= 64)
+            hipLaunchKernelGGL((lse_merge_kernel<D, PAGED, 1024>), mgrid, dim3(1024), 0, st, a);
+        else
+            hipLaunchKernelGGL((lse_merge_kernel<D, PAGED, 256>), mgrid, dim3(256), 0, st, a);
+        SA_CHECK_LAUNCH();
+    }
+    return SA_OK;
+}
+
+template <int D, bool BF16, bool PAGED>
+sa_status dispatch_nrep(const DecodeArgs& a, int n_seq, int nrep, hipStream_t st) {
+    switch (nrep) {
+        case 1: return launch_decode<D, 1, BF16, PAGED>(a, n_seq, st);
+        case 2: return launch_decode<D, 2, BF16, PAGED>(a, n_seq, st);
+        case 4: return launch_decode<D, 4, BF16, PAGED>(a, n_seq, st);
+        case 8: return launch_decode<D, 8, BF16, PAGED>(a, n_seq, st);
+        default: return fail(SA_EINVAL, "n_q_heads / n_kv_heads must be 1, 2, 4 or 8");
+    }
+}
+
+template <bool BF16, bool PAGED>
+sa_status dispatch_decode(const DecodeArgs& a, int n_seq, int d, int nrep, hipStream_t st) {
+    switch (d) {
+        case 64: return dispatch_nrep<64, BF16, PAGED>(a, n_seq, nrep, st);
+        case 128: return dispatch_nrep<128, BF16, PAGED>(a, n_seq, nrep, st);
+        case 256: return dispatch_nrep<256, BF16, PAGED>(a, n_seq, nrep, st);
+        default: return fail(SA_EINVAL, "head_dim must be 64, 128 or 256");
+    }
+}
+
+bool supported_d(int d) { return d == 64 || d == 128 || d == 256; }
+
+}  // namespace
+
+// ----- dense -----------------------------------------------------------------
+
+sa_status decode_dense(const float* q, const float* k, const float* v, int batch, int n_q,
+                       int n_kv, int T, int d, float scale, float* out, void* ws,
+                       size_t ws_bytes, hipStream_t st) {
+    if (!q || !out || (T > 0 && (!k || !v))) return fail(SA_EINVAL, "null pointer");
+    if (batch <= 0 || n_q <= 0 || n_kv <= 0 || n_q % n_kv)
+        return fail(SA_EINVAL, "bad head counts");
+    if (!supported_d(d)) return fail(SA_EINVAL, "head_dim must be 64, 128 or 256");
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+        return fail(SA_EINVAL, "q, k, v and out must be 16-byte aligned");
+    if (T <= 0) {
+        size_t n = (size_t)batch * n_q * d;
+        hipLaunchKernelGGL(zero_kernel, dim3((n + 255) / 256), dim3(256), 0, st, out, n);
+        SA_CHECK_LAUNCH();
+        return SA_OK;
+    }
+    DecodeArgs a{};
+    a.q = q; a.k = k; a.v = v; a.out = out;
+    a.n_kv = n_kv; a.n_q = n_q; a.T = T; a.scale = scale;
+    a.chunk = pick_chunk((long long)batch * n_kv * T, T);
+    a.n_split = (T + a.chunk - 1) / a.chunk;
+    const long long bh = (long long)batch * n_q;
+    const size_t need = ws_bytes_for(bh, a.n_split, d);
+    if (need > 0) {
+        if (!ws || ws_bytes < need) return fail(SA_ENOMEM, "workspace too small for split-KV partials");
+        carve_ws(a, ws, bh);
+    }
+    return dispatch_decode<false, false>(a, batch, d, n_q / n_kv, st);
+}
+
+size_t decode_dense_ws(int batch, int n_q, int T, int d) {
+    if (batch <= 0 || n_q <= 0 || T <= 0 || !supported_d(d)) return 0;
+    // n_kv <= n_q: sized for the most groups and the most chunks.
+    return ws_bytes_for((long long)batch * n_q, max_splits_for(T), d);
+}
+
+// ----- paged -----------------------------------------------------------------
+
+size_t paged_ws(int n_seq, int n_q, int n_kv, int d, int max_pages) {
+    const long long max_tokens = (long long)max_pages * 64;
+    (void)n_kv;
+    return ws_bytes_for((long long)n_seq * n_q, max_splits_for(max_tokens), d);
+}
+
+sa_status decode_paged(const PagedView& c, const float* q, int n_seq, const int32_t* seq_ids,
+                       int n_q, int n_pending, int max_len, long long total_len, float scale,
+                       float* out, void* ws, size_t ws_bytes, hipStream_t st) {
+    if (!q || !out) return fail(SA_EINVAL, "null pointer");
+    if (n_seq <= 0 || n_q <= 0 || n_q % c.n_kv) return fail(SA_EINVAL, "bad head counts");
+    if (!aligned16(q) || !aligned16(out)) return fail(SA_EINVAL, "q and out must be 16-byte aligned");
+    if (max_len <= 0) max_len = 1;
+    DecodeArgs a{};
+    a.q = q; a.k = c.k_pool; a.v = c.v_pool; a.out = out;
+    a.block_table = c.block_table; a.seq_lens = c.seq_lens; a.seq_ids = seq_ids;
+    a.n_kv = c.n_kv; a.n_q = n_q; a.max_pages = c.max_pages; a.n_pending = n_pending;
+    a.scale = scale;
+    // The chunk bound uses the table capacity so the workspace size holds.
+    a.chunk = pick_chunk(total_len * c.n_kv, (long long)c.max_pages * 64);
+    a.n_split = (max_len + a.chunk - 1) / a.chunk;
+    const long long bh = (long long)n_seq * n_q;
+    const size_t need = ws_bytes_for(bh, a.n_split, c.d);
+    if (need > 0) {
+        if (!ws || ws_bytes < need) return fail(SA_ENOMEM, "workspace too small for split-KV partials");
+        carve_ws(a, ws, bh);
+    }
+    if (c.bf16) return dispatch_decode<true, true>(a, n_seq, c.d, n_q / c.n_kv, st);
+    return dispatch_decode<false, true>(a, n_seq, c.d, n_q / c.n_kv, st);
+}
+
+}  // namespace sa
+
+// ----- C ABI -------------------------------------------------------------------
+
+extern "C" size_t sa_stream_attn_ws_bytes(int T, int d) { return sa::decode_dense_ws(1, 1, T, d); }
+
+extern "C" sa_status sa_stream_attn_f32(const float* Q, const float* K, const float* V, int T,
+                                        int d, int block_size, float scale, float* O, void* ws,
+                                        size_t ws_bytes, sa_stream_t stream) {
+    sa::clear_error();
+    if (block_size <= 0) return sa::fail(SA_EINVAL, "block_size must be positive");
+    return sa::decode_dense(Q, K, V, 1, 1, 1, T, d, scale, O, ws, ws_bytes, sa::as_stream(stream));
+}
+
+extern "C" size_t sa_decode_dense_ws_bytes(int batch, int n_q_heads, int T, int d) {
+    return sa::decode_dense_ws(batch, n_q_heads, T, d);
+}
+
+extern "C" sa_status sa_decode_dense_f32(const float* q, const float* k, const float* v, int batch,
+                                         int n_q_heads, int n_kv_heads, int T, int d, float scale,
+                                         float* out, void* ws, size_t ws_bytes, sa_stream_t stream) {
+    sa::clear_error();
+    return sa::decode_dense(q, k, v, batch, n_q_heads, n_kv_heads, T, d, scale, out, ws, ws_bytes,
+                            sa::as_stream(stream));
+}

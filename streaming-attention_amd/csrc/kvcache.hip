@@ -1,0 +1,562 @@
+// Paged KV cache for gfx950 and the fused q/k RMSNorm + RoPE + K/V append.
+//
+// Storage: one device allocation holding, per layer, a K pool and a V pool of
+// [num_pages][n_kv_heads][64][head_dim] elements (fp32 or bf16).  A page of one
+// head is 64 consecutive rows, so the decode kernel streams 8-32 KiB of
+// contiguous memory per page.  Pages are handed out from a host free list;
+// block_table[seq][j] names the page holding tokens 64j..64j+63 (-1: none).
+//
+// The reference keeps a dense [B, Hkv, max_seq, D] fp32 tensor per layer and
+// copies it out on every step (reference tensor_cpp/include/tensor_cpp/kv_cache.h:27-238);
+// here the cache stays resident and the decode kernel reads it in place.
+#include "sa_internal.h"
+
+#include <algorithm>
+#include <cmath>
+#include <vector>
+
+struct sa_kvcache {
+    sa_kv_desc desc{};
+    int device = 0;
+    char* pool = nullptr;          // [layers][2][num_pages][n_kv][64][D]
+    size_t elem_bytes = 4;
+    size_t page_bytes = 0;         // one page of one of K / V: n_kv * 64 * D * elem
+    size_t layer_bytes = 0;        // K pool + V pool of one layer
+    size_t total_bytes = 0;
+    int32_t* d_table = nullptr;    // [max_seqs][max_pages_per_seq]
+    int32_t* d_lens = nullptr;     // [max_seqs]
+    std::vector<int32_t> h_table;
+    std::vector<int> h_lens;
+    std::vector<int> h_npages;     // pages assigned to each sequence
+    std::vector<int32_t> free_pages;
+};
+
+namespace sa {
+namespace {
+
+__global__ void fill_i32_kernel(int32_t* p, size_t n, int32_t v) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+__global__ void fill_zero_u128_kernel(uint4* p, size_t n) {
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        p[i] = make_uint4(0, 0, 0, 0);
+}
+
+// Row [first, first + n) of the block table, values passed by value.
+struct TableRow {
+    int32_t v[64];
+};
+
+__global__ void write_table_kernel(int32_t* dst, TableRow row, int n) {
+    if ((int)threadIdx.x < n) dst[threadIdx.x] = row.v[threadIdx.x];
+}
+
+struct SeqList {
+    int32_t id[32];
+};
+
+// seq_lens[ids[i]] = add ? seq_lens[ids[i]] + val : val
+__global__ void update_lens_kernel(int32_t* lens, SeqList ids, int n, int val, int add) {
+    int i = threadIdx.x;
+    if (i < n) lens[ids.id[i]] = add ? lens[ids.id[i]] + val : val;
+}
+
+__global__ void add_lens_range_kernel(int32_t* lens, int n, int val) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) lens[i] += val;
+}
+
+sa_status write_table_row(sa_kvcache* c, int seq, hipStream_t st) {
+    const int mp = c->desc.max_pages_per_seq;
+    for (int j0 = 0; j0 < mp; j0 += 64) {
+        TableRow row;
+        const int n = std::min(64, mp - j0);
+        for (int j = 0; j < n; ++j) row.v[j] = c->h_table[(size_t)seq * mp + j0 + j];
+        hipLaunchKernelGGL(write_table_kernel, dim3(1), dim3(64), 0, st,
+                           c->d_table + (size_t)seq * mp + j0, row, n);
+        SA_CHECK_LAUNCH();
+    }
+    return SA_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Fused QK-norm + RoPE + append.  One wave per (token, head row): waves
+// [0, n_q) handle query heads, [n_q, n_q + n_kv) handle a key head and its
+// value head.  Lane j holds the rotate-half pairs (i, i + D/2) for
+// i = j, j + 64, ... so RoPE needs no lane exchange.
+// ---------------------------------------------------------------------------
+struct AppendArgs {
+    const float* q; const float* k; const float* v;
+    float* q_out;
+    const float* wq; const float* wk;
+    const float* cos_t; const float* sin_t;
+    const int32_t* seq_ids;
+    const int32_t* seq_lens;
+    const int32_t* table;
+    char* k_pool; char* v_pool;
+    int n_q, n_kv, S, max_pages, rope_max_pos;
+    float eps;
+};
+
+template <int D, bool BF16>
+__global__ void __launch_bounds__(256)
+qknorm_rope_append_kernel(AppendArgs a) {
+    constexpr int H = D / 2;
+    constexpr int NP = (H + kWave - 1) / kWave;   // pairs per lane
+    const int lane = threadIdx.x & (kWave - 1);
+    const int row_id = blockIdx.x * 4 + threadIdx.x / kWave;
+    const int s = blockIdx.y;
+    const int i_seq = blockIdx.z;
+    const int n_rows = a.n_q + a.n_kv;
+    if (row_id >= n_rows) return;
+    const bool is_q = row_id < a.n_q;
+    if (is_q && !a.q) return;
+    const int head = is_q ? row_id : row_id - a.n_q;
+    const int cache_row = a.seq_ids ? a.seq_ids[i_seq] : i_seq;
+    const int pos = a.seq_lens[cache_row] + s;
+
+    const int nh = is_q ? a.n_q : a.n_kv;
+    const size_t src = (((size_t)i_seq * a.S + s) * nh + head) * D;
+    const float* x = (is_q ? a.q : a.k) + src;
+    const float* w = is_q ? a.wq : a.wk;
+
+    float lo[NP], hi[NP];
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < NP; ++c) {
+        const int i = lane + c * kWave;
+        lo[c] = (i < H) ? x[i] : 0.f;
+        hi[c] = (i < H) ? x[i + H] : 0.f;
+        ss = fmaf(lo[c], lo[c], fmaf(hi[c], hi[c], ss));
+    }
+    if (w) {
+        // RMSNorm with eps inside the sqrt (reference tensor_cpp/src/qwen3_ops.cpp:716-717).
+        ss = group_reduce<OpSum, 1, kWave>(ss);
+        const float rms = sqrtf(ss / (float)D + a.eps);
+#pragma unroll
+        for (int c = 0; c < NP; ++c) {
+            const int i = lane + c * kWave;
+            if (i < H) {
+                lo[c] = (lo[c] / rms) * w[i];
+                hi[c] = (hi[c] / rms) * w[i + H];
+            }
+        }
+    }
+    if (a.cos_t && pos < a.rope_max_pos) {
+        // x' = x cos + rotate_half(x) sin, rotate_half(x) = [-x2, x1]
+        // (reference tensor_cpp/src/qwen3_ops.cpp:30-64, 110-188).
+#pragma unroll
+        for (int c = 0; c < NP; ++c) {
+            const int i = lane + c * kWave;
+            if (i < H) {
+                const float cs = a.cos_t[(size_t)pos * H + i];
+                const float sn = a.sin_t[(size_t)pos * H + i];
+                const float l2 = lo[c] * cs - hi[c] * sn;
+                const float h2 = hi[c] * cs + lo[c] * sn;
+                lo[c] = l2;
+                hi[c] = h2;
+            }
+        }
+    }
+    if (is_q) {
+        float* y = a.q_out + src;
+#pragma unroll
+        for (int c = 0; c < NP; ++c) {
+            const int i = lane + c * kWave;
+            if (i < H) { y[i] = lo[c]; y[i + H] = hi[c]; }
+        }
+        return;
+    }
+    // Append K (normed, rotated) and V (as given) at pos.
+    if (pos >= a.max_pages * 64) return;
+    const int page = a.table[(size_t)cache_row * a.max_pages + (pos >> 6)];
+    if (page < 0) return;
+    const size_t row = (((size_t)page * a.n_kv + head) * 64 + (pos & 63)) * D;
+    const float* vx = a.v + src;
+#pragma unroll
+    for (int c = 0; c < NP; ++c) {
+        const int i = lane + c * kWave;
+        if (i < H) {
+            if constexpr (BF16) {
+                uint16_t* kd = reinterpret_cast<uint16_t*>(a.k_pool) + row;
+                uint16_t* vd = reinterpret_cast<uint16_t*>(a.v_pool) + row;
+                kd[i] = f32_to_bf16_rne(lo[c]);
+                kd[i + H] = f32_to_bf16_rne(hi[c]);
+                vd[i] = f32_to_bf16_rne(vx[i]);
+                vd[i + H] = f32_to_bf16_rne(vx[i + H]);
+            } else {
+                float* kd = reinterpret_cast<float*>(a.k_pool) + row;
+                float* vd = reinterpret_cast<float*>(a.v_pool) + row;
+                kd[i] = lo[c];
+                kd[i + H] = hi[c];
+                vd[i] = vx[i];
+                vd[i + H] = vx[i + H];
+            }
+        }
+    }
+}
+
+// Dense copy [n_kv][len][D] of one sequence (fp32 out).
+template <bool BF16>
+__global__ void gather_kernel(const char* k_pool, const char* v_pool, const int32_t* table_row,
+                              int n_kv, int D, int len, float* k_out, float* v_out) {
+    const int t = blockIdx.x;
+    const int h = blockIdx.y;
+    const int page = table_row[t >> 6];
+    const size_t row = (((size_t)page * n_kv + h) * 64 + (t & 63)) * D;
+    const size_t dst = ((size_t)h * len + t) * D;
+    for (int i = threadIdx.x; i < D; i += blockDim.x) {
+        float kv, vv;
+        if constexpr (BF16) {
+            kv = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(k_pool)[row + i] << 16);
+            vv = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(v_pool)[row + i] << 16);
+        } else {
+            kv = reinterpret_cast<const float*>(k_pool)[row + i];
+            vv = reinterpret_cast<const float*>(v_pool)[row + i];
+        }
+        if (k_out) k_out[dst + i] = kv;
+        if (v_out) v_out[dst + i] = vv;
+    }
+}
+
+bool valid_cache(const sa_kvcache* c) { return c && c->pool; }
+
+char* k_pool_of(const sa_kvcache* c, int layer) { return c->pool + (size_t)layer * c->layer_bytes; }
+char* v_pool_of(const sa_kvcache* c, int layer) {
+    return c->pool + (size_t)layer * c->layer_bytes + c->layer_bytes / 2;
+}
+
+}  // namespace
+}  // namespace sa
+
+using namespace sa;
+
+extern "C" sa_status sa_kvcache_create(const sa_kv_desc* d, sa_kvcache** out) {
+    clear_error();
+    if (!d || !out) return fail(SA_EINVAL, "null pointer");
+    *out = nullptr;
+    if (d->num_layers <= 0 || d->num_kv_heads <= 0 || d->max_seqs <= 0 ||
+        d->max_pages_per_seq <= 0 || d->num_pages <= 0)
+        return fail(SA_EINVAL, "cache dimensions must be positive");
+    if (d->head_dim != 64 && d->head_dim != 128 && d->head_dim != 256)
+        return fail(SA_EINVAL, "head_dim must be 64, 128 or 256");
+    if (d->kv_dtype != SA_DTYPE_F32 && d->kv_dtype != SA_DTYPE_BF16)
+        return fail(SA_EINVAL, "kv_dtype must be F32 or BF16");
+    auto* c = new sa_kvcache();
+    c->desc = *d;
+    hipGetDevice(&c->device);
+    c->elem_bytes = d->kv_dtype == SA_DTYPE_BF16 ? 2 : 4;
+    c->page_bytes = (size_t)d->num_kv_heads * 64 * d->head_dim * c->elem_bytes;
+    c->layer_bytes = 2 * c->page_bytes * (size_t)d->num_pages;
+    c->total_bytes = c->layer_bytes * (size_t)d->num_layers;
+    const size_t n_table = (size_t)d->max_seqs * d->max_pages_per_seq;
+    hipError_t e = hipMalloc(&c->pool, c->total_bytes);
+    if (e != hipSuccess) {
+        delete c;
+        return fail(SA_ENOMEM, "KV pool allocation failed");
+    }
+    e = hipMalloc(&c->d_table, n_table * sizeof(int32_t));
+    if (e == hipSuccess) e = hipMalloc(&c->d_lens, (size_t)d->max_seqs * sizeof(int32_t));
+    if (e != hipSuccess) {
+        hipFree(c->pool); hipFree(c->d_table); hipFree(c->d_lens);
+        delete c;
+        return fail(SA_ENOMEM, "KV table allocation failed");
+    }
+    c->h_table.assign(n_table, -1);
+    c->h_lens.assign(d->max_seqs, 0);
+    c->h_npages.assign(d->max_seqs, 0);
+    *out = c;
+    sa_status st = sa_kvcache_reset(c, nullptr);
+    if (st == SA_OK) {
+        hipError_t se = hipStreamSynchronize(nullptr);
+        if (se != hipSuccess) st = hip_fail(se, "hipStreamSynchronize");
+    }
+    if (st != SA_OK) {
+        sa_kvcache_destroy(c);
+        *out = nullptr;
+    }
+    return st;
+}
+
+extern "C" sa_status sa_kvcache_destroy(sa_kvcache* c) {
+    clear_error();
+    if (!c) return SA_OK;
+    hipDeviceSynchronize();
+    hipFree(c->pool);
+    hipFree(c->d_table);
+    hipFree(c->d_lens);
+    delete c;
+    return SA_OK;
+}
+
+extern "C" sa_status sa_kvcache_reset(sa_kvcache* c, sa_stream_t stream) {
+    clear_error();
+    if (!valid_cache(c)) return fail(SA_EINVAL, "invalid cache");
+    hipStream_t st = as_stream(stream);
+    const size_t n_table = c->h_table.size();
+    std::fill(c->h_table.begin(), c->h_table.end(), -1);
+    std::fill(c->h_lens.begin(), c->h_lens.end(), 0);
+    std::fill(c->h_npages.begin(), c->h_npages.end(), 0);
+    c->free_pages.resize(c->desc.num_pages);
+    // Stack: page 0 is handed out first.
+    for (int i = 0; i < c->desc.num_pages; ++i) c->free_pages[i] = c->desc.num_pages - 1 - i;
+    hipLaunchKernelGGL(fill_i32_kernel, dim3((n_table + 255) / 256), dim3(256), 0, st, c->d_table,
+                       n_table, -1);
+    SA_CHECK_LAUNCH();
+    hipLaunchKernelGGL(fill_i32_kernel, dim3((c->desc.max_seqs + 255) / 256), dim3(256), 0, st,
+                       c->d_lens, (size_t)c->desc.max_seqs, 0);
+    SA_CHECK_LAUNCH();
+    const size_t n16 = c->total_bytes / 16;
+    hipLaunchKernelGGL(fill_zero_u128_kernel, dim3(4096), dim3(256), 0, st,
+                       reinterpret_cast<uint4*>(c->pool), n16);
+    SA_CHECK_LAUNCH();
+    return SA_OK;
+}
+
+extern "C" sa_status sa_kvcache_reserve(sa_kvcache* c, int seq, int n_tokens) {
+    clear_error();
+    if (!valid_cache(c)) return fail(SA_EINVAL, "invalid cache");
+    if (seq < 0 || seq >= c->desc.max_seqs) return fail(SA_ERANGE, "sequence index out of range");
+    if (n_tokens < 0) return fail(SA_EINVAL, "n_tokens must be >= 0");
+    const int need = (n_tokens + 63) / 64;
+    if (need > c->desc.max_pages_per_seq)
+        return fail(SA_EFULL, "KV cache full, cannot append more tokens");
+    int have = c->h_npages[seq];
+    if (need <= have) return SA_OK;
+    if ((int)c->free_pages.size() < need - have)
+        return fail(SA_EFULL, "KV cache full, cannot append more tokens");
+    const int mp = c->desc.max_pages_per_seq;
+    for (; have < need; ++have) {
+        c->h_table[(size_t)seq * mp + have] = c->free_pages.back();
+        c->free_pages.pop_back();
+    }
+    c->h_npages[seq] = have;
+    return write_table_row(c, seq, nullptr);
+}
+
+extern "C" sa_status sa_kvcache_set_pages(sa_kvcache* c, int seq, const int32_t* pages, int n_pages) {
+    clear_error();
+    if (!valid_cache(c)) return fail(SA_EINVAL, "invalid cache");
+    if (seq < 0 || seq >= c->desc.max_seqs) return fail(SA_ERANGE, "sequence index out of range");
+    if (n_pages < 0 || n_pages > c->desc.max_pages_per_seq || (n_pages > 0 && !pages))
+        return fail(SA_EINVAL, "bad page list");
+    for (int j = 0; j < n_pages; ++j)
+        if (pages[j] < 0 || pages[j] >= c->desc.num_pages)
+            return fail(SA_ERANGE, "page id out of range");
+    const int mp = c->desc.max_pages_per_seq;
+    // Pages the sequence held go back to the free list unless reused.
+    std::vector<char> used(c->desc.num_pages, 0);
+    for (int j = 0; j < n_pages; ++j) used[pages[j]] = 1;
+    for (int j = 0; j < c->h_npages[seq]; ++j) {
+        const int32_t p = c->h_table[(size_t)seq * mp + j];
+        if (p >= 0 && !used[p]) c->free_pages.push_back(p);
+    }
+    // Pages taken from the free list.
+    std::vector<int32_t> keep;
+    keep.reserve(c->free_pages.size());
+    for (int32_t p : c->free_pages)
+        if (!used[p]) keep.push_back(p);
+    c->free_pages.swap(keep);
+    for (int j = 0; j < mp; ++j) c->h_table[(size_t)seq * mp + j] = j < n_pages ? pages[j] : -1;
+    c->h_npages[seq] = n_pages;
+    if (c->h_lens[seq] > n_pages * 64) c->h_lens[seq] = n_pages * 64;
+    return write_table_row(c, seq, nullptr);
+}
+
+extern "C" sa_status sa_kvcache_set_len(sa_kvcache* c, int seq, int len, sa_stream_t stream) {
+    clear_error();
+    if (!valid_cache(c)) return fail(SA_EINVAL, "invalid cache");
+    if (seq < 0 || seq >= c->desc.max_seqs) return fail(SA_ERANGE, "sequence index out of range");
+    if (len < 0 || len > c->h_npages[seq] * 64) return fail(SA_EFULL, "length exceeds reserved pages");
+    c->h_lens[seq] = len;
+    SeqList ids;
+    ids.id[0] = seq;
+    hipLaunchKernelGGL(update_lens_kernel, dim3(1), dim3(32), 0, as_stream(stream), c->d_lens, ids, 1,
+                       len, 0);
+    SA_CHECK_LAUNCH();
+    return SA_OK;
+}
+
+extern "C" int sa_kvcache_len(const sa_kvcache* c, int seq) {
+    if (!valid_cache(c) || seq < 0 || seq >= c->desc.max_seqs) return -1;
+    return c->h_lens[seq];
+}
+
+extern "C" sa_status sa_kvcache_commit(sa_kvcache* c, const int32_t* seqs, int n_seqs, int n,
+                                       sa_stream_t stream) {
+    clear_error();
+    if (!valid_cache(c)) return fail(SA_EINVAL, "invalid cache");
+    if (n_seqs < 0 || n_seqs > c->desc.max_seqs) return fail(SA_ERANGE, "bad sequence count");
+    if (n < 0) return fail(SA_EINVAL, "n must be >= 0");
+    for (int i = 0; i < n_seqs; ++i) {
+        const int s = seqs ? seqs[i] : i;
+        if (s < 0 || s >= c->desc.max_seqs) return fail(SA_ERANGE, "sequence index out of range");
+        if (c->h_lens[s] + n > c->h_npages[s] * 64)
+            return fail(SA_EFULL, "KV cache full, cannot append more tokens");
+    }
+    hipStream_t st = as_stream(stream);
+    for (int i = 0; i < n_seqs; ++i) c->h_lens[seqs ? seqs[i] : i] += n;
+    if (!seqs) {
+        hipLaunchKernelGGL(add_lens_range_kernel, dim3((n_seqs + 255) / 256), dim3(256), 0, st,
+                           c->d_lens, n_seqs, n);
+        SA_CHECK_LAUNCH();
+        return SA_OK;
+    }
+    for (int i0 = 0; i0 < n_seqs; i0 += 32) {
+        SeqList ids;
+        const int m = std::min(32, n_seqs - i0);
+        for (int i = 0; i < m; ++i) ids.id[i] = seqs[i0 + i];
+        hipLaunchKernelGGL(update_lens_kernel, dim3(1), dim3(32), 0, st, c->d_lens, ids, m, n, 1);
+        SA_CHECK_LAUNCH();
+    }
+    return SA_OK;
+}
+
+extern "C" void* sa_kvcache_k_pool(sa_kvcache* c, int layer) {
+    if (!valid_cache(c) || layer < 0 || layer >= c->desc.num_layers) return nullptr;
+    return k_pool_of(c, layer);
+}
+extern "C" void* sa_kvcache_v_pool(sa_kvcache* c, int layer) {
+    if (!valid_cache(c) || layer < 0 || layer >= c->desc.num_layers) return nullptr;
+    return v_pool_of(c, layer);
+}
+extern "C" int32_t* sa_kvcache_block_table(sa_kvcache* c) { return valid_cache(c) ? c->d_table : nullptr; }
+extern "C" int32_t* sa_kvcache_seq_lens(sa_kvcache* c) { return valid_cache(c) ? c->d_lens : nullptr; }
+extern "C" size_t sa_kvcache_bytes(const sa_kvcache* c) { return valid_cache(c) ? c->total_bytes : 0; }
+
+extern "C" sa_status sa_rope_table_init(float* d_cos, float* d_sin, int max_pos, int head_dim,
+                                        float theta, sa_stream_t stream) {
+    clear_error();
+    if (!d_cos || !d_sin) return fail(SA_EINVAL, "null pointer");
+    if (max_pos <= 0 || head_dim <= 0 || head_dim % 2) return fail(SA_EINVAL, "bad table size");
+    const int half = head_dim / 2;
+    // Same fp32 arithmetic as the reference (powf, then cosf / sinf of the
+    // fp32 angle), evaluated once on the host with the C library.
+    std::vector<float> inv(half), cs((size_t)max_pos * half), sn((size_t)max_pos * half);
+    for (int i = 0; i < half; ++i)
+        inv[i] = 1.0f / std::pow(theta, static_cast<float>(i) / static_cast<float>(head_dim));
+    for (int p = 0; p < max_pos; ++p) {
+        for (int i = 0; i < half; ++i) {
+            const float ang = static_cast<float>(p) * inv[i];
+            cs[(size_t)p * half + i] = std::cos(ang);
+            sn[(size_t)p * half + i] = std::sin(ang);
+        }
+    }
+    hipStream_t st = as_stream(stream);
+    SA_HIP_TRY(hipMemcpyAsync(d_cos, cs.data(), cs.size() * sizeof(float), hipMemcpyHostToDevice, st));
+    SA_HIP_TRY(hipMemcpyAsync(d_sin, sn.data(), sn.size() * sizeof(float), hipMemcpyHostToDevice, st));
+    SA_HIP_TRY(hipStreamSynchronize(st));
+    return SA_OK;
+}
+
+extern "C" sa_status sa_qknorm_rope_append(sa_kvcache* c, int layer, const float* q, const float* k,
+                                           const float* v, int n_seq, int S, const int32_t* seq_ids,
+                                           int n_q_heads, const float* q_norm_w,
+                                           const float* k_norm_w, float eps, const float* rope_cos,
+                                           const float* rope_sin, int rope_max_pos, float* q_out,
+                                           sa_stream_t stream) {
+    clear_error();
+    if (!valid_cache(c)) return fail(SA_EINVAL, "invalid cache");
+    if (layer < 0 || layer >= c->desc.num_layers) return fail(SA_ERANGE, "Layer index out of range");
+    if (!k || !v) return fail(SA_EINVAL, "null k or v");
+    if (q && (!q_out || n_q_heads <= 0)) return fail(SA_EINVAL, "q needs q_out and n_q_heads > 0");
+    if (n_seq <= 0 || S <= 0) return fail(SA_EINVAL, "n_seq and S must be positive");
+    if ((rope_cos == nullptr) != (rope_sin == nullptr)) return fail(SA_EINVAL, "cos and sin go together");
+    if (!seq_ids) {
+        if (n_seq > c->desc.max_seqs) return fail(SA_ERANGE, "sequence index out of range");
+        for (int i = 0; i < n_seq; ++i)
+            if (c->h_lens[i] + S > c->h_npages[i] * 64)
+                return fail(SA_EFULL, "KV cache full, cannot append more tokens");
+    }
+    if (rope_cos && !seq_ids) {
+        for (int i = 0; i < n_seq; ++i)
+            if (c->h_lens[i] + S > rope_max_pos) return fail(SA_ERANGE, "position beyond RoPE table");
+    }
+    AppendArgs a{};
+    a.q = q; a.k = k; a.v = v; a.q_out = q_out;
+    a.wq = q_norm_w; a.wk = k_norm_w; a.cos_t = rope_cos; a.sin_t = rope_sin;
+    a.seq_ids = seq_ids; a.seq_lens = c->d_lens; a.table = c->d_table;
+    a.k_pool = k_pool_of(c, layer); a.v_pool = v_pool_of(c, layer);
+    a.n_q = q ? n_q_heads : 0; a.n_kv = c->desc.num_kv_heads; a.S = S;
+    a.max_pages = c->desc.max_pages_per_seq; a.rope_max_pos = rope_max_pos; a.eps = eps;
+    const int rows = a.n_q + a.n_kv;
+    dim3 grid((rows + 3) / 4, S, n_seq);
+    hipStream_t st = as_stream(stream);
+    const bool bf = c->desc.kv_dtype == SA_DTYPE_BF16;
+    switch (c->desc.head_dim) {
+#define SA_APPEND_CASE(DD)                                                                        \
+    case DD:                                                                                      \
+        if (bf) hipLaunchKernelGGL((qknorm_rope_append_kernel<DD, true>), grid, dim3(256), 0, st, a); \
+        else hipLaunchKernelGGL((qknorm_rope_append_kernel<DD, false>), grid, dim3(256), 0, st, a); \
+        break;
+        SA_APPEND_CASE(64)
+        SA_APPEND_CASE(128)
+        SA_APPEND_CASE(256)
+#undef SA_APPEND_CASE
+        default: return fail(SA_EINVAL, "head_dim");
+    }
+    SA_CHECK_LAUNCH();
+    return SA_OK;
+}
+
+extern "C" size_t sa_paged_decode_ws_bytes(const sa_kvcache* c, int n_seq, int n_q_heads) {
+    if (!valid_cache(c) || n_seq <= 0 || n_q_heads <= 0) return 0;
+    return paged_ws(n_seq, n_q_heads, c->desc.num_kv_heads, c->desc.head_dim, c->desc.max_pages_per_seq);
+}
+
+extern "C" sa_status sa_paged_decode(const sa_kvcache* c, int layer, const float* q, int n_seq,
+                                     const int32_t* seq_ids, int n_q_heads, int n_pending, float scale,
+                                     float* out, void* ws, size_t ws_bytes, sa_stream_t stream) {
+    clear_error();
+    if (!valid_cache(c)) return fail(SA_EINVAL, "invalid cache");
+    if (layer < 0 || layer >= c->desc.num_layers) return fail(SA_ERANGE, "Layer index out of range");
+    if (n_pending < 0) return fail(SA_EINVAL, "n_pending must be >= 0");
+    if (n_seq > c->desc.max_seqs && !seq_ids) return fail(SA_ERANGE, "sequence index out of range");
+    // Grid sizing from the host-side lengths (all rows when ids live on the device).
+    const int rows = seq_ids ? c->desc.max_seqs : n_seq;
+    int max_len = 0;
+    long long total = 0;
+    for (int i = 0; i < rows; ++i) {
+        const int L = c->h_lens[i] + n_pending;
+        if (!seq_ids && L > c->h_npages[i] * 64)
+            return fail(SA_ERANGE, "Requested seq_len exceeds cached length");
+        max_len = std::max(max_len, L);
+        total += L;
+    }
+    if (seq_ids) total = total * n_seq / std::max(1, rows);
+    max_len = std::min(max_len, c->desc.max_pages_per_seq * 64);
+    PagedView pv;
+    pv.k_pool = k_pool_of(c, layer); pv.v_pool = v_pool_of(c, layer);
+    pv.block_table = c->d_table; pv.seq_lens = c->d_lens;
+    pv.n_kv = c->desc.num_kv_heads; pv.d = c->desc.head_dim;
+    pv.max_pages = c->desc.max_pages_per_seq; pv.bf16 = c->desc.kv_dtype == SA_DTYPE_BF16;
+    return decode_paged(pv, q, n_seq, seq_ids, n_q_heads, n_pending, max_len, total, scale, out, ws,
+                        ws_bytes, as_stream(stream));
+}
+
+extern "C" sa_status sa_kvcache_gather(const sa_kvcache* c, int layer, int seq, int len, float* k_out,
+                                       float* v_out, sa_stream_t stream) {
+    clear_error();
+    if (!valid_cache(c)) return fail(SA_EINVAL, "invalid cache");
+    if (layer < 0 || layer >= c->desc.num_layers) return fail(SA_ERANGE, "Layer index out of range");
+    if (seq < 0 || seq >= c->desc.max_seqs) return fail(SA_ERANGE, "sequence index out of range");
+    if (len < 0 || len > c->h_lens[seq]) return fail(SA_ERANGE, "Requested seq_len exceeds cached length");
+    if (len == 0) return SA_OK;
+    if (!k_out && !v_out) return fail(SA_EINVAL, "null outputs");
+    dim3 grid(len, c->desc.num_kv_heads);
+    const int32_t* row = c->d_table + (size_t)seq * c->desc.max_pages_per_seq;
+    hipStream_t st = as_stream(stream);
+    if (c->desc.kv_dtype == SA_DTYPE_BF16)
+        hipLaunchKernelGGL(gather_kernel<true>, grid, dim3(128), 0, st, k_pool_of(c, layer),
+                           v_pool_of(c, layer), row, c->desc.num_kv_heads, c->desc.head_dim, len,
+                           k_out, v_out);
+    else
+        hipLaunchKernelGGL(gather_kernel<false>, grid, dim3(128), 0, st, k_pool_of(c, layer),
+                           v_pool_of(c, layer), row, c->desc.num_kv_heads, c->desc.head_dim, len,
+                           k_out, v_out);
+    SA_CHECK_LAUNCH();
+    return SA_OK;
+}

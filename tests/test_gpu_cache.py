@@ -1,0 +1,302 @@
+"""GPU parity: paged KV cache, fused QK-norm + RoPE + append, paged GQA decode,
+and the one-layer Qwen3-0.6B-shape decode loop (128-token prompt + 100 steps).
+
+fp32 KV: max-abs <= 1e-4 and relative L2 <= 1e-5 against the oracle.
+bf16 KV: relative L2 <= 2e-2 against the fp32 oracle, and the oracle run on
+the same bf16-rounded K/V agrees to fp32 rounding.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import golden_inputs as gi
+
+pytestmark = pytest.mark.gpu
+
+HQ, HKV, D = 16, 8, 128
+SCALE = np.float32(1.0 / np.sqrt(D))
+
+
+def dev(a, dtype=np.float32):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=dtype)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def assert_f32(out, want, max_abs=1e-4, rl2=1e-5):
+    assert np.abs(out - want).max() <= max_abs, np.abs(out - want).max()
+    assert rel_l2(out, want) <= rl2, rel_l2(out, want)
+
+
+def make_cache(sa, kv_dtype, max_seqs=4, max_pages=80, num_pages=300, layers=2):
+    return sa.KVCache(layers, HKV, D, max_seqs, max_pages, num_pages, kv_dtype)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_append_gather_roundtrip_shuffled_pages(sa, synth, bf16):
+    cache = make_cache(sa, sa.SA_DTYPE_BF16 if bf16 else sa.SA_DTYPE_F32)
+    perm = synth.permutation(21, 1, 300)
+    lens = [1, 64, 65, 1000]
+    off = 0
+    for s, L in enumerate(lens):
+        n = (L + 63) // 64
+        cache.set_pages(s, perm[off:off + n])
+        off += n
+    for s, L in enumerate(lens):
+        k = synth.normal(22, s, (1, L, HKV, D))
+        v = synth.normal(23, s, (1, L, HKV, D))
+        ids = torch.tensor([s], dtype=torch.int32, device="cuda")
+        cache.append(1, None, dev(k), dev(v), seq_ids=ids)
+        cache.commit(L, seqs=[s])
+        gk, gv = cache.gather(1, s, L)
+        want_k = k[0].transpose(1, 0, 2)
+        want_v = v[0].transpose(1, 0, 2)
+        if bf16:
+            want_k, want_v = synth.bf16_round(want_k), synth.bf16_round(want_v)
+        np.testing.assert_array_equal(host(gk), want_k)
+        np.testing.assert_array_equal(host(gv), want_v)
+        assert cache.length(s) == L
+    cache.close()
+
+
+def test_fused_append_matches_oracle(sa, oracle, synth):
+    """q/k RMSNorm (eps in the sqrt) + rotate-half RoPE at pos = len + s."""
+    cache = make_cache(sa, sa.SA_DTYPE_F32)
+    cos, sin = sa.rope_tables(4096, D, 1e6)
+    ocos, osin = oracle.rope_tables(4096, D, 1e6)
+    np.testing.assert_array_equal(host(cos), ocos)
+    np.testing.assert_array_equal(host(sin), osin)
+    wq = 1 + synth.normal(24, 1, D, 0.02)
+    wk = 1 + synth.normal(24, 2, D, 0.02)
+    start = [0, 5, 70]
+    S = 3
+    for s, L0 in enumerate(start):
+        cache.reserve(s, L0 + S)
+        cache.set_len(s, L0)
+    q = synth.normal(25, 1, (3, S, HQ, D))
+    k = synth.normal(25, 2, (3, S, HKV, D))
+    v = synth.normal(25, 3, (3, S, HKV, D))
+    q_out = cache.append(0, dev(q), dev(k), dev(v), dev(wq), dev(wk), 1e-6, rope=(cos, sin))
+    q_out = host(q_out)
+    for s, L0 in enumerate(start):
+        pos_q = np.repeat(L0 + np.arange(S), HQ)
+        want_q = oracle.apply_rope(oracle.rms_norm_rows(q[s], wq, 1e-6), pos_q, ocos, osin)
+        assert_f32(q_out[s], want_q, 1e-5, 1e-6)
+    cache.commit(S, n_seqs=3)
+    for s, L0 in enumerate(start):
+        gk, gv = cache.gather(0, s, L0 + S)
+        pos_k = np.repeat(L0 + np.arange(S), HKV)
+        want_k = oracle.apply_rope(oracle.rms_norm_rows(k[s], wk, 1e-6), pos_k, ocos, osin)
+        assert_f32(host(gk)[:, L0:].transpose(1, 0, 2), want_k, 1e-5, 1e-6)
+        np.testing.assert_array_equal(host(gv)[:, L0:].transpose(1, 0, 2), v[s])
+    cache.close()
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_paged_decode_matches_oracle(sa, oracle, synth, bf16):
+    lens = [1, 63, 64, 65, 1000, 5000]
+    cache = sa.KVCache(1, HKV, D, len(lens), 80, 400, sa.SA_DTYPE_BF16 if bf16 else sa.SA_DTYPE_F32)
+    perm = synth.permutation(26, 1, 400)
+    off = 0
+    ks, vs = [], []
+    for s, L in enumerate(lens):
+        n = (L + 63) // 64
+        cache.set_pages(s, perm[off:off + n])
+        off += n
+        k = synth.normal(27, s, (1, L, HKV, D))
+        v = synth.normal(28, s, (1, L, HKV, D))
+        cache.append(0, None, dev(k), dev(v), seq_ids=torch.tensor([s], dtype=torch.int32, device="cuda"))
+        cache.commit(L, seqs=[s])
+        ks.append(k[0].transpose(1, 0, 2))
+        vs.append(v[0].transpose(1, 0, 2))
+    q = synth.normal(29, 1, (len(lens), HQ, D))
+    out = host(cache.decode(0, dev(q), float(SCALE)))
+    for s in range(len(lens)):
+        k, v = ks[s][None], vs[s][None]
+        exact = oracle.decode_gqa(q[s][None], k, v, SCALE)[0]
+        if bf16:
+            same_in = oracle.decode_gqa(q[s][None], synth.bf16_round(k), synth.bf16_round(v), SCALE)[0]
+            assert_f32(out[s], same_in)
+            assert rel_l2(out[s], exact) <= 2e-2
+        else:
+            assert_f32(out[s], exact)
+    cache.close()
+
+
+def test_paged_decode_seq_ids_subset(sa, oracle, synth):
+    """Decode a permuted subset of cache rows through device seq_ids."""
+    cache = sa.KVCache(1, HKV, D, 4, 20, 64, sa.SA_DTYPE_F32)
+    data = {}
+    for s, L in enumerate([100, 300, 7, 900]):
+        cache.reserve(s, L)
+        k = synth.normal(30, s, (1, L, HKV, D))
+        v = synth.normal(31, s, (1, L, HKV, D))
+        cache.append(0, None, dev(k), dev(v), seq_ids=torch.tensor([s], dtype=torch.int32, device="cuda"))
+        cache.commit(L, seqs=[s])
+        data[s] = (k[0].transpose(1, 0, 2)[None], v[0].transpose(1, 0, 2)[None])
+    ids = [3, 0, 2]
+    q = synth.normal(32, 1, (3, HQ, D))
+    out = host(cache.decode(0, dev(q), float(SCALE), seq_ids=torch.tensor(ids, dtype=torch.int32, device="cuda")))
+    for i, s in enumerate(ids):
+        assert_f32(out[i], oracle.decode_gqa(q[i][None], *data[s], SCALE)[0])
+    cache.close()
+
+
+def run_cfg3(sa, synth, bf16, steps=100, prompt=128, seed=40):
+    """One layer, B=1, 16q/8kv, D=128: prompt append, then `steps` decode steps.
+    Returns (GPU outputs [steps, 16, 128], the dense fp32 K/V the oracle needs,
+    the roped q of each step)."""
+    cache = sa.KVCache(1, HKV, D, 1, (prompt + steps + 63) // 64, (prompt + steps + 63) // 64,
+                       sa.SA_DTYPE_BF16 if bf16 else sa.SA_DTYPE_F32)
+    cos, sin = sa.rope_tables(prompt + steps, D, 1e6)
+    wq = dev(1 + synth.normal(seed, 1, D, 0.02))
+    wk = dev(1 + synth.normal(seed, 2, D, 0.02))
+    cache.reserve(0, prompt + steps)
+    kp = synth.normal(seed, 3, (1, prompt, HKV, D))
+    vp = synth.normal(seed, 4, (1, prompt, HKV, D))
+    cache.append(0, None, dev(kp), dev(vp), None, wk, 1e-6, rope=(cos, sin))
+    cache.commit(prompt, n_seqs=1)
+    outs, qs = [], []
+    q_all = synth.normal(seed, 5, (steps, 1, 1, HQ, D))
+    k_all = synth.normal(seed, 6, (steps, 1, 1, HKV, D))
+    v_all = synth.normal(seed, 7, (steps, 1, 1, HKV, D))
+    ws = torch.zeros(max(cache.decode_ws_bytes(1, HQ), 1), dtype=torch.uint8, device="cuda")
+    out = torch.empty(1, HQ, D, device="cuda")
+    for t in range(steps):
+        q_r = cache.append(0, dev(q_all[t]), dev(k_all[t]), dev(v_all[t]), wq, wk, 1e-6, rope=(cos, sin))
+        cache.decode(0, q_r.view(1, HQ, D), float(SCALE), n_pending=1, out=out, ws=ws)
+        cache.commit(1, n_seqs=1)
+        outs.append(host(out).copy())
+        qs.append(host(q_r).reshape(HQ, D))
+    gk, gv = cache.gather(0, 0, prompt + steps)
+    cache.close()
+    return (np.stack(outs)[:, 0], host(gk), host(gv), np.stack(qs),
+            (kp, vp, q_all, k_all, v_all, host(wq), host(wk)))
+
+
+def test_cfg3_decode_loop_fp32(sa, oracle, synth):
+    prompt, steps = 128, 100
+    outs, gk, gv, qs, raw = run_cfg3(sa, synth, False, steps, prompt)
+    kp, vp, q_all, k_all, v_all, wq, wk = raw
+    cos, sin = oracle.rope_tables(prompt + steps, D, 1e6)
+    # oracle K/V: normed + roped keys at their positions, raw values
+    k_tok = np.concatenate([kp[0], k_all[:, 0, 0]], 0)          # [N, HKV, D]
+    v_tok = np.concatenate([vp[0], v_all[:, 0, 0]], 0)
+    N = prompt + steps
+    kk = oracle.apply_rope(oracle.rms_norm_rows(k_tok, wk, 1e-6), np.repeat(np.arange(N), HKV), cos, sin)
+    assert_f32(gk.transpose(1, 0, 2), kk, 1e-5, 1e-6)
+    np.testing.assert_array_equal(gv.transpose(1, 0, 2), v_tok)
+    K = kk.transpose(1, 0, 2)[None]
+    V = v_tok.transpose(1, 0, 2)[None]
+    for t in range(steps):
+        pos = prompt + t
+        q_want = oracle.apply_rope(oracle.rms_norm_rows(q_all[t, 0, 0], wq, 1e-6), np.full(HQ, pos), cos, sin)
+        assert_f32(qs[t], q_want, 1e-5, 1e-6)
+        want = oracle.decode_gqa(q_want[None], K[:, :, : pos + 1], V[:, :, : pos + 1], SCALE)[0]
+        assert_f32(outs[t], want)
+
+
+def test_cfg3_decode_loop_bf16(sa, oracle, synth):
+    """bf16 KV: relative L2 <= 2e-2 per step, and a greedy readout of the
+    attention output (fixed random projection to 512 logits) picks the same
+    token as the oracle on the same bf16 K/V for 32 steps."""
+    prompt, steps = 128, 32
+    outs, gk, gv, qs, raw = run_cfg3(sa, synth, True, steps, prompt)
+    kp, vp, q_all, k_all, v_all, wq, wk = raw
+    cos, sin = oracle.rope_tables(prompt + steps, D, 1e6)
+    N = prompt + steps
+    k_tok = np.concatenate([kp[0], k_all[:, 0, 0]], 0)
+    v_tok = np.concatenate([vp[0], v_all[:, 0, 0]], 0)
+    kk = oracle.apply_rope(oracle.rms_norm_rows(k_tok, wk, 1e-6), np.repeat(np.arange(N), HKV), cos, sin)
+    K = kk.transpose(1, 0, 2)[None]
+    V = v_tok.transpose(1, 0, 2)[None]
+    # stored K is the fp32 normed+roped key rounded to bf16; the fp32 key may
+    # differ from the oracle's by an ulp, so the rounding may land one bf16 ulp
+    # away.  V is stored as given, so its rounding is exact.
+    assert np.all(np.abs(gk - synth.bf16_round(K)[0]) <= np.abs(K[0]) * 2.0 ** -7)
+    np.testing.assert_array_equal(gv, synth.bf16_round(V)[0])
+    Kb, Vb = gk[None], gv[None]       # the bf16 K/V the GPU attends over
+    head = synth.normal(41, 9, (HQ * D, 512), 0.02)
+    for t in range(steps):
+        pos = prompt + t
+        q_want = oracle.apply_rope(oracle.rms_norm_rows(q_all[t, 0, 0], wq, 1e-6), np.full(HQ, pos), cos, sin)
+        exact = oracle.decode_gqa(q_want[None], K[:, :, : pos + 1], V[:, :, : pos + 1], SCALE)[0]
+        same = oracle.decode_gqa(q_want[None], Kb[:, :, : pos + 1], Vb[:, :, : pos + 1], SCALE)[0]
+        assert rel_l2(outs[t], exact) <= 2e-2
+        assert_f32(outs[t], same, 1e-4, 1e-5)
+        assert int(np.argmax(outs[t].reshape(-1) @ head)) == int(np.argmax(same.reshape(-1) @ head))
+
+
+def test_reference_layer_golden(sa):
+    """The reference decoder layer (KVCache, prompt of 8 + 4 steps) reproduced by
+    append + prefill + paged decode: STANDARD exactly, STREAMING with its
+    scale-on-output applied afterwards."""
+    meta, g = gi.load("layer")
+    _, _, _, wq, wk = gi.layer_inputs()
+    Hq, Hkv, P = 4, 2, meta["prompt"]
+    eff = g["qkv_eff"]
+    N = eff.shape[0]
+    q = eff[:, : Hq * D].reshape(N, Hq, D)
+    k = eff[:, Hq * D:(Hq + Hkv) * D].reshape(N, Hkv, D)
+    v = eff[:, (Hq + Hkv) * D:].reshape(N, Hkv, D)
+    cache = sa.KVCache(1, Hkv, D, 1, 1, 1, sa.SA_DTYPE_F32)
+    cache.reserve(0, N)
+    cos, sin = sa.rope_tables(4096, D, 1e6)
+    dwq, dwk = dev(wq), dev(wk)
+    # prompt: append all P tokens, prefill attention on the normed+roped q/k
+    qr = cache.append(0, dev(q[:P][None]), dev(k[:P][None]), dev(v[:P][None]), dwq, dwk, 1e-6, rope=(cos, sin))
+    cache.commit(P, n_seqs=1)
+    gk, gv = cache.gather(0, 0, P)
+    pre = sa.prefill_causal(qr[0].transpose(0, 1).contiguous()[None], gk[None].contiguous(),
+                            gv[None].contiguous(), float(SCALE))
+    std = [host(pre)[0].transpose(1, 0, 2)]
+    strm = [std[0]]
+    for t in range(P, N):
+        qr = cache.append(0, dev(q[t][None, None]), dev(k[t][None, None]), dev(v[t][None, None]), dwq, dwk,
+                          1e-6, rope=(cos, sin))
+        qv = qr.view(1, Hq, D)
+        std.append(host(cache.decode(0, qv, float(SCALE), n_pending=1)))
+        strm.append(host(cache.decode(0, qv, 1.0, n_pending=1)) * SCALE)
+        cache.commit(1, n_seqs=1)
+    cache.close()
+    assert_f32(np.concatenate(std, 0), g["attn_avx0_str0"])
+    assert_f32(np.concatenate(strm, 0), g["attn_avx0_str1"])
+    # the AVX2 path puts eps outside the sqrt: inside both bars
+    assert_f32(np.concatenate(std, 0), g["attn_avx1_str0"])
+
+
+def test_cache_errors(sa):
+    cache = sa.KVCache(2, HKV, D, 2, 4, 6, sa.SA_DTYPE_F32)
+    with pytest.raises(sa.SaError) as e:
+        cache.reserve(0, 4 * 64 + 1)               # beyond the table row
+    assert e.value.status == sa.SA_EFULL
+    cache.reserve(0, 4 * 64)
+    with pytest.raises(sa.SaError) as e:
+        cache.reserve(1, 3 * 64)                   # only 2 pages left in the pool
+    assert e.value.status == sa.SA_EFULL
+    with pytest.raises(sa.SaError) as e:
+        cache.commit(1, seqs=[1])                  # nothing reserved for seq 1
+    assert e.value.status == sa.SA_EFULL
+    with pytest.raises(sa.SaError) as e:
+        cache.gather(5, 0, 1)                      # bad layer
+    assert e.value.status == sa.SA_ERANGE
+    with pytest.raises(sa.SaError) as e:
+        cache.gather(0, 0, 1)                      # longer than committed
+    assert e.value.status == sa.SA_ERANGE
+    with pytest.raises(sa.SaError):
+        cache.set_pages(1, [99])                   # page id out of range
+    cache.reset()
+    assert cache.length(0) == 0
+    cache.reserve(1, 6 * 64 - 64 * 2)              # pages are back after reset
+    cache.close()

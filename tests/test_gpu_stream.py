@@ -1,0 +1,142 @@
+"""GPU parity: single-query streaming attention and dense GQA decode.
+
+Bars (fp32): max-abs <= 1e-4 and relative L2 <= 1e-5 against the reference
+(golden vectors) or the oracle on the same inputs; the reference unit-test
+grid keeps its own 1e-5 max-abs bar.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import golden_inputs as gi
+
+pytestmark = pytest.mark.gpu
+
+SCALE128 = np.float32(1.0 / np.sqrt(128.0))
+MAX_ABS = 1e-4
+REL_L2 = 1e-5
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def assert_f32_parity(out, want):
+    assert np.abs(out - want).max() <= MAX_ABS, np.abs(out - want).max()
+    assert rel_l2(out, want) <= REL_L2, rel_l2(out, want)
+
+
+def test_cfg1_golden(sa):
+    """T=1024, d=128, N(0,1), blocks 64/128, scale 1/sqrt(128) vs the reference."""
+    _, g = gi.load("stream_cfg1")
+    Q, K, V = gi.cfg1_inputs()
+    dQ, dK, dV = dev(Q), dev(K), dev(V)
+    for blk in (64, 128):
+        assert_f32_parity(host(sa.stream_attn(dQ, dK, dV, blk, float(SCALE128))), g[f"serial_scaled_b{blk}"])
+        assert_f32_parity(host(sa.stream_attn(dQ, dK, dV, blk, 1.0)), g[f"serial_b{blk}"])
+    assert_f32_parity(host(sa.stream_attn(dQ, dK, dV, 64, 1.0)), g["naive"])
+
+
+def test_unit_grid_golden(sa):
+    """The reference unit test's grid (T x d, U(-1,1)), its 1e-5 max-abs bar."""
+    _, g = gi.load("stream_unit")
+    for T, d in gi.UNIT_GRID:
+        Q, K, V = gi.unit_inputs(T, d)
+        out = host(sa.stream_attn(dev(Q), dev(K), dev(V), 64))
+        assert np.abs(out - g[f"serial_T{T}_d{d}"]).max() <= 1e-5
+
+
+@pytest.mark.parametrize("T", [8192, 65536, 262144])
+def test_cfg2_long_context(sa, oracle, T):
+    """0.5 N(0,1) with 1% of K rows x8; blocks 64 and 128."""
+    print(f"cfg2 T={T}", flush=True)
+    Q, K, V = gi.cfg2_inputs(T)
+    dQ, dK, dV = dev(Q), dev(K), dev(V)
+    f64 = oracle.sdpa_f64(Q[None], K, V, 1.0)[0]
+    golden = gi.load("stream_cfg2")[1] if T <= 65536 else None
+    for blk in (64, 128):
+        out = host(sa.stream_attn(dQ, dK, dV, blk, 1.0))
+        want = golden[f"serial_T{T}_b{blk}"] if golden else oracle.streaming_serial(Q, K, V, blk)
+        assert_f32_parity(out, want)
+        # the GPU path is at least as close to the exact result as the reference
+        assert rel_l2(out, f64) <= max(2 * rel_l2(want, f64), 2e-6)
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_ragged_lengths(sa, oracle, synth, d):
+    for T in (1, 2, 15, 16, 17, 63, 64, 65, 255, 257, 1000, 4097):
+        Q, K, V = synth.stream_inputs(T, d, seed=100 + T)
+        out = host(sa.stream_attn(dev(Q), dev(K), dev(V), 64, 0.3))
+        assert_f32_parity(out, oracle.streaming_serial(Q * np.float32(0.3), K, V, 64))
+
+
+def test_zero_length(sa):
+    Q = dev(np.ones(128, np.float32))
+    K = torch.empty(0, 128, device="cuda")
+    out = sa.stream_attn(Q, K, K, 64)
+    assert np.all(host(out) == 0)
+
+
+def test_chunk_override_matches(sa, oracle, monkeypatch):
+    """Every split count gives the same answer (SA_DECODE_CHUNK forces it)."""
+    Q, K, V = gi.cfg2_inputs(8192)
+    want = oracle.streaming_serial(Q, K, V, 64)
+    dQ, dK, dV = dev(Q), dev(K), dev(V)
+    for chunk in ("64", "256", "1024", "8192"):
+        monkeypatch.setenv("SA_DECODE_CHUNK", chunk)
+        ws = torch.zeros(1 << 24, dtype=torch.uint8, device="cuda")
+        assert_f32_parity(host(sa.stream_attn(dQ, dK, dV, 64, 1.0, ws=ws)), want)
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(16, 8), (8, 8), (16, 4), (8, 1)])
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_dense_gqa_decode(sa, oracle, synth, Hq, Hkv, D):
+    B = 3
+    for T in (1, 100, 3000):
+        q = synth.normal(T, 1, (B, Hq, D))
+        k = synth.normal(T, 2, (B, Hkv, T, D))
+        v = synth.normal(T, 3, (B, Hkv, T, D))
+        sc = float(1.0 / np.sqrt(D))
+        out = host(sa.decode_dense(dev(q), dev(k), dev(v), sc))
+        assert_f32_parity(out, oracle.decode_gqa(q, k, v, np.float32(sc)))
+
+
+def test_decode_golden(sa):
+    """Reference STANDARD decode (repeat_kv + self_attention) on the golden inputs."""
+    _, g = gi.load("decode")
+    q, k, v = gi.decode_inputs()
+    out = host(sa.decode_dense(dev(q), dev(k), dev(v), float(1.0 / np.sqrt(128))))
+    assert_f32_parity(out, g["standard"])
+    # the reference's STREAMING decode: unscaled scores, output times scale
+    comp = host(sa.decode_dense(dev(q), dev(k), dev(v), 1.0)) * np.float32(1.0 / np.sqrt(128))
+    assert_f32_parity(comp, g["streaming"])
+
+
+def test_argument_errors(sa):
+    Q = dev(np.ones(128, np.float32))
+    K = dev(np.ones((10, 128), np.float32))
+    with pytest.raises(sa.SaError) as e:
+        sa.stream_attn(Q, K, K, 0)
+    assert e.value.status == sa.SA_EINVAL
+    Q100 = dev(np.ones(100, np.float32))
+    K100 = dev(np.ones((10, 100), np.float32))
+    with pytest.raises(sa.SaError):
+        sa.stream_attn(Q100, K100, K100, 64)
+    # workspace too small for a split run
+    Q, K, V = gi.cfg2_inputs(8192)
+    with pytest.raises(sa.SaError) as e:
+        sa.stream_attn(dev(Q), dev(K), dev(V), 64, ws=torch.empty(16, dtype=torch.uint8, device="cuda"))
+    assert e.value.status == sa.SA_ENOMEM
