@@ -158,6 +158,21 @@ sa_status sa_qknorm_rope_append(sa_kvcache* cache, int layer,
                                 float* q_out, sa_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * Per-row RMSNorm + rotate-half RoPE without a cache.
+ *
+ * Replaces apply_rotary_pos_emb and the QK-norm loops when no cache is
+ * involved (reference tensor_cpp/src/qwen3_ops.cpp:110-188, :697-753).
+ * x and y: [n_rows][D] fp32 (y may alias x); pos: device int32 [n_rows].
+ * norm_w: [D] or NULL (no norm); rope_cos / rope_sin: sa_rope_table_init
+ * tables with rope_max_pos rows, or NULL (no RoPE).  Rows whose position is
+ * outside the table are left unrotated.
+ * ------------------------------------------------------------------------ */
+sa_status sa_qk_norm_rope(const float* x, int n_rows, int D, const int32_t* pos,
+                          const float* norm_w, float eps, const float* rope_cos,
+                          const float* rope_sin, int rope_max_pos, float* y,
+                          sa_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * Paged GQA decode attention (split-KV online softmax + LSE merge).
  *
  * Replaces repeat_kv + ops::self_attention_streaming / self_attention on the
@@ -190,6 +205,15 @@ sa_status sa_kvcache_gather(const sa_kvcache* cache, int layer, int seq, int len
 sa_status sa_prefill_causal(const void* q, const void* k, const void* v, sa_dtype dtype,
                             int batch, int n_q_heads, int n_kv_heads, int L, int D,
                             float scale, float* out, sa_stream_t stream);
+
+/* The same with explicit element strides {batch, head, row} for q, for k and
+ * v (shared), and for out; rows of D elements must be contiguous and start
+ * 16-byte aligned.  Token-major [B][L][H][D] tensors use {L*H*D, D, H*D}. */
+sa_status sa_prefill_causal_strided(const void* q, const void* k, const void* v, sa_dtype dtype,
+                                    int batch, int n_q_heads, int n_kv_heads, int L, int D,
+                                    const int64_t q_strides[3], const int64_t kv_strides[3],
+                                    const int64_t out_strides[3], float scale, float* out,
+                                    sa_stream_t stream);
 
 #ifdef __cplusplus
 }

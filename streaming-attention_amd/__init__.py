@@ -74,10 +74,12 @@ SIGNATURES = {
     "sa_rope_table_init": (_I, [_P, _P, _I, _I, _F, _P]),
     "sa_qknorm_rope_append": (_I, [_P, _I, _P, _P, _P, _I, _I, _P, _I, _P, _P, _F, _P, _P, _I,
                                    _P, _P]),
+    "sa_qk_norm_rope": (_I, [_P, _I, _I, _P, _P, _F, _P, _P, _I, _P, _P]),
     "sa_paged_decode_ws_bytes": (_SZ, [_P, _I, _I]),
     "sa_paged_decode": (_I, [_P, _I, _P, _I, _P, _I, _I, _F, _P, _P, _SZ, _P]),
     "sa_kvcache_gather": (_I, [_P, _I, _I, _I, _P, _P, _P]),
     "sa_prefill_causal": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _P]),
+    "sa_prefill_causal_strided": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _F, _P, _P]),
 }
 
 _lib = None
@@ -89,7 +91,9 @@ def lib() -> C.CDLL:
     if _lib is None:
         if not LIB_PATH.exists():
             raise RuntimeError(f"{LIB_PATH} is missing: run `python streaming-attention_amd/build.py`")
-        handle = C.CDLL(str(LIB_PATH), mode=os.RTLD_NOW | os.RTLD_GLOBAL)
+        # RTLD_LOCAL: the library exports the reference API's C++ names, which
+        # must not interpose on another library loaded into the same process.
+        handle = C.CDLL(str(LIB_PATH), mode=os.RTLD_NOW | os.RTLD_LOCAL)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(handle, name)
             fn.restype = res

@@ -101,6 +101,79 @@ struct AppendArgs {
     float eps;
 };
 
+// One head row held by a wave as rotate-half pairs: lane j owns elements
+// i and i + D/2 for i = j, j + 64, ...
+template <int D>
+struct RowPairs {
+    static constexpr int H = D / 2;
+    static constexpr int NP = (H + kWave - 1) / kWave;
+    float lo[NP], hi[NP];
+
+    __device__ __forceinline__ void load(const float* x, int lane) {
+#pragma unroll
+        for (int c = 0; c < NP; ++c) {
+            const int i = lane + c * kWave;
+            lo[c] = (i < H) ? x[i] : 0.f;
+            hi[c] = (i < H) ? x[i + H] : 0.f;
+        }
+    }
+    // y = (x / sqrt(mean(x^2) + eps)) * w, eps inside the sqrt
+    // (reference tensor_cpp/src/qwen3_ops.cpp:716-717).
+    __device__ __forceinline__ void rms_norm(const float* w, float eps, int lane) {
+        float ss = 0.f;
+#pragma unroll
+        for (int c = 0; c < NP; ++c) ss = fmaf(lo[c], lo[c], fmaf(hi[c], hi[c], ss));
+        ss = group_reduce<OpSum, 1, kWave>(ss);
+        const float rms = sqrtf(ss / (float)D + eps);
+#pragma unroll
+        for (int c = 0; c < NP; ++c) {
+            const int i = lane + c * kWave;
+            if (i < H) {
+                lo[c] = (lo[c] / rms) * w[i];
+                hi[c] = (hi[c] / rms) * w[i + H];
+            }
+        }
+    }
+    // x' = x cos + rotate_half(x) sin with rotate_half(x) = [-x2, x1], cos/sin
+    // of row pos (reference tensor_cpp/src/qwen3_ops.cpp:30-64, 110-188).
+    __device__ __forceinline__ void rope(const float* cos_t, const float* sin_t, int pos, int lane) {
+#pragma unroll
+        for (int c = 0; c < NP; ++c) {
+            const int i = lane + c * kWave;
+            if (i < H) {
+                const float cs = cos_t[(size_t)pos * H + i];
+                const float sn = sin_t[(size_t)pos * H + i];
+                const float l2 = lo[c] * cs - hi[c] * sn;
+                const float h2 = hi[c] * cs + lo[c] * sn;
+                lo[c] = l2;
+                hi[c] = h2;
+            }
+        }
+    }
+    __device__ __forceinline__ void store(float* y, int lane) const {
+#pragma unroll
+        for (int c = 0; c < NP; ++c) {
+            const int i = lane + c * kWave;
+            if (i < H) { y[i] = lo[c]; y[i + H] = hi[c]; }
+        }
+    }
+};
+
+template <int D>
+__global__ void __launch_bounds__(256)
+qk_norm_rope_kernel(const float* x, int n_rows, const int32_t* pos, const float* w, float eps,
+                    const float* cos_t, const float* sin_t, int max_pos, float* y) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int row = blockIdx.x * 4 + threadIdx.x / kWave;
+    if (row >= n_rows) return;
+    RowPairs<D> r;
+    r.load(x + (size_t)row * D, lane);
+    if (w) r.rms_norm(w, eps, lane);
+    const int p = pos ? pos[row] : 0;
+    if (cos_t && p >= 0 && p < max_pos) r.rope(cos_t, sin_t, p, lane);
+    r.store(y + (size_t)row * D, lane);
+}
+
 template <int D, bool BF16>
 __global__ void __launch_bounds__(256)
 qknorm_rope_append_kernel(AppendArgs a) {
@@ -123,53 +196,16 @@ qknorm_rope_append_kernel(AppendArgs a) {
     const float* x = (is_q ? a.q : a.k) + src;
     const float* w = is_q ? a.wq : a.wk;
 
-    float lo[NP], hi[NP];
-    float ss = 0.f;
-#pragma unroll
-    for (int c = 0; c < NP; ++c) {
-        const int i = lane + c * kWave;
-        lo[c] = (i < H) ? x[i] : 0.f;
-        hi[c] = (i < H) ? x[i + H] : 0.f;
-        ss = fmaf(lo[c], lo[c], fmaf(hi[c], hi[c], ss));
-    }
-    if (w) {
-        // RMSNorm with eps inside the sqrt (reference tensor_cpp/src/qwen3_ops.cpp:716-717).
-        ss = group_reduce<OpSum, 1, kWave>(ss);
-        const float rms = sqrtf(ss / (float)D + a.eps);
-#pragma unroll
-        for (int c = 0; c < NP; ++c) {
-            const int i = lane + c * kWave;
-            if (i < H) {
-                lo[c] = (lo[c] / rms) * w[i];
-                hi[c] = (hi[c] / rms) * w[i + H];
-            }
-        }
-    }
-    if (a.cos_t && pos < a.rope_max_pos) {
-        // x' = x cos + rotate_half(x) sin, rotate_half(x) = [-x2, x1]
-        // (reference tensor_cpp/src/qwen3_ops.cpp:30-64, 110-188).
-#pragma unroll
-        for (int c = 0; c < NP; ++c) {
-            const int i = lane + c * kWave;
-            if (i < H) {
-                const float cs = a.cos_t[(size_t)pos * H + i];
-                const float sn = a.sin_t[(size_t)pos * H + i];
-                const float l2 = lo[c] * cs - hi[c] * sn;
-                const float h2 = hi[c] * cs + lo[c] * sn;
-                lo[c] = l2;
-                hi[c] = h2;
-            }
-        }
-    }
+    RowPairs<D> r;
+    r.load(x, lane);
+    if (w) r.rms_norm(w, a.eps, lane);
+    if (a.cos_t && pos < a.rope_max_pos) r.rope(a.cos_t, a.sin_t, pos, lane);
     if (is_q) {
-        float* y = a.q_out + src;
-#pragma unroll
-        for (int c = 0; c < NP; ++c) {
-            const int i = lane + c * kWave;
-            if (i < H) { y[i] = lo[c]; y[i + H] = hi[c]; }
-        }
+        r.store(a.q_out + src, lane);
         return;
     }
+    const float* lo = r.lo;
+    const float* hi = r.hi;
     // Append K (normed, rotated) and V (as given) at pos.
     if (pos >= a.max_pages * 64) return;
     const int page = a.table[(size_t)cache_row * a.max_pages + (pos >> 6)];
@@ -557,6 +593,38 @@ extern "C" sa_status sa_kvcache_gather(const sa_kvcache* c, int layer, int seq, 
         hipLaunchKernelGGL(gather_kernel<false>, grid, dim3(128), 0, st, k_pool_of(c, layer),
                            v_pool_of(c, layer), row, c->desc.num_kv_heads, c->desc.head_dim, len,
                            k_out, v_out);
+    SA_CHECK_LAUNCH();
+    return SA_OK;
+}
+
+extern "C" sa_status sa_qk_norm_rope(const float* x, int n_rows, int D, const int32_t* pos,
+                                     const float* norm_w, float eps, const float* rope_cos,
+                                     const float* rope_sin, int rope_max_pos, float* y,
+                                     sa_stream_t stream) {
+    clear_error();
+    if (!x || !y) return fail(SA_EINVAL, "null pointer");
+    if (n_rows < 0) return fail(SA_EINVAL, "n_rows must be >= 0");
+    if ((rope_cos == nullptr) != (rope_sin == nullptr)) return fail(SA_EINVAL, "cos and sin go together");
+    if (rope_cos && !pos) return fail(SA_EINVAL, "RoPE needs positions");
+    if (n_rows == 0) return SA_OK;
+    hipStream_t st = as_stream(stream);
+    const dim3 grid((n_rows + 3) / 4);
+    switch (D) {
+        case 64:
+            hipLaunchKernelGGL(qk_norm_rope_kernel<64>, grid, dim3(256), 0, st, x, n_rows, pos, norm_w, eps,
+                               rope_cos, rope_sin, rope_max_pos, y);
+            break;
+        case 128:
+            hipLaunchKernelGGL(qk_norm_rope_kernel<128>, grid, dim3(256), 0, st, x, n_rows, pos, norm_w, eps,
+                               rope_cos, rope_sin, rope_max_pos, y);
+            break;
+        case 256:
+            hipLaunchKernelGGL(qk_norm_rope_kernel<256>, grid, dim3(256), 0, st, x, n_rows, pos, norm_w, eps,
+                               rope_cos, rope_sin, rope_max_pos, y);
+            break;
+        default:
+            return fail(SA_EINVAL, "head_dim must be 64, 128 or 256");
+    }
     SA_CHECK_LAUNCH();
     return SA_OK;
 }

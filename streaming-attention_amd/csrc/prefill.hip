@@ -40,6 +40,18 @@ struct PrefillLds {
     static constexpr int BYTES = (kKTile * K_STRIDE + V_ROWS * V_STRIDE) * sizeof(elem);
 };
 
+struct PrefillArgs {
+    const void* q;
+    const void* k;
+    const void* v;
+    float* out;
+    long long qs[3];    // element strides {batch, head, row} of q
+    long long kvs[3];   // of k and v
+    long long os[3];    // of out
+    int Hq, Hkv, L;
+    float scale;
+};
+
 __device__ __forceinline__ float xsum16_32(float v) {
     v += swz_xor16(v);
     v += xor32(v);
@@ -53,9 +65,9 @@ __device__ __forceinline__ float xmax16_32(float v) {
 
 template <bool BF16, int D>
 __global__ void __launch_bounds__(kPThreads)
-prefill_causal_kernel(const void* __restrict__ qp, const void* __restrict__ kp,
-                      const void* __restrict__ vp, float* __restrict__ out, int Hq, int Hkv, int L,
-                      float scale) {
+prefill_causal_kernel(PrefillArgs pa) {
+    const int Hq = pa.Hq, Hkv = pa.Hkv, L = pa.L;
+    const float scale = pa.scale;
     using Lds = PrefillLds<BF16, D>;
     using elem = typename Lds::elem;
     constexpr int NDB = D / 16;            // 16-wide d blocks of the output
@@ -73,11 +85,10 @@ prefill_causal_kernel(const void* __restrict__ qp, const void* __restrict__ kp,
     const int g = lane >> 4;                   // lane group 0..3
     const int c16 = lane & 15;
 
-    const size_t q_off = (size_t)bh * L * D;
-    const size_t kv_off = ((size_t)b * Hkv + kvh) * (size_t)L * D;
-    const elem* Q = static_cast<const elem*>(qp) + q_off;
-    const elem* K = static_cast<const elem*>(kp) + kv_off;
-    const elem* V = static_cast<const elem*>(vp) + kv_off;
+    const elem* Q = static_cast<const elem*>(pa.q) + b * pa.qs[0] + h * pa.qs[1];
+    const elem* K = static_cast<const elem*>(pa.k) + b * pa.kvs[0] + kvh * pa.kvs[1];
+    const elem* V = static_cast<const elem*>(pa.v) + b * pa.kvs[0] + kvh * pa.kvs[1];
+    const long long q_row = pa.qs[2], kv_row = pa.kvs[2];
 
     const int q_wave0 = qt * kQTile + wave * 32;   // first query of this wave
 
@@ -92,11 +103,11 @@ prefill_causal_kernel(const void* __restrict__ qp, const void* __restrict__ kp,
 #pragma unroll
         for (int s = 0; s < QF; ++s) {
             if constexpr (BF16) {
-                uint4 raw = ok ? *reinterpret_cast<const uint4*>(Q + (size_t)qi * D + s * 32 + g * 8)
+                uint4 raw = ok ? *reinterpret_cast<const uint4*>(Q + qi * q_row + s * 32 + g * 8)
                                : make_uint4(0, 0, 0, 0);
                 qf[gq][s] = __builtin_bit_cast(bf16x8_t, raw);
             } else {
-                qf[gq][s] = ok ? Q[(size_t)qi * D + s * 4 + g] : 0.f;
+                qf[gq][s] = ok ? Q[qi * q_row + s * 4 + g] : 0.f;
             }
         }
     }
@@ -124,8 +135,8 @@ prefill_causal_kernel(const void* __restrict__ qp, const void* __restrict__ kp,
                 const int key = key0 + r;
                 uint4 kr = make_uint4(0, 0, 0, 0), vr = make_uint4(0, 0, 0, 0);
                 if (key < L) {
-                    kr = *reinterpret_cast<const uint4*>(K + (size_t)key * D + cchunk * EPV);
-                    vr = *reinterpret_cast<const uint4*>(V + (size_t)key * D + cchunk * EPV);
+                    kr = *reinterpret_cast<const uint4*>(K + key * kv_row + cchunk * EPV);
+                    vr = *reinterpret_cast<const uint4*>(V + key * kv_row + cchunk * EPV);
                 }
                 *reinterpret_cast<uint4*>(sK + r * Lds::K_STRIDE + cchunk * EPV) = kr;
                 if constexpr (BF16) {
@@ -234,7 +245,7 @@ prefill_causal_kernel(const void* __restrict__ qp, const void* __restrict__ kp,
         const int qi = q_wave0 + gq * 16 + c16;
         if (qi >= L) continue;
         const float inv = 1.0f / l_run[gq];
-        float* orow = out + ((size_t)bh * L + qi) * D;
+        float* orow = pa.out + b * pa.os[0] + h * pa.os[1] + qi * pa.os[2];
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
             float4 o4 = make_float4(acc[gq][db][0] * inv, acc[gq][db][1] * inv, acc[gq][db][2] * inv,
@@ -245,20 +256,50 @@ prefill_causal_kernel(const void* __restrict__ qp, const void* __restrict__ kp,
 }
 
 template <bool BF16, int D>
-sa_status launch_prefill(const void* q, const void* k, const void* v, int B, int Hq, int Hkv, int L,
-                         float scale, float* out, hipStream_t st) {
+sa_status launch_prefill(const PrefillArgs& pa, int B, hipStream_t st) {
     using Lds = PrefillLds<BF16, D>;
-    static bool lds_set = false;   // the fp32 D=128 tile needs more than 64 KiB
-    if (!lds_set) {
-        SA_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_causal_kernel<BF16, D>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, Lds::BYTES));
-        lds_set = true;
+    if constexpr (Lds::BYTES > 65536) {
+        // The fp32 D=128 tile needs more than 64 KiB of LDS: opt in per device.
+        static thread_local int opted_device = -1;
+        int dev = 0;
+        SA_HIP_TRY(hipGetDevice(&dev));
+        if (opted_device != dev) {
+            SA_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_causal_kernel<BF16, D>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, Lds::BYTES));
+            opted_device = dev;
+        }
     }
-    dim3 grid((L + kQTile - 1) / kQTile, B * Hq);
-    hipLaunchKernelGGL((prefill_causal_kernel<BF16, D>), grid, dim3(kPThreads), Lds::BYTES, st, q, k,
-                       v, out, Hq, Hkv, L, scale);
+    dim3 grid((pa.L + kQTile - 1) / kQTile, B * pa.Hq);
+    hipLaunchKernelGGL((prefill_causal_kernel<BF16, D>), grid, dim3(kPThreads), Lds::BYTES, st, pa);
     SA_CHECK_LAUNCH();
     return SA_OK;
+}
+
+sa_status prefill(const void* q, const void* k, const void* v, sa_dtype dtype, int batch, int n_q_heads,
+                  int n_kv_heads, int L, int D, const int64_t* qs, const int64_t* kvs, const int64_t* os,
+                  float scale, float* out, hipStream_t st) {
+    if (!q || !k || !v || !out || !qs || !kvs || !os) return fail(SA_EINVAL, "null pointer");
+    if (batch <= 0 || n_q_heads <= 0 || n_kv_heads <= 0 || n_q_heads % n_kv_heads)
+        return fail(SA_EINVAL, "bad head counts");
+    if (dtype != SA_DTYPE_F32 && dtype != SA_DTYPE_BF16) return fail(SA_EINVAL, "dtype must be F32 or BF16");
+    if (D != 64 && D != 128) return fail(SA_EINVAL, "prefill head_dim must be 64 or 128");
+    if (L <= 0) return SA_OK;
+    const int elem = dtype == SA_DTYPE_BF16 ? 2 : 4;
+    const int64_t align_in = 16 / elem, align_out = 4;
+    for (int i = 0; i < 3; ++i) {
+        if (qs[i] % align_in || kvs[i] % align_in || os[i] % align_out || qs[i] < 0 || kvs[i] < 0 || os[i] < 0)
+            return fail(SA_EINVAL, "strides must keep every row 16-byte aligned");
+    }
+    if (qs[2] < D || kvs[2] < D || os[2] < D) return fail(SA_EINVAL, "row stride shorter than head_dim");
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+        return fail(SA_EINVAL, "q, k, v and out must be 16-byte aligned");
+    PrefillArgs pa{};
+    pa.q = q; pa.k = k; pa.v = v; pa.out = out;
+    for (int i = 0; i < 3; ++i) { pa.qs[i] = qs[i]; pa.kvs[i] = kvs[i]; pa.os[i] = os[i]; }
+    pa.Hq = n_q_heads; pa.Hkv = n_kv_heads; pa.L = L; pa.scale = scale;
+    if (dtype == SA_DTYPE_BF16)
+        return D == 64 ? launch_prefill<true, 64>(pa, batch, st) : launch_prefill<true, 128>(pa, batch, st);
+    return D == 64 ? launch_prefill<false, 64>(pa, batch, st) : launch_prefill<false, 128>(pa, batch, st);
 }
 
 }  // namespace
@@ -267,23 +308,20 @@ sa_status launch_prefill(const void* q, const void* k, const void* v, int B, int
 extern "C" sa_status sa_prefill_causal(const void* q, const void* k, const void* v, sa_dtype dtype,
                                        int batch, int n_q_heads, int n_kv_heads, int L, int D,
                                        float scale, float* out, sa_stream_t stream) {
-    using namespace sa;
-    clear_error();
-    if (!q || !k || !v || !out) return fail(SA_EINVAL, "null pointer");
-    if (batch <= 0 || n_q_heads <= 0 || n_kv_heads <= 0 || n_q_heads % n_kv_heads)
-        return fail(SA_EINVAL, "bad head counts");
-    if (L <= 0) return SA_OK;
-    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
-        return fail(SA_EINVAL, "q, k, v and out must be 16-byte aligned");
-    hipStream_t st = as_stream(stream);
-    if (dtype == SA_DTYPE_BF16) {
-        if (D == 64) return launch_prefill<true, 64>(q, k, v, batch, n_q_heads, n_kv_heads, L, scale, out, st);
-        if (D == 128) return launch_prefill<true, 128>(q, k, v, batch, n_q_heads, n_kv_heads, L, scale, out, st);
-    } else if (dtype == SA_DTYPE_F32) {
-        if (D == 64) return launch_prefill<false, 64>(q, k, v, batch, n_q_heads, n_kv_heads, L, scale, out, st);
-        if (D == 128) return launch_prefill<false, 128>(q, k, v, batch, n_q_heads, n_kv_heads, L, scale, out, st);
-    } else {
-        return fail(SA_EINVAL, "dtype must be F32 or BF16");
-    }
-    return fail(SA_EINVAL, "prefill head_dim must be 64 or 128");
+    sa::clear_error();
+    const int64_t Ld = (int64_t)L * D;
+    const int64_t qs[3] = {n_q_heads * Ld, Ld, D};
+    const int64_t kvs[3] = {n_kv_heads * Ld, Ld, D};
+    return sa::prefill(q, k, v, dtype, batch, n_q_heads, n_kv_heads, L, D, qs, kvs, qs, scale, out,
+                       sa::as_stream(stream));
+}
+
+extern "C" sa_status sa_prefill_causal_strided(const void* q, const void* k, const void* v, sa_dtype dtype,
+                                               int batch, int n_q_heads, int n_kv_heads, int L, int D,
+                                               const int64_t q_strides[3], const int64_t kv_strides[3],
+                                               const int64_t out_strides[3], float scale, float* out,
+                                               sa_stream_t stream) {
+    sa::clear_error();
+    return sa::prefill(q, k, v, dtype, batch, n_q_heads, n_kv_heads, L, D, q_strides, kv_strides, out_strides,
+                       scale, out, sa::as_stream(stream));
 }

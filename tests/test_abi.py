@@ -48,6 +48,17 @@ def test_last_error_starts_empty():
     assert lib.sa_last_error() == b""
 
 
+def test_library_does_not_interpose_on_the_reference(ref):
+    """libsa_amd exports the reference API's names (streaming_attention_serial,
+    ...); loading it first must not redirect the reference build's own calls."""
+    import numpy as np
+    load_pkg().lib()
+    Q = np.ones(64, np.float32)
+    K = np.ones((3, 64), np.float32)
+    V = np.arange(192, dtype=np.float32).reshape(3, 64)
+    np.testing.assert_allclose(ref.streaming_serial(Q, K, V, 64), V.mean(0), rtol=1e-6)
+
+
 def test_no_gpu_compute_without_device():
     """Argument validation runs on the host: a bad call fails before any launch."""
     sa = load_pkg()
