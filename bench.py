@@ -43,6 +43,21 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+PROFILE_SUMMARY = ROOT / "profiles" / "split_kv_decode_T262144_d128_f32.md"
+
+
+def profiled_traffic(T: int):
+    """HBM bytes per launch of the headline kernel from the committed
+    rocprofv3 counter summary (FETCH_SIZE and WRITE_SIZE, calibrated against a
+    plain copy), when it covers this workload; otherwise None."""
+    if T != 262144 or not PROFILE_SUMMARY.exists():
+        return None
+    for line in PROFILE_SUMMARY.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch"):
+            return int(line.split("=")[1])
+    return None
+
+
 def load_pkg():
     from util import load_pkg as lp, load_synth
     return lp(), load_synth()
@@ -191,6 +206,20 @@ def bench_prefill(torch, sa, synth, L: int, bf16: bool, steps: int = 5):
             "mfma_frac": round(tf / peak, 4)}
 
 
+def copy_calibration(torch, nbytes: int = 1 << 30, steps: int = 5):
+    """A plain device-to-device copy of nbytes (reads nbytes, writes nbytes):
+    the reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE, and the
+    bandwidth HBM sustains for a streaming read+write on this device."""
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    per, _ = time_launches(torch, lambda i: dst.copy_(src), steps, 2)
+    ms = statistics.mean(per)
+    del src, dst
+    torch.cuda.empty_cache()
+    return {"bytes_read": nbytes, "bytes_written": nbytes, "ms": round(ms, 4),
+            "gbs_read_plus_write": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -199,6 +228,8 @@ def main() -> int:
     ap.add_argument("--only", choices=["headline", "all"], default="all")
     ap.add_argument("--T", type=int, default=262144)
     ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--profile-copy", action="store_true",
+                    help="also run a 1 GiB device copy (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: every configuration of this path runs on a single "
@@ -213,6 +244,10 @@ def main() -> int:
     sa, synth = load_pkg()
     sa.lib()
 
+    calib = None
+    if args.profile_copy:
+        log("[bench] 1 GiB device copy (counter calibration)")
+        calib = copy_calibration(torch)
     head, (Q, K, V) = bench_stream(torch, sa, synth, args.T, args.steps, args.warmup)
     log(f"[bench] headline: {head['gbs']:.1f} GB/s kernel, {head['wall_gbs']:.1f} GB/s wall, "
         f"err {head['max_abs_err']:.2e}")
@@ -254,14 +289,16 @@ def main() -> int:
         "config": {"workload": f"single-query streaming attention, T={args.T}, d=128, block 128, fp32",
                    "T": args.T, "head_dim": 128, "block": 128, "replicas": head["replicas"]},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "split_kv_decode_kernel<128,1,f32,dense>",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(args.T),
+                     "kernel": "decode call = split_kv_decode_kernel<128,1,f32,dense> + lse_merge_kernel",
                      "kernel_ms": round(head["kernel_ms"], 5),
                      "algorithmic_bytes_per_launch": head["bytes_per_launch"]},
         "cpu_baseline": cpu,
         "parity": {"max_abs_err": head["max_abs_err"], "rel_l2_err": head["rel_l2_err"]},
         "extra": extra,
     }
+    if calib:
+        line["extra"]["copy_calibration"] = calib
     print(json.dumps(line), flush=True)
     return 0
 
