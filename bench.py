@@ -189,6 +189,52 @@ def bench_cfg3(torch, sa, synth, steps_timed: int = 3):
     return res
 
 
+def batch_lengths(synth, B: int = 64, lo: int = 512, hi: int = 32768, seed: int = 70):
+    """Per-sequence context lengths ~ U[lo, hi] (seeded)."""
+    u = synth.uniform(seed, 1, B)
+    return [int(lo + min(int(x * (hi - lo + 1)), hi - lo)) for x in u]
+
+
+def bench_paged_batch(torch, sa, synth, steps: int = 10, bf16: bool = True):
+    """Batched paged GQA decode, one layer: B=64 sequences, lengths U[512, 32768],
+    16 q / 8 KV heads, D=128, 64-token pages assigned from a seeded shuffle of
+    the pool, KV synthesised as N(0,1) (no prefill run)."""
+    HQ, HKV, D, B = 16, 8, 128, 64
+    lens = batch_lengths(synth, B)
+    pages_per = [(L + 1 + 63) // 64 for L in lens]            # room for the step's new token
+    n_pages = sum(pages_per)
+    max_pages = max(pages_per)
+    cache = sa.KVCache(1, HKV, D, B, max_pages, n_pages, sa.SA_DTYPE_BF16 if bf16 else sa.SA_DTYPE_F32)
+    perm = synth.permutation(70, 2, n_pages)
+    off = 0
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(70)
+    for s, L in enumerate(lens):
+        cache.set_pages(s, perm[off:off + pages_per[s]])
+        off += pages_per[s]
+        ids = torch.tensor([s], dtype=torch.int32, device="cuda")
+        for t0 in range(0, L, 4096):
+            n = min(4096, L - t0)
+            k = torch.randn(1, n, HKV, D, device="cuda", generator=gen)
+            v = torch.randn(1, n, HKV, D, device="cuda", generator=gen)
+            cache.append(0, None, k, v, seq_ids=ids)
+            cache.commit(n, seqs=[s])
+    torch.cuda.synchronize()
+    q = torch.randn(B, HQ, D, device="cuda", generator=gen)
+    out = torch.empty_like(q)
+    ws = torch.zeros(max(cache.decode_ws_bytes(B, HQ), 1), dtype=torch.uint8, device="cuda")
+    sc = float(1 / np.sqrt(D))
+    per, _ = time_launches(torch, lambda i: cache.decode(0, q, sc, out=out, ws=ws), steps, 3)
+    ms = statistics.mean(per)
+    elem = 2 if bf16 else 4
+    kv_bytes = sum(lens) * HKV * D * 2 * elem
+    total = kv_bytes + 2 * B * HQ * D * 4
+    cache.close()
+    return {"batch": B, "sum_len": sum(lens), "min_len": min(lens), "max_len": max(lens),
+            "kv": "bf16" if bf16 else "f32", "ms": round(ms, 4), "bytes_per_call": total,
+            "gbs": round(total / (ms * 1e-3) / 1e9, 1), "hbm_frac": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def bench_prefill(torch, sa, synth, L: int, bf16: bool, steps: int = 5):
     HQ, HKV, D = 16, 8, 128
     dt = torch.bfloat16 if bf16 else torch.float32
@@ -265,6 +311,8 @@ def main() -> int:
                                           "rel_l2_err": c2["rel_l2_err"]}
         log("[bench] one-layer Qwen3 decode loop (config 3)")
         extra["qwen3_layer_decode_loop"] = bench_cfg3(torch, sa, synth)
+        log("[bench] batched paged GQA decode, 64 sequences, bf16 KV (config 5 attention)")
+        extra["paged_decode_b64_bf16"] = bench_paged_batch(torch, sa, synth)
         for L in (1024, 8192):
             for bf in (True, False):
                 log(f"[bench] causal prefill L={L} {'bf16' if bf else 'fp32'} (config 4)")

@@ -277,6 +277,8 @@ extern "C" sa_status sa_kvcache_create(const sa_kv_desc* d, sa_kvcache** out) {
     if (d->num_layers <= 0 || d->num_kv_heads <= 0 || d->max_seqs <= 0 ||
         d->max_pages_per_seq <= 0 || d->num_pages <= 0)
         return fail(SA_EINVAL, "cache dimensions must be positive");
+    if (d->max_pages_per_seq > (1 << 18))
+        return fail(SA_EINVAL, "max_pages_per_seq must be at most 262144 (16M tokens)");
     if (d->head_dim != 64 && d->head_dim != 128 && d->head_dim != 256)
         return fail(SA_EINVAL, "head_dim must be 64, 128 or 256");
     if (d->kv_dtype != SA_DTYPE_F32 && d->kv_dtype != SA_DTYPE_BF16)
@@ -568,7 +570,8 @@ extern "C" sa_status sa_paged_decode(const sa_kvcache* c, int layer, const float
     pv.k_pool = k_pool_of(c, layer); pv.v_pool = v_pool_of(c, layer);
     pv.block_table = c->d_table; pv.seq_lens = c->d_lens;
     pv.n_kv = c->desc.num_kv_heads; pv.d = c->desc.head_dim;
-    pv.max_pages = c->desc.max_pages_per_seq; pv.bf16 = c->desc.kv_dtype == SA_DTYPE_BF16;
+    pv.max_pages = c->desc.max_pages_per_seq; pv.num_pages = c->desc.num_pages;
+    pv.bf16 = c->desc.kv_dtype == SA_DTYPE_BF16;
     return decode_paged(pv, q, n_seq, seq_ids, n_q_heads, n_pending, max_len, total, scale, out, ws,
                         ws_bytes, as_stream(stream));
 }

@@ -93,7 +93,7 @@ struct PagedView {
     const void* v_pool;
     const int32_t* block_table;
     const int32_t* seq_lens;
-    int n_kv, d, max_pages;
+    int n_kv, d, max_pages, num_pages;
     bool bf16;
 };
 
