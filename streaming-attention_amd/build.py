@@ -40,6 +40,13 @@ DEVICE = [
 ]
 
 
+# Per-file device flags.  The prefill kernels keep MFMA accumulators in arch
+# VGPRs (their softmax rescales them with VALU ops) and park Q in AGPRs.
+EXTRA = {
+    "prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def sources() -> list[Path]:
     srcs = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
     srcs += sorted((CSRC / "compat").glob("*.cpp"))
@@ -51,7 +58,7 @@ def compile_one(src: Path) -> Path:
     obj = BUILD / (str(rel).replace("/", "__") + ".o")
     obj.parent.mkdir(parents=True, exist_ok=True)
     if src.suffix == ".hip":
-        cmd = [HIPCC, "-x", "hip", *COMMON, *DEVICE, "-c", str(src), "-o", str(obj)]
+        cmd = [HIPCC, "-x", "hip", *COMMON, *DEVICE, *EXTRA.get(src.name, []), "-c", str(src), "-o", str(obj)]
     else:
         cmd = [HIPCC, *COMMON, "-D__HIP_PLATFORM_AMD__", "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -6,47 +6,40 @@
 // 0..i, scores = (q.k) * scale.  GQA: query head h reads KV head h / (Hq/Hkv)
 // (the repeat_kv map of tensor_cpp/src/qwen3_ops.cpp:194-234), no copy.
 //
-// Tiling: a workgroup of 4 waves owns 128 queries of one head (32 per wave,
-// as two 16-query groups) and walks 64-key tiles staged in LDS.  Scores are
-// computed transposed, S^T = K Q^T, with 16x16 MFMA blocks: lane l then holds
-// query l%16 and 4 keys per block, so row max / row sum are in-lane plus two
-// cross-lane steps, and P^T is already in the B-operand layout of the
-// O^T += V^T P^T product.  bf16 inputs use v_mfma_f32_16x16x32_bf16 (P is
-// rounded to bf16, accumulation fp32); fp32 inputs use v_mfma_f32_16x16x4f32.
-// Tiles entirely above the diagonal are never loaded; only tiles that cross
-// the diagonal apply the element mask.
+// Both kernels compute scores transposed, S^T = K Q^T, so a lane owns one
+// query column and the row max / row sum need almost no cross-lane work, and
+// P^T comes out of the score MFMA already in the B-operand layout of the
+// O^T += V^T P^T product.  Softmax runs in the log2 domain, p = 2^(s*c - m)
+// with c = scale * log2(e).  Tiles entirely above the diagonal are never
+// computed; only the tile that crosses a wave's diagonal applies the mask.
+//
+// bf16 inputs (v_mfma_f32_32x32x16_bf16, fp32 accumulation): a wave owns 64
+// queries as two 32-query blocks, a workgroup of 4 waves 256 queries.  The
+// running max is raised lazily: a wave rescales its accumulators only when
+// some score exceeds the current max by more than 2^8, so p stays below 256
+// and the common tile does no rescale at all.  P is rounded to bf16 for the
+// PV product; the row sums use the fp32 p.
+//
+// fp32 inputs (v_mfma_f32_16x16x4f32): a wave owns 32 queries as two
+// 16-query blocks, a workgroup 128 queries, eager rescale.
+#include <type_traits>
+
 #include "sa_internal.h"
 
 namespace sa {
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+// Staging registers use the native vector type: HIP's uint4 is a struct whose
+// copies lower to memcpy and end up in scratch memory.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kQTile = 128;   // queries per workgroup
-constexpr int kKTile = 64;    // keys per LDS tile
-constexpr int kPThreads = 256;
+constexpr int kKTile = 64;    // keys per LDS tile (both kernels)
 constexpr float kLog2eP = 1.4426950408889634f;
-
-template <bool BF16, int D>
-struct PrefillLds {
-    // Two stages.  K row-major [64][D + pad]; V fp32 row-major [64][D + pad],
-    // bf16 transposed [D][64 + pad] so a lane reads 4 consecutive keys of one d.
-    static constexpr int KPAD = BF16 ? 8 : 4;
-    static constexpr int K_STRIDE = D + KPAD;
-    static constexpr int V_STRIDE = BF16 ? (kKTile + 8) : (D + 4);
-    static constexpr int V_ROWS = BF16 ? D : kKTile;
-    using elem = typename std::conditional<BF16, uint16_t, float>::type;
-    static constexpr int STAGE = kKTile * K_STRIDE + V_ROWS * V_STRIDE;   // elements
-    static constexpr int BYTES = 2 * STAGE * (int)sizeof(elem);
-    // 16-byte global loads per thread per tile, for K and for V.
-    static constexpr int EPV = 16 / (int)sizeof(elem);
-    static constexpr int CPR = D / EPV;                 // 16 B chunks per row
-    static constexpr int NK = kKTile * CPR / 256;       // K loads per thread
-    static constexpr int NV = NK;                       // V loads per thread
-};
 
 struct PrefillArgs {
     const void* q;
@@ -57,8 +50,358 @@ struct PrefillArgs {
     long long kvs[3];   // of k and v
     long long os[3];    // of out
     int Hq, Hkv, L;
-    float scale;
+    int n_qt;           // query tiles per head
+    int xcd_groups;     // KV groups per XCD when the grid maps groups to XCDs, else 0
+    float sl2;          // |scale| * log2(e)
+    uint32_t q_sign;    // 0x80008000 to negate bf16 q pairs (negative scale), else 0
+    float scale;        // signed scale (fp32 kernel)
 };
+
+// Work mapping shared by both kernels.  A KV group is one (batch, kv head);
+// its G = Hq/Hkv query heads read the same K/V.  When the number of groups is
+// a multiple of 8, hardware workgroup i (dispatched to XCD i % 8) takes work
+// slot i / 8 of the groups owned by that XCD, so each XCD's L2 holds the K/V
+// of its own groups only.  Inside an XCD (or the whole grid otherwise) slots
+// run heaviest query tile first, which balances the causal triangle.
+struct Work { int b, h, kvh, qt; };
+__device__ __forceinline__ Work map_work(const PrefillArgs& pa, int i) {
+    const int G = pa.Hq / pa.Hkv;
+    int x = 0, j = i, span = gridDim.x / (G * pa.n_qt);   // groups in this slot range
+    if (pa.xcd_groups) { x = i & 7; j = i >> 3; span = pa.xcd_groups; }
+    const int per_qt = span * G;
+    Work w;
+    w.qt = pa.n_qt - 1 - j / per_qt;
+    const int rem = j % per_qt;
+    const int group = x * span + rem / G;
+    w.b = group / pa.Hkv;
+    w.kvh = group % pa.Hkv;
+    w.h = w.kvh * G + rem % G;
+    return w;
+}
+
+// ===========================================================================
+// bf16 kernel
+// ===========================================================================
+constexpr int kBWaves = 4;
+constexpr int kBQWave = 64;                      // queries per wave
+constexpr int kBQTile = kBWaves * kBQWave;       // queries per workgroup
+constexpr int kBThreads = kBWaves * 64;
+constexpr float kLazyRescale = 8.f;              // log2 headroom before a rescale
+
+template <int D>
+struct BfLds {
+    static constexpr int K_STRIDE = D + 8;           // K row-major [64][D + 8]
+    static constexpr int V_STRIDE = kKTile + 8;      // V transposed [D][64 + 8]
+    static constexpr int K_ELEMS = kKTile * K_STRIDE;
+    static constexpr int STAGE = K_ELEMS + D * V_STRIDE;   // bf16 elements per stage
+    static constexpr int BYTES = 2 * STAGE * 2;            // two stages
+    static constexpr int CPR = D / 8;                // 16-byte chunks per row
+    static constexpr int NK = kKTile * CPR / kBThreads;    // K chunks per thread
+    static constexpr int NVI = 32 * CPR / kBThreads;       // V (row pair, chunk) items per thread
+    static_assert(NK >= 1 && NVI >= 1, "tile too small for the workgroup");
+};
+
+// The K rows a lane feeds to the score MFMA are permuted within each 32-key
+// block (bits 2 and 3 of the row swapped).  With the 32x32 output layout
+// (lane l: column l%32, rows 8*(j/4) + 4*(l/32) + j%4 for element j) this
+// makes element j of lane l the score of key 16*(j/8) + 8*(l/32) + j%8: each
+// lane's 8-element groups are 8 consecutive keys, exactly what the B operand
+// of the 32x32x16 PV step needs, and what one 16-byte read of V^T supplies.
+__device__ __forceinline__ int swap_bits23(int m) { return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1); }
+
+template <int D>
+struct BfStage {
+    u32x4_t k[BfLds<D>::NK];
+    u32x4_t v[2 * BfLds<D>::NVI];
+};
+
+// Per-thread element offsets of the tile loads, relative to the tile's first
+// row.  K: chunk idx = tid + i*256 -> row idx / CPR.  V: item = tid + i*256
+// -> row pair item % 32 (rows 2rp, 2rp + 1), chunk item / 32.
+template <int D>
+struct BfLoadMap {
+    int k_row[BfLds<D>::NK], k_col[BfLds<D>::NK];
+    int v_row[BfLds<D>::NVI], v_col[BfLds<D>::NVI];
+    __device__ __forceinline__ BfLoadMap() {
+        using Lds = BfLds<D>;
+#pragma unroll
+        for (int i = 0; i < Lds::NK; ++i) {
+            const int idx = threadIdx.x + i * kBThreads;
+            k_row[i] = idx / Lds::CPR;
+            k_col[i] = (idx % Lds::CPR) * 8;
+        }
+#pragma unroll
+        for (int i = 0; i < Lds::NVI; ++i) {
+            const int item = threadIdx.x + i * kBThreads;
+            v_row[i] = 2 * (item % 32);
+            v_col[i] = (item / 32) * 8;
+        }
+    }
+};
+
+// Global -> registers.  Rows past the end of the sequence are clamped to the
+// last row: they only feed keys that the causal mask removes.
+template <int D>
+__device__ __forceinline__ void bf_load(BfStage<D>& st, const BfLoadMap<D>& mp, const uint16_t* K,
+                                        const uint16_t* V, int kv_row, int key0, int L) {
+    using Lds = BfLds<D>;
+    const uint16_t* Kt = K + (long long)key0 * kv_row;
+    const uint16_t* Vt = V + (long long)key0 * kv_row;
+    const int rmax = L - 1 - key0;
+#pragma unroll
+    for (int i = 0; i < Lds::NK; ++i)
+        st.k[i] = *reinterpret_cast<const u32x4_t*>(Kt + min(mp.k_row[i], rmax) * kv_row + mp.k_col[i]);
+#pragma unroll
+    for (int i = 0; i < Lds::NVI; ++i) {
+        st.v[2 * i] = *reinterpret_cast<const u32x4_t*>(Vt + min(mp.v_row[i], rmax) * kv_row + mp.v_col[i]);
+        st.v[2 * i + 1] = *reinterpret_cast<const u32x4_t*>(Vt + min(mp.v_row[i] + 1, rmax) * kv_row + mp.v_col[i]);
+    }
+}
+
+
+// Registers -> LDS stage.  K row-major; V transposed with one 4-byte store
+// per (d, key pair): lanes of a wave cover 32 consecutive key pairs of one d,
+// so each store instruction touches 32 distinct banks per half-wave.
+template <int D>
+__device__ __forceinline__ void bf_store(const BfStage<D>& st, const BfLoadMap<D>& mp, uint16_t* sK, uint16_t* sV) {
+    using Lds = BfLds<D>;
+#pragma unroll
+    for (int i = 0; i < Lds::NK; ++i)
+        *reinterpret_cast<u32x4_t*>(sK + mp.k_row[i] * Lds::K_STRIDE + mp.k_col[i]) = st.k[i];
+#pragma unroll
+    for (int i = 0; i < Lds::NVI; ++i) {
+        const u32x4_t lo = st.v[2 * i], hi = st.v[2 * i + 1];
+        uint16_t* col = sV + mp.v_col[i] * Lds::V_STRIDE + mp.v_row[i];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            // elements 2w, 2w+1 of the chunk: key pair (lo, hi) for each
+            *reinterpret_cast<uint32_t*>(col + (2 * w) * Lds::V_STRIDE) = __builtin_amdgcn_perm(hi[w], lo[w], 0x05040100u);
+            *reinterpret_cast<uint32_t*>(col + (2 * w + 1) * Lds::V_STRIDE) =
+                __builtin_amdgcn_perm(hi[w], lo[w], 0x07060302u);
+        }
+    }
+}
+
+__device__ __forceinline__ bf16x8_t lds_b128(const uint16_t* p) { return *reinterpret_cast<const bf16x8_t*>(p); }
+
+template <int D>
+__global__ void __launch_bounds__(kBThreads)
+prefill_bf16_kernel(PrefillArgs pa) {
+    using Lds = BfLds<D>;
+    constexpr int NKS = D / 16;     // k-steps of the score product
+    constexpr int NDB = D / 32;     // 32-row d blocks of O^T
+    extern __shared__ __align__(16) unsigned char smem[];
+    uint16_t* stage_base = reinterpret_cast<uint16_t*>(smem);
+
+    const int L = pa.L;
+    const Work wk = map_work(pa, blockIdx.x);
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int n = lane & 31;        // query column inside a 32-query block
+    const int hh = lane >> 5;       // lane half
+    const float sl2 = pa.sl2;
+
+    const uint16_t* Q = static_cast<const uint16_t*>(pa.q) + wk.b * pa.qs[0] + wk.h * pa.qs[1];
+    const uint16_t* K = static_cast<const uint16_t*>(pa.k) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
+    const uint16_t* V = static_cast<const uint16_t*>(pa.v) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
+    const int kv_row = static_cast<int>(pa.kvs[2]);
+
+    const int q_wave0 = wk.qt * kBQTile + wave * kBQWave;
+    const int n_kt = (min(L, (wk.qt + 1) * kBQTile) - 1) / kKTile + 1;
+    // Tiles this wave computes: keys up to its last query.  The last one is
+    // the diagonal tile (q_wave0 is a multiple of the key tile).
+    const int wave_kt = q_wave0 < L ? q_wave0 / kKTile + 1 : 0;
+
+    const BfLoadMap<D> mp;
+    BfStage<D> next;
+    bf_load<D>(next, mp, K, V, kv_row, 0, L);
+
+    // Q^T fragments (B operand): lane holds q[n][16 ks + 8 hh .. + 7].
+    bf16x8_t qf[2][NKS];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        const int qi = min(q_wave0 + qb * 32 + n, L - 1);
+        const uint16_t* qrow = Q + qi * pa.qs[2] + 8 * hh;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+            const u32x4_t raw = *reinterpret_cast<const u32x4_t*>(qrow + ks * 16) ^ pa.q_sign;
+            qf[qb][ks] = __builtin_bit_cast(bf16x8_t, raw);
+            // MFMA sources may be AGPRs: Q waits there, leaving VGPRs to the softmax.
+            asm("" : "+a"(qf[qb][ks]));
+        }
+    }
+
+    f32x16_t acc[2][NDB];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) acc[qb][db] = f32x16_t{};
+    float ms[2] = {-INFINITY, -INFINITY};   // running max (log2 domain), equal in both lane halves
+    float lp[2] = {0.f, 0.f};               // row-sum part over this lane half's keys
+
+    // Per-lane LDS read offsets (elements) inside a stage.
+    const int k_off = swap_bits23(n) * Lds::K_STRIDE + 8 * hh;
+    const int v_off = Lds::K_ELEMS + n * Lds::V_STRIDE + 8 * hh;
+
+    bf_store<D>(next, mp, stage_base, stage_base + Lds::K_ELEMS);
+    __syncthreads();
+
+    for (int kt = 0; kt < n_kt; ++kt) {
+        const uint16_t* sK = stage_base + (kt & 1) * Lds::STAGE;
+        const bool more = kt + 1 < n_kt;
+        if (more) bf_load<D>(next, mp, K, V, kv_row, (kt + 1) * kKTile, L);
+
+        // One tile, as two 32-key halves kb: scores, softmax, then the PV
+        // product of that half.  DIAG instantiates the diagonal tile's mask.
+        auto tile = [&](auto diag_tag) {
+            constexpr bool DIAG = decltype(diag_tag)::value;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                // ---- S^T = K Q^T for keys 32 kb .. 32 kb + 31 ----
+                f32x16_t s[2] = {f32x16_t{}, f32x16_t{}};
+#pragma unroll
+                for (int ks = 0; ks < NKS; ++ks) {
+                    const bf16x8_t a = lds_b128(sK + k_off + kb * 32 * Lds::K_STRIDE + ks * 16);
+                    s[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[0][ks], s[0], 0, 0, 0);
+                    s[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[1][ks], s[1], 0, 0, 0);
+                }
+                // Element j of s[qb] is key kt*64 + 32 kb + 16 (j/8) + 8 hh + j%8
+                // for query q_wave0 + 32 qb + n.  On the diagonal tile
+                // (q_wave0 == kt*64) keys past the query are removed:
+                // lim = query - kt*64 - 8 hh.
+                bf16x8_t pb[2][2];   // [qb][k-step]
+#pragma unroll
+                for (int qb = 0; qb < 2; ++qb) {
+                    const int lim = 32 * qb + n - 8 * hh;
+                    if constexpr (DIAG) {
+#pragma unroll
+                        for (int j = 0; j < 16; ++j)
+                            if (32 * kb + 16 * (j / 8) + (j % 8) > lim) s[qb][j] = -INFINITY;
+                    }
+                    float mt = s[qb][0];
+#pragma unroll
+                    for (int j = 1; j < 16; ++j) mt = fmaxf(mt, s[qb][j]);
+                    if (__any(mt * sl2 > ms[qb] + kLazyRescale)) {
+                        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+                        const float m_new = fmaxf(ms[qb], mt * sl2);
+                        const float alpha = ms[qb] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms[qb] - m_new);
+#pragma unroll
+                        for (int db = 0; db < NDB; ++db) acc[qb][db] *= alpha;
+                        lp[qb] *= alpha;
+                        ms[qb] = m_new;
+                    }
+                    const float nm = -ms[qb];
+                    float p[16];
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) {
+                        p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][j], sl2, nm));
+                        if constexpr (DIAG) {
+                            // exact zero also when the scale is 0 (0 * -inf)
+                            if (32 * kb + 16 * (j / 8) + (j % 8) > lim) p[j] = 0.f;
+                        }
+                        lp[qb] += p[j];
+                    }
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+                        const bf16x2_t p01 = __builtin_convertvector(f32x2_t{p[8 * t + 0], p[8 * t + 1]}, bf16x2_t);
+                        const bf16x2_t p23 = __builtin_convertvector(f32x2_t{p[8 * t + 2], p[8 * t + 3]}, bf16x2_t);
+                        const bf16x2_t p45 = __builtin_convertvector(f32x2_t{p[8 * t + 4], p[8 * t + 5]}, bf16x2_t);
+                        const bf16x2_t p67 = __builtin_convertvector(f32x2_t{p[8 * t + 6], p[8 * t + 7]}, bf16x2_t);
+                        pb[qb][t] = __builtin_bit_cast(
+                            bf16x8_t, make_uint4(__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23),
+                                                 __builtin_bit_cast(uint32_t, p45), __builtin_bit_cast(uint32_t, p67)));
+                    }
+                }
+                // ---- O^T += V^T P^T over the same 32 keys ----
+#pragma unroll
+                for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+                        const bf16x8_t a = lds_b128(sK + v_off + db * 32 * Lds::V_STRIDE + kb * 32 + t * 16);
+                        acc[0][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[0][t], acc[0][db], 0, 0, 0);
+                        acc[1][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[1][t], acc[1][db], 0, 0, 0);
+                    }
+            }
+        };
+        if (kt + 1 < wave_kt) tile(std::false_type{});
+        else if (kt + 1 == wave_kt) tile(std::true_type{});
+
+        if (more) {
+            // The other stage was last read before the barrier that ended the
+            // previous iteration.
+            uint16_t* nK = stage_base + ((kt + 1) & 1) * Lds::STAGE;
+            bf_store<D>(next, mp, nK, nK + Lds::K_ELEMS);
+        }
+        __syncthreads();
+    }
+
+    // ---- normalise and store: element j of acc[qb][db] is
+    //      O[q_wave0 + 32 qb + n][32 db + 8 (j/4) + 4 hh + j%4] ----
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        const float l = lp[qb] + __shfl_xor(lp[qb], 32, 64);
+        const int qi = q_wave0 + qb * 32 + n;
+        if (qi >= L) continue;
+        const float inv = 1.0f / l;
+        float* orow = pa.out + wk.b * pa.os[0] + wk.h * pa.os[1] + qi * pa.os[2] + 4 * hh;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+                *reinterpret_cast<float4*>(orow + 32 * db + 8 * jj) =
+                    make_float4(acc[qb][db][4 * jj] * inv, acc[qb][db][4 * jj + 1] * inv,
+                                acc[qb][db][4 * jj + 2] * inv, acc[qb][db][4 * jj + 3] * inv);
+    }
+}
+
+// ===========================================================================
+// fp32 kernel
+// ===========================================================================
+constexpr int kFQTile = 128;    // queries per workgroup
+constexpr int kFThreads = 256;
+
+template <int D>
+struct F32Lds {
+    static constexpr int K_STRIDE = D + 4;           // K row-major [64][D + 4]
+    static constexpr int V_STRIDE = D + 4;           // V row-major [64][D + 4]
+    static constexpr int K_ELEMS = kKTile * K_STRIDE;
+    static constexpr int STAGE = K_ELEMS + kKTile * V_STRIDE;   // floats per stage
+    static constexpr int BYTES = 2 * STAGE * 4;
+    static constexpr int CPR = D / 4;                // 16-byte chunks per row
+    static constexpr int NK = kKTile * CPR / kFThreads;
+};
+
+template <int D>
+struct F32Stage {
+    u32x4_t k[F32Lds<D>::NK];
+    u32x4_t v[F32Lds<D>::NK];
+};
+
+template <int D>
+__device__ __forceinline__ void f32_load(F32Stage<D>& st, const float* K, const float* V, long long kv_row,
+                                         int key0, int L) {
+    using Lds = F32Lds<D>;
+    const int rmax = L - 1 - key0;
+#pragma unroll
+    for (int i = 0; i < Lds::NK; ++i) {
+        const int idx = threadIdx.x + i * kFThreads;
+        const long long off = min(idx / Lds::CPR, rmax) * kv_row + (idx % Lds::CPR) * 4;
+        st.k[i] = *reinterpret_cast<const u32x4_t*>(K + key0 * kv_row + off);
+        st.v[i] = *reinterpret_cast<const u32x4_t*>(V + key0 * kv_row + off);
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void f32_store(const F32Stage<D>& st, float* sK, float* sV) {
+    using Lds = F32Lds<D>;
+#pragma unroll
+    for (int i = 0; i < Lds::NK; ++i) {
+        const int idx = threadIdx.x + i * kFThreads;
+        const int r = idx / Lds::CPR, c = (idx % Lds::CPR) * 4;
+        *reinterpret_cast<u32x4_t*>(sK + r * Lds::K_STRIDE + c) = st.k[i];
+        *reinterpret_cast<u32x4_t*>(sV + r * Lds::V_STRIDE + c) = st.v[i];
+    }
+}
 
 __device__ __forceinline__ float xsum16_32(float v) {
     v += swz_xor16(v);
@@ -71,136 +414,41 @@ __device__ __forceinline__ float xmax16_32(float v) {
     return v;
 }
 
-template <bool BF16, int D>
-struct TileStage {
-    uint4 k[PrefillLds<BF16, D>::NK];
-    uint4 v[PrefillLds<BF16, D>::NV];
-};
-
-// Global -> registers for the K/V tile starting at key0.  K: thread t reads
-// row t / CPR (consecutive lanes cover whole rows).  bf16 V: thread t reads
-// the row pair (2 rp, 2 rp + 1), rp = t % 32, at chunk t / 32, so the
-// transposed LDS writes of a wave land on distinct banks.  Rows past L read 0.
-template <bool BF16, int D>
-__device__ __forceinline__ void load_tile(TileStage<BF16, D>& st, const typename PrefillLds<BF16, D>::elem* K,
-                                          const typename PrefillLds<BF16, D>::elem* V, long long kv_row,
-                                          int key0, int L) {
-    using Lds = PrefillLds<BF16, D>;
-    constexpr int CPR = Lds::CPR, EPV = Lds::EPV;
-#pragma unroll
-    for (int i = 0; i < Lds::NK; ++i) {
-        const int idx = threadIdx.x + i * kPThreads;
-        const int r = idx / CPR, c = idx % CPR;
-        const int key = key0 + r;
-        st.k[i] = key < L ? *reinterpret_cast<const uint4*>(K + key * kv_row + c * EPV) : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < Lds::NV; ++i) {
-        int r, c;
-        if constexpr (BF16) {
-            const int item = threadIdx.x + (i / 2) * kPThreads;   // (row pair, chunk)
-            r = 2 * (item % 32) + (i & 1);
-            c = item / 32;
-        } else {
-            const int idx = threadIdx.x + i * kPThreads;
-            r = idx / CPR;
-            c = idx % CPR;
-        }
-        const int key = key0 + r;
-        st.v[i] = key < L ? *reinterpret_cast<const uint4*>(V + key * kv_row + c * EPV) : make_uint4(0, 0, 0, 0);
-    }
-}
-
-// Registers -> LDS stage (K row-major; bf16 V transposed with one 4-byte
-// store per (d, key pair)).
-template <bool BF16, int D>
-__device__ __forceinline__ void store_tile(const TileStage<BF16, D>& st, typename PrefillLds<BF16, D>::elem* sK,
-                                           typename PrefillLds<BF16, D>::elem* sV) {
-    using Lds = PrefillLds<BF16, D>;
-    constexpr int CPR = Lds::CPR, EPV = Lds::EPV;
-#pragma unroll
-    for (int i = 0; i < Lds::NK; ++i) {
-        const int idx = threadIdx.x + i * kPThreads;
-        *reinterpret_cast<uint4*>(sK + (idx / CPR) * Lds::K_STRIDE + (idx % CPR) * EPV) = st.k[i];
-    }
-    if constexpr (BF16) {
-#pragma unroll
-        for (int i = 0; i < Lds::NV; i += 2) {
-            const int item = threadIdx.x + (i / 2) * kPThreads;
-            const int rp = item % 32, c = item / 32;
-            const uint32_t* lo = reinterpret_cast<const uint32_t*>(&st.v[i]);
-            const uint32_t* hi = reinterpret_cast<const uint32_t*>(&st.v[i + 1]);
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                // elements 2w, 2w+1 of the chunk for keys 2rp (lo) and 2rp+1 (hi)
-                const uint32_t e0 = (lo[w] & 0xffffu) | (hi[w] << 16);
-                const uint32_t e1 = (lo[w] >> 16) | (hi[w] & 0xffff0000u);
-                *reinterpret_cast<uint32_t*>(sV + (c * 8 + 2 * w) * Lds::V_STRIDE + 2 * rp) = e0;
-                *reinterpret_cast<uint32_t*>(sV + (c * 8 + 2 * w + 1) * Lds::V_STRIDE + 2 * rp) = e1;
-            }
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < Lds::NV; ++i) {
-            const int idx = threadIdx.x + i * kPThreads;
-            *reinterpret_cast<uint4*>(sV + (idx / CPR) * Lds::V_STRIDE + (idx % CPR) * EPV) = st.v[i];
-        }
-    }
-}
-
-template <bool BF16, int D>
-__global__ void __launch_bounds__(kPThreads)
-prefill_causal_kernel(PrefillArgs pa) {
-    const int Hq = pa.Hq, Hkv = pa.Hkv, L = pa.L;
-    // Scores go to the log2 domain once: p = 2^(s - m) with s = q.k * scale * log2(e).
+template <int D>
+__global__ void __launch_bounds__(kFThreads)
+prefill_f32_kernel(PrefillArgs pa) {
+    using Lds = F32Lds<D>;
+    const int L = pa.L;
     const float sl2 = pa.scale * kLog2eP;
-    using Lds = PrefillLds<BF16, D>;
-    using elem = typename Lds::elem;
     constexpr int NDB = D / 16;            // 16-wide d blocks of the output
+    constexpr int QF = D / 4;              // k-steps over D
     extern __shared__ __align__(16) unsigned char smem[];
-    elem* stage_base = reinterpret_cast<elem*>(smem);
+    float* stage_base = reinterpret_cast<float*>(smem);
 
-    const int n_qt = (L + kQTile - 1) / kQTile;
-    const int qt = n_qt - 1 - blockIdx.x;      // heaviest tiles first
-    const int bh = blockIdx.y;                 // b * Hq + h
-    const int b = bh / Hq, h = bh % Hq;
-    const int kvh = h / (Hq / Hkv);
+    const Work wk = map_work(pa, blockIdx.x);
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int g = lane >> 4;                   // lane group 0..3
     const int c16 = lane & 15;
 
-    const elem* Q = static_cast<const elem*>(pa.q) + b * pa.qs[0] + h * pa.qs[1];
-    const elem* K = static_cast<const elem*>(pa.k) + b * pa.kvs[0] + kvh * pa.kvs[1];
-    const elem* V = static_cast<const elem*>(pa.v) + b * pa.kvs[0] + kvh * pa.kvs[1];
+    const float* Q = static_cast<const float*>(pa.q) + wk.b * pa.qs[0] + wk.h * pa.qs[1];
+    const float* K = static_cast<const float*>(pa.k) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
+    const float* V = static_cast<const float*>(pa.v) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
     const long long q_row = pa.qs[2], kv_row = pa.kvs[2];
 
-    const int q_wave0 = qt * kQTile + wave * 32;   // first query of this wave
-    const int q_last_wg = min(L, (qt + 1) * kQTile) - 1;
-    const int n_kt = q_last_wg / kKTile + 1;
+    const int q_wave0 = wk.qt * kFQTile + wave * 32;   // first query of this wave
+    const int n_kt = (min(L, (wk.qt + 1) * kFQTile) - 1) / kKTile + 1;
 
-    // Tile 0 in flight while Q is read.
-    TileStage<BF16, D> next;
-    load_tile<BF16, D>(next, K, V, kv_row, 0, L);
+    F32Stage<D> next;
+    f32_load<D>(next, K, V, kv_row, 0, L);
 
     // Q^T fragments (B operand) per 16-query group.
-    constexpr int QF = BF16 ? D / 32 : D / 4;      // k-steps over D
-    using qfrag_t = typename std::conditional<BF16, bf16x8_t, float>::type;
-    qfrag_t qf[2][QF];
+    float qf[2][QF];
 #pragma unroll
     for (int gq = 0; gq < 2; ++gq) {
-        const int qi = q_wave0 + gq * 16 + c16;
-        const bool ok = qi < L;
+        const int qi = min(q_wave0 + gq * 16 + c16, L - 1);
 #pragma unroll
-        for (int s = 0; s < QF; ++s) {
-            if constexpr (BF16) {
-                uint4 raw = ok ? *reinterpret_cast<const uint4*>(Q + qi * q_row + s * 32 + g * 8)
-                               : make_uint4(0, 0, 0, 0);
-                qf[gq][s] = __builtin_bit_cast(bf16x8_t, raw);
-            } else {
-                qf[gq][s] = ok ? Q[qi * q_row + s * 4 + g] : 0.f;
-            }
-        }
+        for (int s = 0; s < QF; ++s) qf[gq][s] = Q[qi * q_row + s * 4 + g];
     }
 
     f32x4_t acc[2][NDB];
@@ -211,18 +459,17 @@ prefill_causal_kernel(PrefillArgs pa) {
     float m_run[2] = {-INFINITY, -INFINITY};
     float l_run[2] = {0.f, 0.f};
 
-    store_tile<BF16, D>(next, stage_base, stage_base + kKTile * Lds::K_STRIDE);
+    f32_store<D>(next, stage_base, stage_base + Lds::K_ELEMS);
     __syncthreads();
 
     for (int kt = 0; kt < n_kt; ++kt) {
         const int key0 = kt * kKTile;
-        elem* sK = stage_base + (kt & 1) * Lds::STAGE;
-        elem* sV = sK + kKTile * Lds::K_STRIDE;
+        const float* sK = stage_base + (kt & 1) * Lds::STAGE;
+        const float* sV = sK + Lds::K_ELEMS;
         const bool more = kt + 1 < n_kt;
-        // Next tile's loads fly during this tile's MFMAs.
-        if (more) load_tile<BF16, D>(next, K, V, kv_row, key0 + kKTile, L);
+        if (more) f32_load<D>(next, K, V, kv_row, key0 + kKTile, L);
 
-        if (key0 <= q_wave0 + 31) {   // else the whole wave is above the diagonal
+        if (key0 <= q_wave0 + 31 && q_wave0 < L) {   // else the whole wave is above the diagonal
             const bool diag = key0 + kKTile - 1 > q_wave0;
 #pragma unroll
             for (int gq = 0; gq < 2; ++gq) {
@@ -232,17 +479,10 @@ prefill_causal_kernel(PrefillArgs pa) {
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
                     f32x4_t s = {0.f, 0.f, 0.f, 0.f};
-                    const elem* krow = sK + (c * 16 + c16) * Lds::K_STRIDE;
+                    const float* krow = sK + (c * 16 + c16) * Lds::K_STRIDE;
 #pragma unroll
-                    for (int ks = 0; ks < QF; ++ks) {
-                        if constexpr (BF16) {
-                            bf16x8_t a = __builtin_bit_cast(
-                                bf16x8_t, *reinterpret_cast<const uint4*>(krow + ks * 32 + g * 8));
-                            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[gq][ks], s, 0, 0, 0);
-                        } else {
-                            s = __builtin_amdgcn_mfma_f32_16x16x4f32(krow[ks * 4 + g], qf[gq][ks], s, 0, 0, 0);
-                        }
-                    }
+                    for (int ks = 0; ks < QF; ++ks)
+                        s = __builtin_amdgcn_mfma_f32_16x16x4f32(krow[ks * 4 + g], qf[gq][ks], s, 0, 0, 0);
                     st[c] = s;
                 }
                 // ---- mask, online softmax in the log2 domain (per query = per lane) ----
@@ -254,7 +494,7 @@ prefill_causal_kernel(PrefillArgs pa) {
                         float sv = st[c][i] * sl2;
                         if (diag) {
                             const int key = key0 + c * 16 + g * 4 + i;
-                            if (key > qi || key >= L) sv = -INFINITY;
+                            if (key > qi) sv = -INFINITY;
                         }
                         st[c][i] = sv;
                         mt = fmaxf(mt, sv);
@@ -278,47 +518,24 @@ prefill_causal_kernel(PrefillArgs pa) {
                 for (int db = 0; db < NDB; ++db) acc[gq][db] *= alpha;
 
                 // ---- O^T += V^T P^T ----
-                if constexpr (BF16) {
 #pragma unroll
-                    for (int j = 0; j < 2; ++j) {
-                        const int c0 = 2 * j, c1 = 2 * j + 1;
-                        // hardware RNE conversion, two values per instruction
-                        bf16x2_t p01 = __builtin_convertvector(f32x2_t{st[c0][0], st[c0][1]}, bf16x2_t);
-                        bf16x2_t p23 = __builtin_convertvector(f32x2_t{st[c0][2], st[c0][3]}, bf16x2_t);
-                        bf16x2_t p45 = __builtin_convertvector(f32x2_t{st[c1][0], st[c1][1]}, bf16x2_t);
-                        bf16x2_t p67 = __builtin_convertvector(f32x2_t{st[c1][2], st[c1][3]}, bf16x2_t);
-                        const bf16x8_t pb = __builtin_bit_cast(
-                            bf16x8_t, make_uint4(__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23),
-                                                 __builtin_bit_cast(uint32_t, p45), __builtin_bit_cast(uint32_t, p67)));
+                for (int c = 0; c < 4; ++c)
 #pragma unroll
-                        for (int db = 0; db < NDB; ++db) {
-                            const elem* vrow = sV + (db * 16 + c16) * Lds::V_STRIDE;
-                            const uint2 lo = *reinterpret_cast<const uint2*>(vrow + c0 * 16 + g * 4);
-                            const uint2 hi = *reinterpret_cast<const uint2*>(vrow + c1 * 16 + g * 4);
-                            const bf16x8_t a = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
-                            acc[gq][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, acc[gq][db], 0, 0, 0);
-                        }
+                    for (int i = 0; i < 4; ++i) {
+                        const float pv = st[c][i];
+                        const float* vrow = sV + (c * 16 + g * 4 + i) * Lds::V_STRIDE;
+#pragma unroll
+                        for (int db = 0; db < NDB; ++db)
+                            acc[gq][db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vrow[db * 16 + c16], pv,
+                                                                               acc[gq][db], 0, 0, 0);
                     }
-                } else {
-#pragma unroll
-                    for (int c = 0; c < 4; ++c)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            const float pv = st[c][i];
-                            const elem* vrow = sV + (c * 16 + g * 4 + i) * Lds::V_STRIDE;
-#pragma unroll
-                            for (int db = 0; db < NDB; ++db)
-                                acc[gq][db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vrow[db * 16 + c16], pv,
-                                                                                   acc[gq][db], 0, 0, 0);
-                        }
-                }
             }
         }
         if (more) {
-            // The other stage was last read in the previous iteration, before
-            // the barrier that ended it.
-            elem* nK = stage_base + ((kt + 1) & 1) * Lds::STAGE;
-            store_tile<BF16, D>(next, nK, nK + kKTile * Lds::K_STRIDE);
+            // The other stage was last read before the barrier that ended the
+            // previous iteration.
+            float* nK = stage_base + ((kt + 1) & 1) * Lds::STAGE;
+            f32_store<D>(next, nK, nK + Lds::K_ELEMS);
         }
         __syncthreads();
     }
@@ -329,7 +546,7 @@ prefill_causal_kernel(PrefillArgs pa) {
         const int qi = q_wave0 + gq * 16 + c16;
         if (qi >= L) continue;
         const float inv = 1.0f / l_run[gq];
-        float* orow = pa.out + b * pa.os[0] + h * pa.os[1] + qi * pa.os[2];
+        float* orow = pa.out + wk.b * pa.os[0] + wk.h * pa.os[1] + qi * pa.os[2];
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
             float4 o4 = make_float4(acc[gq][db][0] * inv, acc[gq][db][1] * inv, acc[gq][db][2] * inv,
@@ -339,22 +556,53 @@ prefill_causal_kernel(PrefillArgs pa) {
     }
 }
 
-template <bool BF16, int D>
-sa_status launch_prefill(const PrefillArgs& pa, int B, hipStream_t st) {
-    using Lds = PrefillLds<BF16, D>;
-    if constexpr (Lds::BYTES > 65536) {
-        // The fp32 D=128 tile needs more than 64 KiB of LDS: opt in per device.
-        static thread_local int opted_device = -1;
-        int dev = 0;
-        SA_HIP_TRY(hipGetDevice(&dev));
-        if (opted_device != dev) {
-            SA_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_causal_kernel<BF16, D>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, Lds::BYTES));
-            opted_device = dev;
+// ===========================================================================
+// Launch
+// ===========================================================================
+template <class Kernel>
+sa_status opt_in_lds(Kernel* kernel, int bytes) {
+    if (bytes <= 65536) return SA_OK;
+    // Tiles above 64 KiB of LDS need the per-device opt-in.
+    static thread_local int opted_device = -1;
+    int dev = 0;
+    SA_HIP_TRY(hipGetDevice(&dev));
+    if (opted_device != dev) {
+        SA_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
+        opted_device = dev;
+    }
+    return SA_OK;
+}
+
+sa_status launch(PrefillArgs pa, int B, bool bf16, int D, hipStream_t st) {
+    const int q_tile = bf16 ? kBQTile : kFQTile;
+    pa.n_qt = (pa.L + q_tile - 1) / q_tile;
+    const int groups = B * pa.Hkv;
+    pa.xcd_groups = groups % 8 == 0 ? groups / 8 : 0;
+    const long long n_wg = (long long)B * pa.Hq * pa.n_qt;
+    if (n_wg > 0x7fffffffLL) return fail(SA_ERANGE, "prefill grid too large");
+    const dim3 grid(static_cast<unsigned>(n_wg));
+    if (bf16) {
+        if (D == 64) {
+            sa_status s = opt_in_lds(&prefill_bf16_kernel<64>, BfLds<64>::BYTES);
+            if (s != SA_OK) return s;
+            hipLaunchKernelGGL(prefill_bf16_kernel<64>, grid, dim3(kBThreads), BfLds<64>::BYTES, st, pa);
+        } else {
+            sa_status s = opt_in_lds(&prefill_bf16_kernel<128>, BfLds<128>::BYTES);
+            if (s != SA_OK) return s;
+            hipLaunchKernelGGL(prefill_bf16_kernel<128>, grid, dim3(kBThreads), BfLds<128>::BYTES, st, pa);
+        }
+    } else {
+        if (D == 64) {
+            sa_status s = opt_in_lds(&prefill_f32_kernel<64>, F32Lds<64>::BYTES);
+            if (s != SA_OK) return s;
+            hipLaunchKernelGGL(prefill_f32_kernel<64>, grid, dim3(kFThreads), F32Lds<64>::BYTES, st, pa);
+        } else {
+            sa_status s = opt_in_lds(&prefill_f32_kernel<128>, F32Lds<128>::BYTES);
+            if (s != SA_OK) return s;
+            hipLaunchKernelGGL(prefill_f32_kernel<128>, grid, dim3(kFThreads), F32Lds<128>::BYTES, st, pa);
         }
     }
-    dim3 grid((pa.L + kQTile - 1) / kQTile, B * pa.Hq);
-    hipLaunchKernelGGL((prefill_causal_kernel<BF16, D>), grid, dim3(kPThreads), Lds::BYTES, st, pa);
     SA_CHECK_LAUNCH();
     return SA_OK;
 }
@@ -375,15 +623,20 @@ sa_status prefill(const void* q, const void* k, const void* v, sa_dtype dtype, i
             return fail(SA_EINVAL, "strides must keep every row 16-byte aligned");
     }
     if (qs[2] < D || kvs[2] < D || os[2] < D) return fail(SA_EINVAL, "row stride shorter than head_dim");
+    // The kernels index rows inside one (batch, head) with 32-bit element offsets.
+    if ((int64_t)L * qs[2] >= (1LL << 31) || (int64_t)L * kvs[2] >= (1LL << 31) ||
+        (int64_t)L * os[2] >= (1LL << 31))
+        return fail(SA_ERANGE, "L * row stride must stay below 2^31 elements");
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
         return fail(SA_EINVAL, "q, k, v and out must be 16-byte aligned");
     PrefillArgs pa{};
     pa.q = q; pa.k = k; pa.v = v; pa.out = out;
     for (int i = 0; i < 3; ++i) { pa.qs[i] = qs[i]; pa.kvs[i] = kvs[i]; pa.os[i] = os[i]; }
-    pa.Hq = n_q_heads; pa.Hkv = n_kv_heads; pa.L = L; pa.scale = scale;
-    if (dtype == SA_DTYPE_BF16)
-        return D == 64 ? launch_prefill<true, 64>(pa, batch, st) : launch_prefill<true, 128>(pa, batch, st);
-    return D == 64 ? launch_prefill<false, 64>(pa, batch, st) : launch_prefill<false, 128>(pa, batch, st);
+    pa.Hq = n_q_heads; pa.Hkv = n_kv_heads; pa.L = L;
+    pa.scale = scale;
+    pa.sl2 = fabsf(scale) * kLog2eP;
+    pa.q_sign = scale < 0.f ? 0x80008000u : 0u;
+    return launch(pa, batch, dtype == SA_DTYPE_BF16, D, st);
 }
 
 }  // namespace

@@ -102,3 +102,45 @@ def test_prefill_last_row_is_decode(sa, synth):
     out = host(sa.prefill_causal(dev(q), dev(k), dev(v), sc))
     dec = host(sa.decode_dense(dev(q[:, :, L - 1]), dev(k), dev(v), sc))
     assert np.abs(out[:, :, L - 1] - dec).max() <= 1e-5
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,L", [(4, 4, 128, 300), (8, 2, 128, 513), (16, 8, 64, 300),
+                                        (2, 1, 64, 700), (16, 16, 128, 257)])
+def test_prefill_bf16_shapes(sa, oracle, synth, Hq, Hkv, D, L):
+    """bf16 at other head layouts, D = 64, batch 2, L off the tile sizes; 16/8
+    heads at batch 2 also exercise the per-XCD mapping of KV groups."""
+    q, k, v = inputs(synth, L, Hq, Hkv, D, seed=55)
+    q2 = synth.bf16_round(np.concatenate([q, synth.normal(56, 1, q.shape)], 0))
+    k2 = synth.bf16_round(np.concatenate([k, synth.normal(56, 2, k.shape)], 0))
+    v2 = synth.bf16_round(np.concatenate([v, synth.normal(56, 3, v.shape)], 0))
+    sc = np.float32(1 / np.sqrt(D))
+    t = lambda a: dev(a).to(torch.bfloat16)
+    out = host(sa.prefill_causal(t(q2), t(k2), t(v2), float(sc)))
+    want = oracle.prefill_blockwise(q2, k2, v2, sc, 64)
+    assert rel_l2(out, want) <= 2e-2
+    # every row, not only the aggregate: the worst row stays within tolerance
+    err = np.linalg.norm(out - want, axis=-1) / np.linalg.norm(want, axis=-1)
+    assert err.max() <= 4e-2
+
+
+@pytest.mark.parametrize("scale", [-0.3, 0.0])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_prefill_scale_sign(sa, oracle, synth, scale, bf16):
+    """Negative and zero scales (zero: uniform average over the prefix)."""
+    L = 200
+    q, k, v = inputs(synth, L, 4, 2, 128, seed=57)
+    if bf16:
+        q, k, v = synth.bf16_round(q), synth.bf16_round(k), synth.bf16_round(v)
+        t = lambda a: dev(a).to(torch.bfloat16)
+    else:
+        t = dev
+    out = host(sa.prefill_causal(t(q), t(k), t(v), scale))
+    want = oracle.prefill_blockwise(q, k, v, np.float32(scale), 64)
+    if bf16:
+        assert rel_l2(out, want) <= 2e-2
+    else:
+        assert np.abs(out - want).max() <= 1e-4
+        assert rel_l2(out, want) <= 1e-5
+    if scale == 0.0:
+        cum = np.cumsum(v.astype(np.float64), axis=2) / np.arange(1, L + 1)[:, None]
+        assert np.abs(out[:, ::2] - cum).max() <= (2e-2 if bf16 else 1e-5)
