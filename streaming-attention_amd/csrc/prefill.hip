@@ -82,23 +82,25 @@ __device__ __forceinline__ Work map_work(const PrefillArgs& pa, int i) {
 // ===========================================================================
 // bf16 kernel
 // ===========================================================================
-constexpr int kBWaves = 4;
-constexpr int kBQWave = 64;                      // queries per wave
-constexpr int kBQTile = kBWaves * kBQWave;       // queries per workgroup
-constexpr int kBThreads = kBWaves * 64;
+// A wave owns QB 32-query blocks; a workgroup of W waves owns W * QB * 32
+// queries and streams 64-key K/V tiles through two LDS stages.
 constexpr float kLazyRescale = 8.f;              // log2 headroom before a rescale
 
-template <int D>
+template <int D, int W>
 struct BfLds {
+    static constexpr int THREADS = W * 64;
     static constexpr int K_STRIDE = D + 8;           // K row-major [64][D + 8]
     static constexpr int V_STRIDE = kKTile + 8;      // V transposed [D][64 + 8]
     static constexpr int K_ELEMS = kKTile * K_STRIDE;
     static constexpr int STAGE = K_ELEMS + D * V_STRIDE;   // bf16 elements per stage
     static constexpr int BYTES = 2 * STAGE * 2;            // two stages
     static constexpr int CPR = D / 8;                // 16-byte chunks per row
-    static constexpr int NK = kKTile * CPR / kBThreads;    // K chunks per thread
-    static constexpr int NVI = 32 * CPR / kBThreads;       // V (row pair, chunk) items per thread
-    static_assert(NK >= 1 && NVI >= 1, "tile too small for the workgroup");
+    static constexpr int K_ITEMS = kKTile * CPR;     // 16-byte K chunks per tile
+    static constexpr int V_ITEMS = 32 * CPR;         // (row pair, chunk) V items per tile
+    static constexpr int NK = (K_ITEMS + THREADS - 1) / THREADS;
+    static constexpr int NVI = (V_ITEMS + THREADS - 1) / THREADS;
+    static_assert(K_ITEMS % THREADS == 0 || THREADS % K_ITEMS == 0, "K items must tile the workgroup");
+    static_assert(V_ITEMS % THREADS == 0 || THREADS % V_ITEMS == 0, "V items must tile the workgroup");
 };
 
 // The K rows a lane feeds to the score MFMA are permuted within each 32-key
@@ -109,30 +111,35 @@ struct BfLds {
 // of the 32x32x16 PV step needs, and what one 16-byte read of V^T supplies.
 __device__ __forceinline__ int swap_bits23(int m) { return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1); }
 
-template <int D>
+template <int D, int W>
 struct BfStage {
-    u32x4_t k[BfLds<D>::NK];
-    u32x4_t v[2 * BfLds<D>::NVI];
+    u32x4_t k[BfLds<D, W>::NK];
+    u32x4_t v[2 * BfLds<D, W>::NVI];
 };
 
 // Per-thread element offsets of the tile loads, relative to the tile's first
-// row.  K: chunk idx = tid + i*256 -> row idx / CPR.  V: item = tid + i*256
-// -> row pair item % 32 (rows 2rp, 2rp + 1), chunk item / 32.
-template <int D>
+// row.  K: chunk idx = tid + i*THREADS -> row idx / CPR.  V: item = tid +
+// i*THREADS -> row pair item % 32 (rows 2rp, 2rp + 1), chunk item / 32.
+// Threads past the item count (small head dims, many waves) idle; that split
+// falls on whole waves.
+template <int D, int W>
 struct BfLoadMap {
-    int k_row[BfLds<D>::NK], k_col[BfLds<D>::NK];
-    int v_row[BfLds<D>::NVI], v_col[BfLds<D>::NVI];
+    using Lds = BfLds<D, W>;
+    int k_row[Lds::NK], k_col[Lds::NK];
+    int v_row[Lds::NVI], v_col[Lds::NVI];
+    bool k_on, v_on;
     __device__ __forceinline__ BfLoadMap() {
-        using Lds = BfLds<D>;
+        k_on = threadIdx.x < Lds::K_ITEMS;
+        v_on = threadIdx.x < Lds::V_ITEMS;
 #pragma unroll
         for (int i = 0; i < Lds::NK; ++i) {
-            const int idx = threadIdx.x + i * kBThreads;
+            const int idx = threadIdx.x + i * Lds::THREADS;
             k_row[i] = idx / Lds::CPR;
             k_col[i] = (idx % Lds::CPR) * 8;
         }
 #pragma unroll
         for (int i = 0; i < Lds::NVI; ++i) {
-            const int item = threadIdx.x + i * kBThreads;
+            const int item = threadIdx.x + i * Lds::THREADS;
             v_row[i] = 2 * (item % 32);
             v_col[i] = (item / 32) * 8;
         }
@@ -141,55 +148,67 @@ struct BfLoadMap {
 
 // Global -> registers.  Rows past the end of the sequence are clamped to the
 // last row: they only feed keys that the causal mask removes.
-template <int D>
-__device__ __forceinline__ void bf_load(BfStage<D>& st, const BfLoadMap<D>& mp, const uint16_t* K,
+template <int D, int W>
+__device__ __forceinline__ void bf_load(BfStage<D, W>& st, const BfLoadMap<D, W>& mp, const uint16_t* K,
                                         const uint16_t* V, int kv_row, int key0, int L) {
-    using Lds = BfLds<D>;
+    using Lds = BfLds<D, W>;
     const uint16_t* Kt = K + (long long)key0 * kv_row;
     const uint16_t* Vt = V + (long long)key0 * kv_row;
     const int rmax = L - 1 - key0;
+    if (mp.k_on) {
 #pragma unroll
-    for (int i = 0; i < Lds::NK; ++i)
-        st.k[i] = *reinterpret_cast<const u32x4_t*>(Kt + min(mp.k_row[i], rmax) * kv_row + mp.k_col[i]);
+        for (int i = 0; i < Lds::NK; ++i)
+            st.k[i] = *reinterpret_cast<const u32x4_t*>(Kt + min(mp.k_row[i], rmax) * kv_row + mp.k_col[i]);
+    }
+    if (mp.v_on) {
 #pragma unroll
-    for (int i = 0; i < Lds::NVI; ++i) {
-        st.v[2 * i] = *reinterpret_cast<const u32x4_t*>(Vt + min(mp.v_row[i], rmax) * kv_row + mp.v_col[i]);
-        st.v[2 * i + 1] = *reinterpret_cast<const u32x4_t*>(Vt + min(mp.v_row[i] + 1, rmax) * kv_row + mp.v_col[i]);
+        for (int i = 0; i < Lds::NVI; ++i) {
+            st.v[2 * i] = *reinterpret_cast<const u32x4_t*>(Vt + min(mp.v_row[i], rmax) * kv_row + mp.v_col[i]);
+            st.v[2 * i + 1] =
+                *reinterpret_cast<const u32x4_t*>(Vt + min(mp.v_row[i] + 1, rmax) * kv_row + mp.v_col[i]);
+        }
     }
 }
-
 
 // Registers -> LDS stage.  K row-major; V transposed with one 4-byte store
 // per (d, key pair): lanes of a wave cover 32 consecutive key pairs of one d,
 // so each store instruction touches 32 distinct banks per half-wave.
-template <int D>
-__device__ __forceinline__ void bf_store(const BfStage<D>& st, const BfLoadMap<D>& mp, uint16_t* sK, uint16_t* sV) {
-    using Lds = BfLds<D>;
+template <int D, int W>
+__device__ __forceinline__ void bf_store(const BfStage<D, W>& st, const BfLoadMap<D, W>& mp, uint16_t* sK,
+                                         uint16_t* sV) {
+    using Lds = BfLds<D, W>;
+    if (mp.k_on) {
 #pragma unroll
-    for (int i = 0; i < Lds::NK; ++i)
-        *reinterpret_cast<u32x4_t*>(sK + mp.k_row[i] * Lds::K_STRIDE + mp.k_col[i]) = st.k[i];
+        for (int i = 0; i < Lds::NK; ++i)
+            *reinterpret_cast<u32x4_t*>(sK + mp.k_row[i] * Lds::K_STRIDE + mp.k_col[i]) = st.k[i];
+    }
+    if (mp.v_on) {
 #pragma unroll
-    for (int i = 0; i < Lds::NVI; ++i) {
-        const u32x4_t lo = st.v[2 * i], hi = st.v[2 * i + 1];
-        uint16_t* col = sV + mp.v_col[i] * Lds::V_STRIDE + mp.v_row[i];
+        for (int i = 0; i < Lds::NVI; ++i) {
+            const u32x4_t lo = st.v[2 * i], hi = st.v[2 * i + 1];
+            uint16_t* col = sV + mp.v_col[i] * Lds::V_STRIDE + mp.v_row[i];
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            // elements 2w, 2w+1 of the chunk: key pair (lo, hi) for each
-            *reinterpret_cast<uint32_t*>(col + (2 * w) * Lds::V_STRIDE) = __builtin_amdgcn_perm(hi[w], lo[w], 0x05040100u);
-            *reinterpret_cast<uint32_t*>(col + (2 * w + 1) * Lds::V_STRIDE) =
-                __builtin_amdgcn_perm(hi[w], lo[w], 0x07060302u);
+            for (int w = 0; w < 4; ++w) {
+                // elements 2w, 2w+1 of the chunk: key pair (lo, hi) for each
+                *reinterpret_cast<uint32_t*>(col + (2 * w) * Lds::V_STRIDE) =
+                    __builtin_amdgcn_perm(hi[w], lo[w], 0x05040100u);
+                *reinterpret_cast<uint32_t*>(col + (2 * w + 1) * Lds::V_STRIDE) =
+                    __builtin_amdgcn_perm(hi[w], lo[w], 0x07060302u);
+            }
         }
     }
 }
 
 __device__ __forceinline__ bf16x8_t lds_b128(const uint16_t* p) { return *reinterpret_cast<const bf16x8_t*>(p); }
 
-template <int D>
-__global__ void __launch_bounds__(kBThreads)
+template <int D, int QB, int W>
+__global__ void __launch_bounds__(W * 64)
 prefill_bf16_kernel(PrefillArgs pa) {
-    using Lds = BfLds<D>;
+    using Lds = BfLds<D, W>;
     constexpr int NKS = D / 16;     // k-steps of the score product
     constexpr int NDB = D / 32;     // 32-row d blocks of O^T
+    constexpr int QWAVE = 32 * QB;  // queries per wave
+    constexpr int QTILE = W * QWAVE;
     extern __shared__ __align__(16) unsigned char smem[];
     uint16_t* stage_base = reinterpret_cast<uint16_t*>(smem);
 
@@ -206,20 +225,21 @@ prefill_bf16_kernel(PrefillArgs pa) {
     const uint16_t* V = static_cast<const uint16_t*>(pa.v) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
     const int kv_row = static_cast<int>(pa.kvs[2]);
 
-    const int q_wave0 = wk.qt * kBQTile + wave * kBQWave;
-    const int n_kt = (min(L, (wk.qt + 1) * kBQTile) - 1) / kKTile + 1;
+    const int q_wave0 = wk.qt * QTILE + wave * QWAVE;
+    const int n_kt = (min(L, (wk.qt + 1) * QTILE) - 1) / kKTile + 1;
     // Tiles this wave computes: keys up to its last query.  The last one is
-    // the diagonal tile (q_wave0 is a multiple of the key tile).
-    const int wave_kt = q_wave0 < L ? q_wave0 / kKTile + 1 : 0;
+    // the diagonal tile; dq is the wave's first query relative to it.
+    const int wave_kt = q_wave0 < L ? (q_wave0 + QWAVE - 1) / kKTile + 1 : 0;
+    const int dq = q_wave0 - (wave_kt - 1) * kKTile;
 
-    const BfLoadMap<D> mp;
-    BfStage<D> next;
-    bf_load<D>(next, mp, K, V, kv_row, 0, L);
+    const BfLoadMap<D, W> mp;
+    BfStage<D, W> next;
+    bf_load<D, W>(next, mp, K, V, kv_row, 0, L);
 
     // Q^T fragments (B operand): lane holds q[n][16 ks + 8 hh .. + 7].
-    bf16x8_t qf[2][NKS];
+    bf16x8_t qf[QB][NKS];
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
         const int qi = min(q_wave0 + qb * 32 + n, L - 1);
         const uint16_t* qrow = Q + qi * pa.qs[2] + 8 * hh;
 #pragma unroll
@@ -231,75 +251,86 @@ prefill_bf16_kernel(PrefillArgs pa) {
         }
     }
 
-    f32x16_t acc[2][NDB];
+    f32x16_t acc[QB][NDB];
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
+    for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
         for (int db = 0; db < NDB; ++db) acc[qb][db] = f32x16_t{};
-    float ms[2] = {-INFINITY, -INFINITY};   // running max (log2 domain), equal in both lane halves
-    float lp[2] = {0.f, 0.f};               // row-sum part over this lane half's keys
+    float ms[QB], lp[QB];   // running max (log2 domain, equal in both lane halves); row-sum part
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) { ms[qb] = -INFINITY; lp[qb] = 0.f; }
 
     // Per-lane LDS read offsets (elements) inside a stage.
     const int k_off = swap_bits23(n) * Lds::K_STRIDE + 8 * hh;
     const int v_off = Lds::K_ELEMS + n * Lds::V_STRIDE + 8 * hh;
 
-    bf_store<D>(next, mp, stage_base, stage_base + Lds::K_ELEMS);
+    bf_store<D, W>(next, mp, stage_base, stage_base + Lds::K_ELEMS);
     __syncthreads();
 
     for (int kt = 0; kt < n_kt; ++kt) {
         const uint16_t* sK = stage_base + (kt & 1) * Lds::STAGE;
-        const bool more = kt + 1 < n_kt;
-        if (more) bf_load<D>(next, mp, K, V, kv_row, (kt + 1) * kKTile, L);
+        // Next tile's loads fly during this tile's MFMAs.  Past the last tile
+        // they read clamped, in-range rows into a stage nobody reads.
+        bf_load<D, W>(next, mp, K, V, kv_row, (kt + 1) * kKTile, L);
 
-        // One tile, as two 32-key halves kb: scores, softmax, then the PV
-        // product of that half.  DIAG instantiates the diagonal tile's mask.
+        // One tile, as two 32-key halves kb.  Per half: the K fragments are
+        // read up front, the score MFMAs of all query blocks share them; the
+        // V fragments are issued next so their latency hides behind the
+        // softmax; the softmax assumes the running max holds and a rare fix-up
+        // handles a raised max; then the PV MFMAs.  DIAG instantiates the
+        // diagonal tile's mask.
         auto tile = [&](auto diag_tag) {
             constexpr bool DIAG = decltype(diag_tag)::value;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
                 // ---- S^T = K Q^T for keys 32 kb .. 32 kb + 31 ----
-                f32x16_t s[2] = {f32x16_t{}, f32x16_t{}};
+                bf16x8_t kf[NKS];
 #pragma unroll
-                for (int ks = 0; ks < NKS; ++ks) {
-                    const bf16x8_t a = lds_b128(sK + k_off + kb * 32 * Lds::K_STRIDE + ks * 16);
-                    s[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[0][ks], s[0], 0, 0, 0);
-                    s[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[1][ks], s[1], 0, 0, 0);
-                }
+                for (int ks = 0; ks < NKS; ++ks) kf[ks] = lds_b128(sK + k_off + kb * 32 * Lds::K_STRIDE + ks * 16);
+                f32x16_t s[QB];
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb) s[qb] = f32x16_t{};
+#pragma unroll
+                for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+                    for (int qb = 0; qb < QB; ++qb)
+                        s[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qf[qb][ks], s[qb], 0, 0, 0);
+                bf16x8_t vf[NDB][2];
+#pragma unroll
+                for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                    for (int t = 0; t < 2; ++t)
+                        vf[db][t] = lds_b128(sK + v_off + db * 32 * Lds::V_STRIDE + kb * 32 + t * 16);
+
                 // Element j of s[qb] is key kt*64 + 32 kb + 16 (j/8) + 8 hh + j%8
-                // for query q_wave0 + 32 qb + n.  On the diagonal tile
-                // (q_wave0 == kt*64) keys past the query are removed:
-                // lim = query - kt*64 - 8 hh.
-                bf16x8_t pb[2][2];   // [qb][k-step]
+                // for query q_wave0 + 32 qb + n.  On the diagonal tile keys past
+                // the query are removed (query - kt*64 = dq + 32 qb + n).
+                auto masked = [&](int qb, int j) {
+                    return DIAG && 32 * kb + 16 * (j / 8) + 8 * hh + (j % 8) > dq + 32 * qb + n;
+                };
+                float mt[QB];
 #pragma unroll
-                for (int qb = 0; qb < 2; ++qb) {
-                    const int lim = 32 * qb + n - 8 * hh;
+                for (int qb = 0; qb < QB; ++qb) {
                     if constexpr (DIAG) {
 #pragma unroll
                         for (int j = 0; j < 16; ++j)
-                            if (32 * kb + 16 * (j / 8) + (j % 8) > lim) s[qb][j] = -INFINITY;
+                            if (masked(qb, j)) s[qb][j] = -INFINITY;
                     }
-                    float mt = s[qb][0];
+                    mt[qb] = s[qb][0];
 #pragma unroll
-                    for (int j = 1; j < 16; ++j) mt = fmaxf(mt, s[qb][j]);
-                    if (__any(mt * sl2 > ms[qb] + kLazyRescale)) {
-                        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-                        const float m_new = fmaxf(ms[qb], mt * sl2);
-                        const float alpha = ms[qb] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms[qb] - m_new);
-#pragma unroll
-                        for (int db = 0; db < NDB; ++db) acc[qb][db] *= alpha;
-                        lp[qb] *= alpha;
-                        ms[qb] = m_new;
-                    }
+                    for (int j = 1; j < 16; ++j) mt[qb] = fmaxf(mt[qb], s[qb][j]);
+                }
+                bf16x8_t pb[QB][2];
+                float rs[QB];
+                auto softmax = [&](int qb) {
                     const float nm = -ms[qb];
                     float p[16];
+                    rs[qb] = 0.f;
 #pragma unroll
                     for (int j = 0; j < 16; ++j) {
                         p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][j], sl2, nm));
-                        if constexpr (DIAG) {
-                            // exact zero also when the scale is 0 (0 * -inf)
-                            if (32 * kb + 16 * (j / 8) + (j % 8) > lim) p[j] = 0.f;
-                        }
-                        lp[qb] += p[j];
+                        if (masked(qb, j)) p[j] = 0.f;   // exact zero also for a zero scale
+                        rs[qb] += p[j];
                     }
 #pragma unroll
                     for (int t = 0; t < 2; ++t) {
@@ -311,34 +342,58 @@ prefill_bf16_kernel(PrefillArgs pa) {
                             bf16x8_t, make_uint4(__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23),
                                                  __builtin_bit_cast(uint32_t, p45), __builtin_bit_cast(uint32_t, p67)));
                     }
+                };
+                bool up = false;
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb) {
+                    softmax(qb);
+                    // Keep the common-case softmax ahead of the branch (the
+                    // compiler would otherwise sink it into the no-rescale path).
+                    asm volatile("" : "+v"(pb[qb][0]), "+v"(pb[qb][1]), "+v"(rs[qb]));
+                    up = up || mt[qb] * sl2 > ms[qb] + kLazyRescale;
                 }
+                if (__any(up)) {
+                    // Raise the max to the exact row max of this half (both
+                    // lane halves agree), rescale, redo the softmax.
+#pragma unroll
+                    for (int qb = 0; qb < QB; ++qb) {
+                        const float mq = fmaxf(mt[qb], __shfl_xor(mt[qb], 32, 64));
+                        const float m_new = fmaxf(ms[qb], mq * sl2);
+                        const float alpha = ms[qb] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms[qb] - m_new);
+#pragma unroll
+                        for (int db = 0; db < NDB; ++db) acc[qb][db] *= alpha;
+                        lp[qb] *= alpha;
+                        ms[qb] = m_new;
+                        softmax(qb);
+                    }
+                }
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb) lp[qb] += rs[qb];
                 // ---- O^T += V^T P^T over the same 32 keys ----
 #pragma unroll
                 for (int db = 0; db < NDB; ++db)
 #pragma unroll
-                    for (int t = 0; t < 2; ++t) {
-                        const bf16x8_t a = lds_b128(sK + v_off + db * 32 * Lds::V_STRIDE + kb * 32 + t * 16);
-                        acc[0][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[0][t], acc[0][db], 0, 0, 0);
-                        acc[1][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[1][t], acc[1][db], 0, 0, 0);
-                    }
+                    for (int t = 0; t < 2; ++t)
+#pragma unroll
+                        for (int qb = 0; qb < QB; ++qb)
+                            acc[qb][db] =
+                                __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][t], pb[qb][t], acc[qb][db], 0, 0, 0);
             }
         };
         if (kt + 1 < wave_kt) tile(std::false_type{});
         else if (kt + 1 == wave_kt) tile(std::true_type{});
 
-        if (more) {
-            // The other stage was last read before the barrier that ended the
-            // previous iteration.
-            uint16_t* nK = stage_base + ((kt + 1) & 1) * Lds::STAGE;
-            bf_store<D>(next, mp, nK, nK + Lds::K_ELEMS);
-        }
+        // The other stage was last read before the barrier that ended the
+        // previous iteration.
+        uint16_t* nK = stage_base + ((kt + 1) & 1) * Lds::STAGE;
+        bf_store<D, W>(next, mp, nK, nK + Lds::K_ELEMS);
         __syncthreads();
     }
 
     // ---- normalise and store: element j of acc[qb][db] is
     //      O[q_wave0 + 32 qb + n][32 db + 8 (j/4) + 4 hh + j%4] ----
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
         const float l = lp[qb] + __shfl_xor(lp[qb], 32, 64);
         const int qi = q_wave0 + qb * 32 + n;
         if (qi >= L) continue;
@@ -574,35 +629,42 @@ sa_status opt_in_lds(Kernel* kernel, int bytes) {
     return SA_OK;
 }
 
+// bf16 shape: W waves of QB 32-query blocks each.  Measured at L = 8192 on
+// MI355X: 4 waves x 64 queries (one wave per SIMD) 0.383 ms, 8 waves x 32
+// queries (two per SIMD) 0.414 ms.
+constexpr int kBfQB = 2;
+constexpr int kBfW = 4;
+
+template <int D, int QB, int W>
+sa_status launch_bf16(const PrefillArgs& pa, dim3 grid, hipStream_t st) {
+    constexpr int bytes = BfLds<D, W>::BYTES;
+    sa_status s = opt_in_lds(&prefill_bf16_kernel<D, QB, W>, bytes);
+    if (s != SA_OK) return s;
+    hipLaunchKernelGGL((prefill_bf16_kernel<D, QB, W>), grid, dim3(W * 64), bytes, st, pa);
+    return SA_OK;
+}
+
 sa_status launch(PrefillArgs pa, int B, bool bf16, int D, hipStream_t st) {
-    const int q_tile = bf16 ? kBQTile : kFQTile;
+    const int q_tile = bf16 ? kBfW * kBfQB * 32 : kFQTile;
     pa.n_qt = (pa.L + q_tile - 1) / q_tile;
     const int groups = B * pa.Hkv;
     pa.xcd_groups = groups % 8 == 0 ? groups / 8 : 0;
     const long long n_wg = (long long)B * pa.Hq * pa.n_qt;
     if (n_wg > 0x7fffffffLL) return fail(SA_ERANGE, "prefill grid too large");
     const dim3 grid(static_cast<unsigned>(n_wg));
+    sa_status s = SA_OK;
     if (bf16) {
-        if (D == 64) {
-            sa_status s = opt_in_lds(&prefill_bf16_kernel<64>, BfLds<64>::BYTES);
-            if (s != SA_OK) return s;
-            hipLaunchKernelGGL(prefill_bf16_kernel<64>, grid, dim3(kBThreads), BfLds<64>::BYTES, st, pa);
-        } else {
-            sa_status s = opt_in_lds(&prefill_bf16_kernel<128>, BfLds<128>::BYTES);
-            if (s != SA_OK) return s;
-            hipLaunchKernelGGL(prefill_bf16_kernel<128>, grid, dim3(kBThreads), BfLds<128>::BYTES, st, pa);
-        }
-    } else {
-        if (D == 64) {
-            sa_status s = opt_in_lds(&prefill_f32_kernel<64>, F32Lds<64>::BYTES);
-            if (s != SA_OK) return s;
+        s = D == 64 ? launch_bf16<64, kBfQB, kBfW>(pa, grid, st) : launch_bf16<128, kBfQB, kBfW>(pa, grid, st);
+    } else if (D == 64) {
+        s = opt_in_lds(&prefill_f32_kernel<64>, F32Lds<64>::BYTES);
+        if (s == SA_OK)
             hipLaunchKernelGGL(prefill_f32_kernel<64>, grid, dim3(kFThreads), F32Lds<64>::BYTES, st, pa);
-        } else {
-            sa_status s = opt_in_lds(&prefill_f32_kernel<128>, F32Lds<128>::BYTES);
-            if (s != SA_OK) return s;
+    } else {
+        s = opt_in_lds(&prefill_f32_kernel<128>, F32Lds<128>::BYTES);
+        if (s == SA_OK)
             hipLaunchKernelGGL(prefill_f32_kernel<128>, grid, dim3(kFThreads), F32Lds<128>::BYTES, st, pa);
-        }
     }
+    if (s != SA_OK) return s;
     SA_CHECK_LAUNCH();
     return SA_OK;
 }
