@@ -125,6 +125,9 @@ void* sa_kvcache_v_pool(sa_kvcache* cache, int layer);
 int32_t* sa_kvcache_block_table(sa_kvcache* cache);   /* [max_seqs][max_pages_per_seq] */
 int32_t* sa_kvcache_seq_lens(sa_kvcache* cache);      /* [max_seqs] committed lengths */
 size_t sa_kvcache_bytes(const sa_kvcache* cache);
+/* The geometry the cache was created with (an accessor with no counterpart in
+ * the reference; the model driver checks its shapes against it). */
+sa_status sa_kvcache_get_desc(const sa_kvcache* cache, sa_kv_desc* out);
 
 /* ------------------------------------------------------------------------
  * RoPE tables, built exactly as the reference: inv_freq[i] = 1/theta^(i/D),

@@ -50,6 +50,7 @@ _REF_SIGS = {
     "ref_self_attention_streaming": (None, [_P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _P]),
     "ref_blockwise": (None, [_P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _I, _P]),
     "ref_layer_attention": (_I, [_I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _F, _I, _I, _I, _P, _P]),
+    "ref_qwen3_forward": (_I, [_I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _I] + [_P] * 13),
 }
 
 
@@ -276,3 +277,26 @@ class Reference:
         if rc != 0:
             raise RuntimeError("reference layer raised")
         return attn, eff
+
+    def qwen3_forward(self, weights, cfg, tokens, prompt_len):
+        """qwen3_forward_with_cache over tokens [B][P + n] (teacher forcing):
+        a P-token prompt, then n one-token forwards.  weights as in
+        oracle.qwen3_model.  Returns logits [n + 1][B][V] at the last position
+        of each forward."""
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        B, N = tokens.shape
+        n_steps = N - prompt_len
+        c = cfg
+        L = weights["layers"]
+        stack = {t: _f32(np.stack([layer[t] for layer in L])) for t in L[0]}
+        glob = {t: _f32(weights[t]) for t in ("embed", "final_norm", "lm_head")}
+        logits = np.empty((n_steps + 1, B, c["vocab"]), np.float32)
+        rc = self.lib.ref_qwen3_forward(
+            c["num_layers"], c["hidden"], c["intermediate"], c["vocab"], c["n_q_heads"], c["n_kv_heads"],
+            c["head_dim"], c["rms_eps"], B, prompt_len, n_steps, _p(tokens), _p(glob["embed"]),
+            _p(stack["in_norm"]), _p(stack["qkv"]), _p(stack["q_norm"]), _p(stack["k_norm"]), _p(stack["o"]),
+            _p(stack["post_norm"]), _p(stack["gate_up"]), _p(stack["down"]), _p(glob["final_norm"]),
+            _p(glob["lm_head"]), _p(logits))
+        if rc != 0:
+            raise RuntimeError("reference forward raised")
+        return logits

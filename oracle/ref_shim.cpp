@@ -206,4 +206,59 @@ int ref_layer_attention(int Hq, int Hkv, int D, int prompt_len, int n_steps, con
     }
 }
 
+// Whole-model forward through the reference (qwen3_forward_with_cache,
+// tensor_cpp/src/qwen3_ops.cpp:936-1014) with its dense KVCache and STANDARD
+// attention: a prompt of P tokens per sequence, then n_steps one-token
+// forwards fed the given tokens (teacher forcing).  tokens [B][P + n_steps];
+// logits [n_steps + 1][B][V]: the last position of each forward.
+// Weights, all row-major fp32: embed [V][H], in_norm [nl][H],
+// qkv [nl][(Hq+2Hkv)D][H], q_norm/k_norm [nl][D], o [nl][H][Hq D],
+// post_norm [nl][H], gate_up [nl][2I][H] (gate rows then up rows),
+// down [nl][H][I], final_norm [H], lm_head [V][H].
+int ref_qwen3_forward(int nl, int H, int I, int V, int Hq, int Hkv, int D, float eps, int B, int P,
+                      int n_steps, const int* tokens, const float* embed, const float* in_norm,
+                      const float* qkv, const float* q_norm, const float* k_norm, const float* o,
+                      const float* post_norm, const float* gate_up, const float* down,
+                      const float* final_norm, const float* lm_head, float* logits) {
+    try {
+        const size_t qd = (size_t)Hq * D, kd = (size_t)Hkv * D, proj = qd + 2 * kd;
+        std::vector<q3::Qwen3LayerWeights> layers(nl);
+        for (int l = 0; l < nl; ++l) {
+            auto& w = layers[l];
+            w.input_layernorm_weight = make(in_norm + (size_t)l * H, {(size_t)H});
+            w.qkv_projs = make(qkv + (size_t)l * proj * H, {proj, (size_t)H});
+            w.q_norm_weight = make(q_norm + (size_t)l * D, {(size_t)D});
+            w.k_norm_weight = make(k_norm + (size_t)l * D, {(size_t)D});
+            w.o_proj = make(o + (size_t)l * H * qd, {(size_t)H, qd});
+            w.post_attention_layernorm_weight = make(post_norm + (size_t)l * H, {(size_t)H});
+            const float* gu = gate_up + (size_t)l * 2 * I * H;
+            w.gate_proj = make(gu, {(size_t)I, (size_t)H});
+            w.up_proj = make(gu + (size_t)I * H, {(size_t)I, (size_t)H});
+            w.down_proj = make(down + (size_t)l * H * I, {(size_t)H, (size_t)I});
+        }
+        Tensor t_embed = make(embed, {(size_t)V, (size_t)H});
+        Tensor t_norm = make(final_norm, {(size_t)H});
+        Tensor t_head = make(lm_head, {(size_t)V, (size_t)H});
+        q3::KVCache cache(nl, B, Hkv, D, P + n_steps + 1);
+        const int N = P + n_steps;
+        int t0 = 0;
+        for (int call = 0; call <= n_steps; ++call) {
+            const int S = call == 0 ? P : 1;
+            std::vector<long> ids((size_t)B * S);
+            for (int b = 0; b < B; ++b)
+                for (int s = 0; s < S; ++s) ids[(size_t)b * S + s] = tokens[(size_t)b * N + t0 + s];
+            TensorL input(ids, Shape({(size_t)B, (size_t)S}));
+            Tensor out = q3::qwen3_forward_with_cache(input, &cache, t_embed, layers, t_norm, t_head, nl, Hq,
+                                                      Hkv, D, eps, q3::AttentionType::STANDARD);
+            for (int b = 0; b < B; ++b)
+                std::memcpy(logits + ((size_t)call * B + b) * V, out.data() + ((size_t)b * S + S - 1) * V,
+                            (size_t)V * sizeof(float));
+            t0 += S;
+        }
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
 }  // extern "C"

@@ -51,7 +51,14 @@ _I = C.c_int
 _F = C.c_float
 _SZ = C.c_size_t
 
-# name -> (restype, argtypes); mirrors include/sa_amd.h
+class Qwen3Desc(C.Structure):
+    _fields_ = [("num_layers", C.c_int), ("hidden", C.c_int), ("intermediate", C.c_int),
+                ("vocab", C.c_int), ("n_q_heads", C.c_int), ("n_kv_heads", C.c_int),
+                ("head_dim", C.c_int), ("max_pos", C.c_int), ("rms_eps", C.c_float),
+                ("rope_theta", C.c_float)]
+
+
+# name -> (restype, argtypes); mirrors include/sa_amd.h and include/sa_qwen3.h
 SIGNATURES = {
     "sa_last_error": (C.c_char_p, []),
     "sa_stream_attn_ws_bytes": (_SZ, [_I, _I]),
@@ -71,6 +78,7 @@ SIGNATURES = {
     "sa_kvcache_block_table": (_P, [_P]),
     "sa_kvcache_seq_lens": (_P, [_P]),
     "sa_kvcache_bytes": (_SZ, [_P]),
+    "sa_kvcache_get_desc": (_I, [_P, C.POINTER(KvDesc)]),
     "sa_rope_table_init": (_I, [_P, _P, _I, _I, _F, _P]),
     "sa_qknorm_rope_append": (_I, [_P, _I, _P, _P, _P, _I, _I, _P, _I, _P, _P, _F, _P, _P, _I,
                                    _P, _P]),
@@ -80,6 +88,11 @@ SIGNATURES = {
     "sa_kvcache_gather": (_I, [_P, _I, _I, _I, _P, _P, _P]),
     "sa_prefill_causal": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _P]),
     "sa_prefill_causal_strided": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _F, _P, _P]),
+    "sa_qwen3_create": (_I, [C.POINTER(Qwen3Desc), _I, C.POINTER(_P)]),
+    "sa_qwen3_destroy": (_I, [_P]),
+    "sa_qwen3_tensor_ptr": (_I, [_P, _I, _I, C.POINTER(_P), C.POINTER(_SZ), C.POINTER(_I)]),
+    "sa_qwen3_init_random": (_I, [_P, C.c_uint64, _F, _P]),
+    "sa_qwen3_decode_step": (_I, [_P, _P, _P, _I, _P, _P, _P]),
 }
 
 _lib = None
@@ -284,3 +297,91 @@ def prefill_causal(q, k, v, scale: float, out=None, stream=None):
     check(lib().sa_prefill_causal(_ptr(q), _ptr(k), _ptr(v), dt, B, Hq, Hkv, L, D, scale, _ptr(out),
                                   _stream(stream)))
     return out
+
+
+# ---------------------------------------------------------------- Qwen3 decoder
+
+QW_EMBED, QW_IN_NORM, QW_QKV, QW_Q_NORM, QW_K_NORM, QW_O, QW_POST_NORM, QW_GATE_UP, QW_DOWN, \
+    QW_FINAL_NORM, QW_LM_HEAD = range(11)
+QW_GLOBAL = (QW_EMBED, QW_FINAL_NORM, QW_LM_HEAD)
+
+QWEN3_0_6B = dict(num_layers=28, hidden=1024, intermediate=3072, vocab=151936, n_q_heads=16,
+                  n_kv_heads=8, head_dim=128, rms_eps=1e-6, rope_theta=1e6)
+
+
+class Qwen3:
+    """Owner of an sa_qwen3 handle: bf16 weights on the device and the greedy
+    decode step of include/sa_qwen3.h."""
+
+    def __init__(self, max_batch: int, max_pos: int, **shape):
+        d = dict(QWEN3_0_6B)
+        d.update(shape)
+        self.desc = Qwen3Desc(d["num_layers"], d["hidden"], d["intermediate"], d["vocab"],
+                              d["n_q_heads"], d["n_kv_heads"], d["head_dim"], max_pos, d["rms_eps"],
+                              d["rope_theta"])
+        h = C.c_void_p()
+        check(lib().sa_qwen3_create(C.byref(self.desc), max_batch, C.byref(h)))
+        self.handle = h
+        self.max_batch = max_batch
+
+    def close(self) -> None:
+        if self.handle:
+            lib().sa_qwen3_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def tensor_ptr(self, which: int, layer: int = 0):
+        """(device pointer, element count, dtype code) of one weight tensor."""
+        p, n, dt = C.c_void_p(), C.c_size_t(), C.c_int()
+        check(lib().sa_qwen3_tensor_ptr(self.handle, layer, which, C.byref(p), C.byref(n), C.byref(dt)))
+        return p.value, n.value, dt.value
+
+    def tensor(self, which: int, layer: int = 0):
+        """A torch view of one weight tensor (bfloat16 or float32, flat)."""
+        import torch
+        ptr, n, dt = self.tensor_ptr(which, layer)
+        return _device_view(ptr, n, torch.bfloat16 if dt == SA_DTYPE_BF16 else torch.float32)
+
+    def init_random(self, seed: int, std: float = 0.02, stream=None) -> None:
+        check(lib().sa_qwen3_init_random(self.handle, seed, std, _stream(stream)))
+
+    def decode_step(self, cache: "KVCache", tokens, next_tokens=None, logits=None, stream=None):
+        """tokens: int32 CUDA [B] -> next tokens int32 CUDA [B] (and logits if given)."""
+        import torch
+        B = tokens.shape[0]
+        if tokens.dtype != torch.int32 or not tokens.is_cuda:
+            raise ValueError("tokens must be an int32 CUDA tensor")
+        next_tokens = torch.empty_like(tokens) if next_tokens is None else next_tokens
+        check(lib().sa_qwen3_decode_step(self.handle, cache.handle, _ptr(tokens), B, _ptr(next_tokens),
+                                         _ptr(logits), _stream(stream)))
+        return next_tokens
+
+
+class _CudaArray:
+    """__cuda_array_interface__ over memory this library owns (no copy)."""
+
+    def __init__(self, ptr: int, n: int, typestr: str):
+        self.__cuda_array_interface__ = {"shape": (n,), "typestr": typestr, "data": (ptr, False),
+                                         "version": 2, "strides": None}
+
+
+def _device_view(ptr: int, n: int, dtype):
+    import torch
+    if dtype == torch.bfloat16:
+        # torch has no bfloat16 typestr: view the bits as int16
+        return torch.as_tensor(_CudaArray(ptr, n, "<i2"), device="cuda").view(torch.bfloat16)
+    return torch.as_tensor(_CudaArray(ptr, n, "<f4"), device="cuda")
+
+
+def kv_pool_views(cache: "KVCache", layer: int):
+    """Flat torch views of one layer's K and V page pools (storage dtype)."""
+    import torch
+    d = cache.desc
+    n = d.num_pages * d.num_kv_heads * PAGE_TOKENS * d.head_dim
+    dt = torch.bfloat16 if d.kv_dtype == SA_DTYPE_BF16 else torch.float32
+    return _device_view(cache.k_pool(layer), n, dt), _device_view(cache.v_pool(layer), n, dt)

@@ -453,6 +453,13 @@ extern "C" sa_status sa_kvcache_commit(sa_kvcache* c, const int32_t* seqs, int n
     return SA_OK;
 }
 
+extern "C" sa_status sa_kvcache_get_desc(const sa_kvcache* c, sa_kv_desc* out) {
+    clear_error();
+    if (!valid_cache(c) || !out) return fail(SA_EINVAL, "invalid cache or null output");
+    *out = c->desc;
+    return SA_OK;
+}
+
 extern "C" void* sa_kvcache_k_pool(sa_kvcache* c, int layer) {
     if (!valid_cache(c) || layer < 0 || layer >= c->desc.num_layers) return nullptr;
     return k_pool_of(c, layer);

@@ -1,0 +1,548 @@
+// Qwen3 greedy decode step on gfx950: the decoder around the attention path.
+//
+// Reference: qwen3_forward_with_cache and qwen3_decoder_layer_with_cache
+// (tensor_cpp/src/qwen3_ops.cpp:620-1014), qwen3_mlp (:265-296), and the ops
+// they call: embedding (tensor_cpp/src/ops.cpp:278-313), linear (:315-372),
+// rms_norm (:375-417).  The attention block itself runs on
+// sa_qknorm_rope_append + sa_paged_decode.
+//
+// Layout: the batch of B <= 64 token rows stays fp32 in a residual stream
+// x[B][hidden]; every projection is one GEMM Y = X W^T with bf16 weights in
+// nn.Linear layout [out][in] and fp32 accumulation, split over K into
+// fixed-order partial sums when the output is narrow, so results do not
+// depend on scheduling.  Epilogue kernels fold the partial sums into the next
+// step: the q | k | v split, residual add + RMSNorm, SwiGLU.
+#include <math.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "sa_internal.h"
+#include "sa_qwen3.h"
+
+struct sa_qwen3 {
+    struct Layer {
+        float* in_norm;
+        uint16_t* qkv;
+        float* q_norm;
+        float* k_norm;
+        uint16_t* o;
+        float* post_norm;
+        uint16_t* gate_up;
+        uint16_t* down;
+    };
+    sa_qwen3_desc d{};
+    int max_batch = 0;
+    int device = 0;
+    std::vector<void*> allocs;
+    uint16_t* embed = nullptr;
+    uint16_t* lm_head = nullptr;
+    float* final_norm = nullptr;
+    std::vector<Layer> layers;
+    float* rope_cos = nullptr;
+    float* rope_sin = nullptr;
+    // activations for max_batch rows
+    float* x = nullptr;        // residual stream [B][hidden]
+    float* h = nullptr;        // normed input of the next projection [B][hidden]
+    float* q = nullptr;        // [B][Hq D]
+    float* k = nullptr;        // [B][Hkv D]
+    float* v = nullptr;        // [B][Hkv D]
+    float* q_rope = nullptr;   // [B][Hq D]
+    float* attn = nullptr;     // [B][Hq D]
+    float* act = nullptr;      // [B][intermediate]
+    float* part = nullptr;     // split-K partial sums
+    float* logits = nullptr;   // [B][vocab]
+    float* am_val = nullptr;   // argmax partials [B][kArgBlocks]
+    int32_t* am_idx = nullptr;
+    void* ws = nullptr;        // paged decode workspace (grow-only)
+    size_t ws_bytes = 0;
+};
+
+namespace sa {
+namespace {
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kMaxRows = 64;     // batch rows one GEMM tile covers
+constexpr int kGN = 64;          // GEMM output columns per workgroup
+constexpr int kGK = 32;          // GEMM k chunk
+constexpr int kArgBlocks = 64;   // argmax workgroups per row
+
+// ---------------------------------------------------------------------------
+// Synthetic weights: the splitmix64 / Box-Muller generator of the test
+// harness, element i = draw i of (seed, stream).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+    uint64_t z = x + 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ double unit_draw(uint64_t key, uint64_t i) {
+    return (double)((splitmix64(key ^ i) >> 11) + 1) * 0x1.0p-53;
+}
+
+__device__ __forceinline__ float normal_draw(uint64_t key, uint64_t i, double scale) {
+    const double u1 = unit_draw(key, 2 * i), u2 = unit_draw(key, 2 * i + 1);
+    const double z = sqrt(-2.0 * log(u1)) * cos(2.0 * M_PI * u2);
+    return (float)(z * scale);
+}
+
+__global__ void init_bf16_kernel(uint16_t* out, size_t n, uint64_t key, double scale) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = f32_to_bf16_rne(normal_draw(key, i, scale));
+}
+
+__global__ void init_norm_kernel(float* out, size_t n, uint64_t key, double scale) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = 1.0f + normal_draw(key, i, scale);
+}
+
+// ---------------------------------------------------------------------------
+// Row reductions (256 threads)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = group_reduce<OpSum, 1, 64>(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();   // red may still be read by a previous call
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float s = 0.f;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) s += red[w];
+    return s;
+}
+
+// x[m] and h[m] = rms_norm(x[m]) * w, as ops::rms_norm: x / sqrt(mean(x^2) + eps) * w.
+__device__ __forceinline__ void norm_row(const float* xr, int H, const float* w, float eps, float* hr,
+                                         float* red) {
+    float ss = 0.f;
+    for (int j = threadIdx.x; j < H; j += blockDim.x) ss += xr[j] * xr[j];
+    ss = block_sum(ss, red);
+    const float rms = sqrtf(ss / (float)H + eps);
+    for (int j = threadIdx.x; j < H; j += blockDim.x) hr[j] = (xr[j] / rms) * w[j];
+}
+
+// Embedding gather (bf16 -> fp32) and the first layer's input RMSNorm.
+__global__ void __launch_bounds__(256)
+embed_norm_kernel(const uint16_t* embed, const int32_t* tokens, int vocab, int H, const float* w, float eps,
+                  float* x, float* h) {
+    __shared__ float red[4];
+    const int m = blockIdx.x;
+    const int tok = tokens[m];
+    const bool ok = tok >= 0 && tok < vocab;
+    float* xr = x + (size_t)m * H;
+    for (int j = threadIdx.x; j < H; j += blockDim.x) {
+        const uint16_t b = ok ? embed[(size_t)tok * H + j] : (uint16_t)0;
+        xr[j] = __uint_as_float((uint32_t)b << 16);
+    }
+    __syncthreads();
+    norm_row(xr, H, w, eps, h + (size_t)m * H, red);
+}
+
+// ---------------------------------------------------------------------------
+// GEMM: P[s][m][n] = sum over k in split s of X[m][k] * W[n][k].
+// X fp32 [M][K] (M <= 64), W bf16 [N][K]; N % 64 == 0, split % 32 == 0.
+// A workgroup owns all M rows and 64 columns; thread (ty, tx) a 4 x 4 block.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256)
+gemm_xwt_kernel(const float* __restrict__ X, int M, int K, const uint16_t* __restrict__ W, int N, int split,
+                float* __restrict__ P) {
+    __shared__ __align__(16) float Xs[kGK][kMaxRows + 4];
+    __shared__ __align__(16) float Ws[kGK][kGN + 4];
+    const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
+    const int n0 = blockIdx.x * kGN;
+    const int k_begin = blockIdx.y * split;
+    float acc[4][4] = {};
+    for (int k0 = k_begin; k0 < k_begin + split; k0 += kGK) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int idx = tid + i * 256, r = idx >> 3, c = (idx & 7) * 4;
+            float4 xv = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (r < M) xv = *reinterpret_cast<const float4*>(X + (size_t)r * K + k0 + c);
+            Xs[c + 0][r] = xv.x;
+            Xs[c + 1][r] = xv.y;
+            Xs[c + 2][r] = xv.z;
+            Xs[c + 3][r] = xv.w;
+        }
+        {
+            const int nn = tid >> 2, c = (tid & 3) * 8;
+            const u32x4_t wv = *reinterpret_cast<const u32x4_t*>(W + (size_t)(n0 + nn) * K + k0 + c);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                Ws[c + 2 * j][nn] = bf16_lo(wv[j]);
+                Ws[c + 2 * j + 1][nn] = bf16_hi(wv[j]);
+            }
+        }
+        __syncthreads();
+#pragma unroll 8
+        for (int kk = 0; kk < kGK; ++kk) {
+            const float4 a = *reinterpret_cast<const float4*>(&Xs[kk][ty * 4]);
+            const float4 b = *reinterpret_cast<const float4*>(&Ws[kk][tx * 4]);
+            const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(av[i], bv[j], acc[i][j]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = ty * 4 + i;
+        if (m < M)
+            *reinterpret_cast<float4*>(P + ((size_t)blockIdx.y * M + m) * N + n0 + tx * 4) =
+                make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+    }
+}
+
+// Sum of the split-K partials of element (m, n), in split order.
+__device__ __forceinline__ float psum(const float* P, int S, int M, int N, int m, int n) {
+    float s = 0.f;
+    for (int i = 0; i < S; ++i) s += P[((size_t)i * M + m) * N + n];
+    return s;
+}
+
+// q | k | v rows of the fused projection into three token-major buffers.
+__global__ void qkv_split_kernel(const float* P, int S, int M, int Nq, int Nk, float* q, float* k, float* v) {
+    const int m = blockIdx.x, N = Nq + 2 * Nk;
+    for (int n = threadIdx.x; n < N; n += blockDim.x) {
+        const float y = psum(P, S, M, N, m, n);
+        if (n < Nq) q[(size_t)m * Nq + n] = y;
+        else if (n < Nq + Nk) k[(size_t)m * Nk + n - Nq] = y;
+        else v[(size_t)m * Nk + n - Nq - Nk] = y;
+    }
+}
+
+// x[m] += projection output; h[m] = rms_norm(x[m]) * w (the next block's norm).
+__global__ void __launch_bounds__(256)
+residual_norm_kernel(const float* P, int S, int M, int H, float* x, const float* w, float eps, float* h) {
+    __shared__ float red[4];
+    const int m = blockIdx.x;
+    float* xr = x + (size_t)m * H;
+    for (int j = threadIdx.x; j < H; j += blockDim.x) xr[j] += psum(P, S, M, H, m, j);
+    __syncthreads();
+    norm_row(xr, H, w, eps, h + (size_t)m * H, red);
+}
+
+// act[m][i] = silu(gate) * up, silu(g) = g * (1 / (1 + exp(-g))) (qwen3_ops.cpp:287).
+__global__ void swiglu_kernel(const float* P, int S, int M, int I, float* act) {
+    const size_t total = (size_t)M * I;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (size_t)gridDim.x * blockDim.x) {
+        const int m = (int)(e / I), i = (int)(e % I);
+        const float g = psum(P, S, M, 2 * I, m, i);
+        const float u = psum(P, S, M, 2 * I, m, I + i);
+        act[e] = g * (1.0f / (1.0f + expf(-g))) * u;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Greedy argmax over the vocabulary (lowest index among equal maxima).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
+
+__device__ __forceinline__ void block_argmax(float& v, int& idx, float* sv, int* si) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(v, off, 64);
+        const int oi = __shfl_xor(idx, off, 64);
+        if (better(ov, oi, v, idx)) { v = ov; idx = oi; }
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) { sv[wave] = v; si[wave] = idx; }
+    __syncthreads();
+    v = sv[0]; idx = si[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w)
+        if (better(sv[w], si[w], v, idx)) { v = sv[w]; idx = si[w]; }
+}
+
+__global__ void __launch_bounds__(256)
+argmax_partial_kernel(const float* logits, int V, float* pv, int32_t* pi) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const int m = blockIdx.y;
+    const int chunk = (V + gridDim.x - 1) / gridDim.x;
+    const int b0 = blockIdx.x * chunk, b1 = min(V, b0 + chunk);
+    const float* row = logits + (size_t)m * V;
+    float v = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = b0 + threadIdx.x; i < b1; i += blockDim.x)
+        if (better(row[i], i, v, idx)) { v = row[i]; idx = i; }
+    block_argmax(v, idx, sv, si);
+    if (threadIdx.x == 0) { pv[m * gridDim.x + blockIdx.x] = v; pi[m * gridDim.x + blockIdx.x] = idx; }
+}
+
+__global__ void argmax_final_kernel(const float* pv, const int32_t* pi, int nb, int32_t* out) {
+    const int m = blockIdx.x;
+    if (threadIdx.x != 0) return;
+    float v = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int b = 0; b < nb; ++b)
+        if (better(pv[m * nb + b], pi[m * nb + b], v, idx)) { v = pv[m * nb + b]; idx = pi[m * nb + b]; }
+    out[m] = idx == 0x7fffffff ? 0 : idx;
+}
+
+// ---------------------------------------------------------------------------
+// Host helpers
+// ---------------------------------------------------------------------------
+int pick_split(int N, int K, int cus) {
+    const int nb = N / kGN, chunks = K / kGK;
+    int s = 1;
+    while (s * 2 <= 32 && nb * s < 2 * cus && chunks % (s * 2) == 0 && chunks / (s * 2) >= 2) s *= 2;
+    return s;
+}
+
+struct Gemm { int N, K, S; };
+
+sa_status gemm(const float* X, int M, const uint16_t* W, const Gemm& g, float* P, hipStream_t st) {
+    hipLaunchKernelGGL(gemm_xwt_kernel, dim3(g.N / kGN, g.S), dim3(256), 0, st, X, M, g.K, W, g.N, g.K / g.S, P);
+    SA_CHECK_LAUNCH();
+    return SA_OK;
+}
+
+uint64_t stream_key(uint64_t seed, uint32_t stream) {
+    return (seed * 0x9E3779B97F4A7C15ull) ^ ((uint64_t)stream << 32);
+}
+
+}  // namespace
+}  // namespace sa
+
+using namespace sa;
+
+namespace {
+
+struct Shapes {
+    int H, I, V, Hq, Hkv, D, Nq, Nk, Nqkv;
+    Gemm qkv, o, gate_up, down, lm;
+};
+
+Shapes shapes_of(const sa_qwen3_desc& d, int cus) {
+    Shapes s;
+    s.H = d.hidden; s.I = d.intermediate; s.V = d.vocab;
+    s.Hq = d.n_q_heads; s.Hkv = d.n_kv_heads; s.D = d.head_dim;
+    s.Nq = s.Hq * s.D; s.Nk = s.Hkv * s.D; s.Nqkv = s.Nq + 2 * s.Nk;
+    s.qkv = {s.Nqkv, s.H, pick_split(s.Nqkv, s.H, cus)};
+    s.o = {s.H, s.Nq, pick_split(s.H, s.Nq, cus)};
+    s.gate_up = {2 * s.I, s.H, pick_split(2 * s.I, s.H, cus)};
+    s.down = {s.H, s.I, pick_split(s.H, s.I, cus)};
+    s.lm = {s.V, s.H, 1};
+    return s;
+}
+
+template <class T>
+sa_status dev_alloc(sa_qwen3* m, T** p, size_t count) {
+    void* raw = nullptr;
+    const hipError_t e = hipMalloc(&raw, std::max<size_t>(count, 1) * sizeof(T));
+    if (e != hipSuccess) return fail(SA_ENOMEM, std::string("hipMalloc: ") + hipGetErrorString(e));
+    m->allocs.push_back(raw);
+    *p = static_cast<T*>(raw);
+    return SA_OK;
+}
+
+void release(sa_qwen3* m) {
+    for (void* p : m->allocs) (void)hipFree(p);
+    m->allocs.clear();
+    if (m->ws) (void)hipFree(m->ws);
+    m->ws = nullptr;
+}
+
+}  // namespace
+
+#define SA_TRY(expr)                      \
+    do {                                  \
+        sa_status _s = (expr);            \
+        if (_s != SA_OK) return _s;       \
+    } while (0)
+
+extern "C" sa_status sa_qwen3_create(const sa_qwen3_desc* desc, int max_batch, sa_qwen3** out) {
+    clear_error();
+    if (!desc || !out) return fail(SA_EINVAL, "null argument");
+    *out = nullptr;
+    const sa_qwen3_desc& d = *desc;
+    if (d.num_layers <= 0 || d.hidden <= 0 || d.intermediate <= 0 || d.vocab <= 0 || d.n_q_heads <= 0 ||
+        d.n_kv_heads <= 0 || d.n_q_heads % d.n_kv_heads || d.max_pos <= 0)
+        return fail(SA_EINVAL, "bad model shape");
+    if (d.head_dim != 64 && d.head_dim != 128) return fail(SA_EINVAL, "head_dim must be 64 or 128");
+    const int nq = d.n_q_heads * d.head_dim, nqkv = nq + 2 * d.n_kv_heads * d.head_dim;
+    if (d.hidden % kGN || nq % kGN || nqkv % kGN || (2 * d.intermediate) % kGN || d.vocab % kGN ||
+        d.hidden % kGK || nq % kGK || d.intermediate % kGK)
+        return fail(SA_EINVAL, "projection sizes must be multiples of 64 (outputs) and 32 (inputs)");
+    if (max_batch < 1 || max_batch > kMaxRows) return fail(SA_ERANGE, "max_batch must be in [1, 64]");
+    sa_qwen3* m = new sa_qwen3();
+    m->d = d;
+    m->max_batch = max_batch;
+    auto cleanup = [&](sa_status s) {
+        release(m);
+        delete m;
+        return s;
+    };
+    if (hipGetDevice(&m->device) != hipSuccess) return cleanup(fail(SA_EHIP, "hipGetDevice failed"));
+    const Shapes s = shapes_of(d, device_cu_count());
+    const size_t H = s.H, V = s.V, B = max_batch;
+    sa_status st;
+    if ((st = dev_alloc(m, &m->embed, V * H)) != SA_OK) return cleanup(st);
+    if ((st = dev_alloc(m, &m->lm_head, V * H)) != SA_OK) return cleanup(st);
+    if ((st = dev_alloc(m, &m->final_norm, H)) != SA_OK) return cleanup(st);
+    m->layers.resize(d.num_layers);
+    for (auto& L : m->layers) {
+        if ((st = dev_alloc(m, &L.in_norm, H)) != SA_OK) return cleanup(st);
+        if ((st = dev_alloc(m, &L.qkv, (size_t)s.Nqkv * H)) != SA_OK) return cleanup(st);
+        if ((st = dev_alloc(m, &L.q_norm, s.D)) != SA_OK) return cleanup(st);
+        if ((st = dev_alloc(m, &L.k_norm, s.D)) != SA_OK) return cleanup(st);
+        if ((st = dev_alloc(m, &L.o, H * s.Nq)) != SA_OK) return cleanup(st);
+        if ((st = dev_alloc(m, &L.post_norm, H)) != SA_OK) return cleanup(st);
+        if ((st = dev_alloc(m, &L.gate_up, 2 * (size_t)s.I * H)) != SA_OK) return cleanup(st);
+        if ((st = dev_alloc(m, &L.down, H * s.I)) != SA_OK) return cleanup(st);
+    }
+    const size_t half = (size_t)d.max_pos * (d.head_dim / 2);
+    if ((st = dev_alloc(m, &m->rope_cos, half)) != SA_OK) return cleanup(st);
+    if ((st = dev_alloc(m, &m->rope_sin, half)) != SA_OK) return cleanup(st);
+    if ((st = sa_rope_table_init(m->rope_cos, m->rope_sin, d.max_pos, d.head_dim, d.rope_theta, nullptr)) != SA_OK)
+        return cleanup(st);
+    size_t part = 0;
+    for (const Gemm* g : {&s.qkv, &s.o, &s.gate_up, &s.down}) part = std::max(part, (size_t)g->S * B * g->N);
+    if ((st = dev_alloc(m, &m->x, B * H)) != SA_OK || (st = dev_alloc(m, &m->h, B * H)) != SA_OK ||
+        (st = dev_alloc(m, &m->q, B * s.Nq)) != SA_OK || (st = dev_alloc(m, &m->k, B * s.Nk)) != SA_OK ||
+        (st = dev_alloc(m, &m->v, B * s.Nk)) != SA_OK || (st = dev_alloc(m, &m->q_rope, B * s.Nq)) != SA_OK ||
+        (st = dev_alloc(m, &m->attn, B * s.Nq)) != SA_OK || (st = dev_alloc(m, &m->act, B * s.I)) != SA_OK ||
+        (st = dev_alloc(m, &m->part, part)) != SA_OK || (st = dev_alloc(m, &m->logits, B * V)) != SA_OK ||
+        (st = dev_alloc(m, &m->am_val, B * kArgBlocks)) != SA_OK ||
+        (st = dev_alloc(m, &m->am_idx, B * kArgBlocks)) != SA_OK)
+        return cleanup(st);
+    if (hipDeviceSynchronize() != hipSuccess) return cleanup(fail(SA_EHIP, "RoPE table init failed"));
+    *out = m;
+    return SA_OK;
+}
+
+extern "C" sa_status sa_qwen3_destroy(sa_qwen3* m) {
+    clear_error();
+    if (!m) return SA_OK;
+    release(m);
+    delete m;
+    return SA_OK;
+}
+
+extern "C" sa_status sa_qwen3_tensor_ptr(sa_qwen3* m, int layer, sa_qwen3_tensor which, void** ptr, size_t* count,
+                                         sa_dtype* dtype) {
+    clear_error();
+    if (!m || !ptr || !count || !dtype) return fail(SA_EINVAL, "null argument");
+    const Shapes s = shapes_of(m->d, 1);
+    const size_t H = s.H;
+    const bool global = which == SA_QW_EMBED || which == SA_QW_FINAL_NORM || which == SA_QW_LM_HEAD;
+    if (!global && (layer < 0 || layer >= m->d.num_layers)) return fail(SA_ERANGE, "layer out of range");
+    const sa_qwen3::Layer* L = global ? nullptr : &m->layers[layer];
+    switch (which) {
+        case SA_QW_EMBED: *ptr = m->embed; *count = (size_t)s.V * H; *dtype = SA_DTYPE_BF16; break;
+        case SA_QW_LM_HEAD: *ptr = m->lm_head; *count = (size_t)s.V * H; *dtype = SA_DTYPE_BF16; break;
+        case SA_QW_FINAL_NORM: *ptr = m->final_norm; *count = H; *dtype = SA_DTYPE_F32; break;
+        case SA_QW_IN_NORM: *ptr = L->in_norm; *count = H; *dtype = SA_DTYPE_F32; break;
+        case SA_QW_QKV: *ptr = L->qkv; *count = (size_t)s.Nqkv * H; *dtype = SA_DTYPE_BF16; break;
+        case SA_QW_Q_NORM: *ptr = L->q_norm; *count = s.D; *dtype = SA_DTYPE_F32; break;
+        case SA_QW_K_NORM: *ptr = L->k_norm; *count = s.D; *dtype = SA_DTYPE_F32; break;
+        case SA_QW_O: *ptr = L->o; *count = H * s.Nq; *dtype = SA_DTYPE_BF16; break;
+        case SA_QW_POST_NORM: *ptr = L->post_norm; *count = H; *dtype = SA_DTYPE_F32; break;
+        case SA_QW_GATE_UP: *ptr = L->gate_up; *count = 2 * (size_t)s.I * H; *dtype = SA_DTYPE_BF16; break;
+        case SA_QW_DOWN: *ptr = L->down; *count = H * s.I; *dtype = SA_DTYPE_BF16; break;
+        default: return fail(SA_EINVAL, "unknown weight tensor");
+    }
+    return SA_OK;
+}
+
+extern "C" sa_status sa_qwen3_init_random(sa_qwen3* m, uint64_t seed, float stdev, sa_stream_t stream) {
+    clear_error();
+    if (!m) return fail(SA_EINVAL, "null model");
+    hipStream_t st = as_stream(stream);
+    const int grid = 4 * device_cu_count();
+    for (int layer = -1; layer < m->d.num_layers; ++layer) {
+        for (int w = SA_QW_EMBED; w <= SA_QW_LM_HEAD; ++w) {
+            const bool global = w == SA_QW_EMBED || w == SA_QW_FINAL_NORM || w == SA_QW_LM_HEAD;
+            if (global != (layer < 0)) continue;
+            void* p;
+            size_t n;
+            sa_dtype dt;
+            SA_TRY(sa_qwen3_tensor_ptr(m, layer < 0 ? 0 : layer, (sa_qwen3_tensor)w, &p, &n, &dt));
+            const uint32_t stream_id = 1000u + 16u * (uint32_t)(layer < 0 ? 0 : layer) + (uint32_t)w;
+            const uint64_t key = stream_key(seed, stream_id);
+            if (dt == SA_DTYPE_BF16)
+                hipLaunchKernelGGL(init_bf16_kernel, dim3(grid), dim3(256), 0, st, static_cast<uint16_t*>(p), n, key,
+                                   (double)stdev);
+            else
+                hipLaunchKernelGGL(init_norm_kernel, dim3(grid), dim3(256), 0, st, static_cast<float*>(p), n, key,
+                                   (double)stdev);
+            SA_CHECK_LAUNCH();
+        }
+    }
+    return SA_OK;
+}
+
+extern "C" sa_status sa_qwen3_decode_step(sa_qwen3* m, sa_kvcache* cache, const int32_t* tokens, int batch,
+                                          int32_t* next_tokens, float* logits, sa_stream_t stream) {
+    clear_error();
+    if (!m || !cache || !tokens || !next_tokens) return fail(SA_EINVAL, "null argument");
+    if (batch < 1 || batch > m->max_batch) return fail(SA_ERANGE, "batch outside [1, max_batch]");
+    sa_kv_desc kd;
+    SA_TRY(sa_kvcache_get_desc(cache, &kd));
+    const sa_qwen3_desc& d = m->d;
+    if (kd.num_layers != d.num_layers || kd.num_kv_heads != d.n_kv_heads || kd.head_dim != d.head_dim)
+        return fail(SA_EINVAL, "cache geometry does not match the model");
+    if (batch > kd.max_seqs) return fail(SA_ERANGE, "batch exceeds the cache's sequences");
+    for (int i = 0; i < batch; ++i) {
+        const int len = sa_kvcache_len(cache, i);
+        if (len < 0 || len >= d.max_pos) return fail(SA_ERANGE, "position outside the RoPE table");
+    }
+    hipStream_t st = as_stream(stream);
+    const size_t need = sa_paged_decode_ws_bytes(cache, batch, d.n_q_heads);
+    if (need > m->ws_bytes) {
+        if (m->ws) SA_HIP_TRY(hipFree(m->ws));
+        m->ws = nullptr;
+        m->ws_bytes = 0;
+        SA_HIP_TRY(hipMalloc(&m->ws, need));
+        m->ws_bytes = need;
+    }
+    const Shapes s = shapes_of(d, device_cu_count());
+    const int M = batch;
+    const float eps = d.rms_eps;
+    const float scale = 1.0f / sqrtf((float)d.head_dim);
+    float* out_logits = logits ? logits : m->logits;
+
+    hipLaunchKernelGGL(embed_norm_kernel, dim3(M), dim3(256), 0, st, m->embed, tokens, s.V, s.H,
+                       m->layers[0].in_norm, eps, m->x, m->h);
+    SA_CHECK_LAUNCH();
+    const int ew_grid = std::min(4 * device_cu_count(), (M * s.I + 255) / 256);
+    for (int l = 0; l < d.num_layers; ++l) {
+        const sa_qwen3::Layer& L = m->layers[l];
+        // ---- attention block ----
+        SA_TRY(gemm(m->h, M, L.qkv, s.qkv, m->part, st));
+        hipLaunchKernelGGL(qkv_split_kernel, dim3(M), dim3(256), 0, st, m->part, s.qkv.S, M, s.Nq, s.Nk, m->q,
+                           m->k, m->v);
+        SA_CHECK_LAUNCH();
+        SA_TRY(sa_qknorm_rope_append(cache, l, m->q, m->k, m->v, M, 1, nullptr, s.Hq, L.q_norm, L.k_norm, eps,
+                                     m->rope_cos, m->rope_sin, d.max_pos, m->q_rope, stream));
+        SA_TRY(sa_paged_decode(cache, l, m->q_rope, M, nullptr, s.Hq, 1, scale, m->attn, m->ws, m->ws_bytes,
+                               stream));
+        SA_TRY(gemm(m->attn, M, L.o, s.o, m->part, st));
+        hipLaunchKernelGGL(residual_norm_kernel, dim3(M), dim3(256), 0, st, m->part, s.o.S, M, s.H, m->x,
+                           L.post_norm, eps, m->h);
+        SA_CHECK_LAUNCH();
+        // ---- MLP ----
+        SA_TRY(gemm(m->h, M, L.gate_up, s.gate_up, m->part, st));
+        hipLaunchKernelGGL(swiglu_kernel, dim3(ew_grid), dim3(256), 0, st, m->part, s.gate_up.S, M, s.I, m->act);
+        SA_CHECK_LAUNCH();
+        SA_TRY(gemm(m->act, M, L.down, s.down, m->part, st));
+        const float* next_norm = l + 1 < d.num_layers ? m->layers[l + 1].in_norm : m->final_norm;
+        hipLaunchKernelGGL(residual_norm_kernel, dim3(M), dim3(256), 0, st, m->part, s.down.S, M, s.H, m->x,
+                           next_norm, eps, m->h);
+        SA_CHECK_LAUNCH();
+    }
+    // ---- final norm (folded above), lm_head, greedy argmax ----
+    SA_TRY(gemm(m->h, M, m->lm_head, s.lm, out_logits, st));
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgBlocks, M), dim3(256), 0, st, out_logits, s.V, m->am_val,
+                       m->am_idx);
+    SA_CHECK_LAUNCH();
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(M), dim3(64), 0, st, m->am_val, m->am_idx, kArgBlocks,
+                       next_tokens);
+    SA_CHECK_LAUNCH();
+    return sa_kvcache_commit(cache, nullptr, M, 1, stream);
+}

@@ -116,6 +116,14 @@ def main() -> None:
             out["qkv_eff"] = eff
     save("layer", {"prompt": gi.LAYER_PROMPT, "inputs_sha256": digest(ql, kl, vl, wq, wk)}, **out)
 
+    # Whole-model forwards (qwen3_forward_with_cache, STANDARD attention).
+    out, shas = {}, []
+    for i, case in enumerate(gi.MODEL_CASES):
+        w, tokens = gi.model_inputs(case)
+        out[f"logits{i}"] = ref.qwen3_forward(w, case["cfg"], tokens, case["prompt"])
+        shas.append(digest(tokens, w["embed"], w["lm_head"], *[v for L in w["layers"] for v in L.values()]))
+    save("qwen3_forward", {"inputs_sha256": shas}, **out)
+
 
 if __name__ == "__main__":
     main()

@@ -59,6 +59,28 @@ def layer_inputs():
             1 + synth.normal(8, 5, 128, 0.02))
 
 
+# Small whole-model configurations for the decoder oracle (reference
+# qwen3_forward_with_cache): shape, weight seed / std, batch, prompt, steps.
+MODEL_CASES = [
+    dict(cfg=dict(num_layers=2, hidden=64, intermediate=128, vocab=256, n_q_heads=4, n_kv_heads=2,
+                  head_dim=16, rms_eps=1e-6, rope_theta=1e6, max_pos=64),
+         seed=7, std=0.2, batch=2, prompt=5, steps=4),
+    dict(cfg=dict(num_layers=3, hidden=128, intermediate=256, vocab=512, n_q_heads=4, n_kv_heads=4,
+                  head_dim=32, rms_eps=1e-6, rope_theta=1e6, max_pos=64),
+         seed=8, std=0.1, batch=3, prompt=3, steps=5),
+]
+
+
+def model_inputs(case: dict):
+    """(weights, tokens [B][prompt + steps]) of one MODEL_CASES entry."""
+    from oracle.qwen3_model import synth_weights
+    c = case["cfg"]
+    w = synth_weights(synth, c, case["seed"], case["std"])
+    n = case["prompt"] + case["steps"]
+    tokens = ((np.arange(case["batch"] * n).reshape(case["batch"], n) * 37 + case["seed"]) % c["vocab"])
+    return w, tokens.astype(np.int32)
+
+
 def load(name: str):
     import json
     from pathlib import Path

@@ -1,5 +1,5 @@
 """CPU checks of the C ABI: the library loads without a GPU and exports every
-function include/sa_amd.h declares, with the argument counts the Python
+function include/sa_*.h declares, with the argument counts the Python
 binding assumes."""
 from __future__ import annotations
 
@@ -11,11 +11,11 @@ import pytest
 
 from util import load_pkg
 
-HEADER = Path(__file__).resolve().parents[1] / "include" / "sa_amd.h"
+HEADERS = sorted((Path(__file__).resolve().parents[1] / "include").glob("sa_*.h"))
 
 
 def declared_functions():
-    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    text = "\n".join(re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S) for h in HEADERS)
     decls = {}
     for m in re.finditer(r"^\s*[\w\s\*]+?\b(sa_\w+)\s*\(([^;]*?)\)\s*;", text, flags=re.M | re.S):
         args = m.group(2).strip()
@@ -27,7 +27,7 @@ def declared_functions():
 def test_header_declares_entry_points():
     decls = declared_functions()
     for name in ("sa_stream_attn_f32", "sa_decode_dense_f32", "sa_kvcache_create", "sa_qknorm_rope_append",
-                 "sa_paged_decode", "sa_prefill_causal", "sa_last_error"):
+                 "sa_paged_decode", "sa_prefill_causal", "sa_last_error", "sa_qwen3_decode_step"):
         assert name in decls
 
 

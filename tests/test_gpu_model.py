@@ -1,0 +1,177 @@
+"""GPU parity: the whole-model greedy decode step (include/sa_qwen3.h) against
+the CPU decoder oracle (oracle/qwen3_model.py, pinned to the reference's
+qwen3_forward_with_cache by tests/test_oracle.py).
+
+The oracle runs on the model's own weights (read back from the device) and on
+the cache's own contents (gathered), so the comparison isolates the step.
+fp32 KV: logits max-abs <= 1e-4 and relative L2 <= 1e-5 per step, tokens
+identical.  bf16 KV at the Qwen3-0.6B shape: relative L2 <= 2e-2 per step and
+greedy tokens identical over 32 steps.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(num_layers=2, hidden=256, intermediate=512, vocab=1024, n_q_heads=4, n_kv_heads=2,
+             head_dim=64, rms_eps=1e-6, rope_theta=1e6)
+SHAPE_KEYS = ("num_layers", "hidden", "intermediate", "vocab", "n_q_heads", "n_kv_heads", "head_dim",
+              "rms_eps", "rope_theta")
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def host_weights(sa, model, cfg):
+    """The model's weights as the oracle's fp32 dict (exact: bf16 widens exactly)."""
+    from oracle.qwen3_model import TENSORS
+    H, I, V = cfg["hidden"], cfg["intermediate"], cfg["vocab"]
+    Hq, Hkv, D = cfg["n_q_heads"], cfg["n_kv_heads"], cfg["head_dim"]
+    shapes = {sa.QW_EMBED: (V, H), sa.QW_LM_HEAD: (V, H), sa.QW_FINAL_NORM: (H,), sa.QW_IN_NORM: (H,),
+              sa.QW_QKV: ((Hq + 2 * Hkv) * D, H), sa.QW_Q_NORM: (D,), sa.QW_K_NORM: (D,),
+              sa.QW_O: (H, Hq * D), sa.QW_POST_NORM: (H,), sa.QW_GATE_UP: (2 * I, H), sa.QW_DOWN: (H, I)}
+
+    def get(which, layer=0):
+        return model.tensor(which, layer).float().cpu().numpy().reshape(shapes[which])
+
+    ids = dict(zip(TENSORS, (sa.QW_IN_NORM, sa.QW_QKV, sa.QW_Q_NORM, sa.QW_K_NORM, sa.QW_O, sa.QW_POST_NORM,
+                             sa.QW_GATE_UP, sa.QW_DOWN)))
+    return {"embed": get(sa.QW_EMBED), "final_norm": get(sa.QW_FINAL_NORM), "lm_head": get(sa.QW_LM_HEAD),
+            "layers": [{t: get(ids[t], l) for t in TENSORS} for l in range(cfg["num_layers"])]}
+
+
+def make_cache(sa, synth, cfg, lens, steps, kv_dtype, seed):
+    """Pages from a seeded shuffle of the pool, room for `steps` more tokens,
+    committed lengths `lens`, every pool element N(0,1)."""
+    pages_per = [(L + steps + 63) // 64 for L in lens]
+    n_pages = sum(pages_per)
+    cache = sa.KVCache(cfg["num_layers"], cfg["n_kv_heads"], cfg["head_dim"], len(lens), max(pages_per),
+                       n_pages, kv_dtype)
+    perm = synth.permutation(seed, 2, n_pages)
+    off = 0
+    for s, (L, n) in enumerate(zip(lens, pages_per)):
+        cache.set_pages(s, perm[off:off + n])
+        cache.set_len(s, L)
+        off += n
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    for l in range(cfg["num_layers"]):
+        for pool in sa.kv_pool_views(cache, l):
+            pool.normal_(generator=gen)
+    torch.cuda.synchronize()
+    return cache
+
+
+def oracle_store(cache, cfg, lens, steps, kv_bf16):
+    from oracle.qwen3_model import KvStore
+    st = KvStore(cfg["num_layers"], len(lens), cfg["n_kv_heads"], cfg["head_dim"], max(lens) + steps, kv_bf16)
+    for l in range(cfg["num_layers"]):
+        for b, L in enumerate(lens):
+            k, v = cache.gather(l, b, L)
+            st.K[l][b][:, :L] = k.cpu().numpy()
+            st.V[l][b][:, :L] = v.cpu().numpy()
+    st.lens[:] = lens
+    return st
+
+
+def run_parity(sa, oracle, synth, cfg, std, lens, steps, kv_dtype, seed, first_tokens, check):
+    from oracle.qwen3_model import Qwen3Decoder
+    max_pos = max(lens) + steps + 1
+    model = sa.Qwen3(len(lens), max_pos, **{k: cfg[k] for k in SHAPE_KEYS})
+    model.init_random(seed, std)
+    cache = make_cache(sa, synth, cfg, lens, steps, kv_dtype, seed)
+    dec = Qwen3Decoder(host_weights(sa, model, cfg), dict(cfg, max_pos=max_pos), oracle)
+    store = oracle_store(cache, cfg, lens, steps, kv_dtype == sa.SA_DTYPE_BF16)
+    tokens = torch.tensor(first_tokens, dtype=torch.int32, device="cuda")
+    logits = torch.empty(len(lens), cfg["vocab"], dtype=torch.float32, device="cuda")
+    for t in range(steps):
+        want = dec.step(tokens.cpu().numpy(), store)
+        nxt = model.decode_step(cache, tokens, logits=logits)
+        got = logits.cpu().numpy()
+        check(t, got, want)
+        g_tok, w_tok = nxt.cpu().numpy(), want.argmax(-1)
+        for b in np.nonzero(g_tok != w_tok)[0]:
+            top2 = np.sort(want[b])[-2:]
+            raise AssertionError(
+                f"step {t} seq {b}: gpu token {g_tok[b]} (oracle logit {want[b, g_tok[b]]:.6f}, gpu "
+                f"{got[b, g_tok[b]]:.6f}) vs oracle token {w_tok[b]} (oracle {want[b, w_tok[b]]:.6f}, gpu "
+                f"{got[b, w_tok[b]]:.6f}); oracle top-2 gap {top2[1] - top2[0]:.2e}, logits rel-L2 "
+                f"{rel_l2(got, want):.2e}")
+        assert [cache.length(s) for s in range(len(lens))] == [L + t + 1 for L in lens]
+        tokens = nxt
+    cache.close()
+    model.close()
+
+
+def test_model_init_matches_generator(sa, synth):
+    """sa_qwen3_init_random draws what oracle.qwen3_model.synth_weights draws."""
+    from oracle.qwen3_model import synth_weights
+    model = sa.Qwen3(2, 64, **{k: SMALL[k] for k in SHAPE_KEYS})
+    model.init_random(5, 0.1)
+    torch.cuda.synchronize()
+    got = host_weights(sa, model, SMALL)
+    want = synth_weights(synth, SMALL, 5, 0.1)
+    pairs = [(got[t], want[t]) for t in ("embed", "final_norm", "lm_head")]
+    pairs += [(g[t], w[t]) for g, w in zip(got["layers"], want["layers"]) for t in g]
+    for g, w in pairs:
+        # fp64 log/cos may differ by an ulp between device and host libm; after
+        # rounding to fp32 / bf16 that can flip at most a rare element by one ulp
+        diff = g != w
+        assert diff.sum() <= 2
+        if diff.any():
+            assert np.abs(g[diff] - w[diff]).max() <= np.abs(w[diff]).max() * 2 ** -7
+    model.close()
+
+
+def test_model_decode_fp32_kv(sa, oracle, synth):
+    """Small model, fp32 KV, three sequences of different lengths (one of a
+    single token), 8 greedy steps at the fp32 bar."""
+
+    def check(t, got, want):
+        assert np.abs(got - want).max() <= 1e-4, f"step {t}"
+        assert rel_l2(got, want) <= 1e-5, f"step {t}"
+
+    run_parity(sa, oracle, synth, SMALL, 0.1, [70, 130, 1], 8, sa.SA_DTYPE_F32, 31, [5, 17, 900], check)
+
+
+def test_model_decode_qwen3_shape_bf16_kv(sa, oracle, synth):
+    """The Qwen3-0.6B shape (28 layers, 16/8 heads, vocab 151936), bf16 KV on
+    shuffled pages, 4 sequences with lengths in [512, 2048], 32 greedy steps:
+    identical tokens, logits within the bf16-KV tolerance."""
+    lens = [int(x) for x in 512 + (synth.uniform(77, 1, 4) * 1536).astype(np.int64)]
+    cfg = dict(sa.QWEN3_0_6B)
+    worst = []
+
+    def check(t, got, want):
+        worst.append(rel_l2(got, want))
+        assert worst[-1] <= 2e-2, f"step {t}"
+
+    run_parity(sa, oracle, synth, cfg, 0.02, lens, 32, sa.SA_DTYPE_BF16, 41, [11, 222, 3333, 44444], check)
+    print(f"lens {lens}: worst logits rel-L2 {max(worst):.2e}")
+
+
+def test_model_rejects_bad_calls(sa):
+    import ctypes as C
+    model = sa.Qwen3(2, 64, **{k: SMALL[k] for k in SHAPE_KEYS})
+    cache = sa.KVCache(SMALL["num_layers"], SMALL["n_kv_heads"], 128, 2, 2, 4)   # wrong head_dim
+    tok = torch.zeros(2, dtype=torch.int32, device="cuda")
+    with pytest.raises(sa.SaError, match="geometry"):
+        model.decode_step(cache, tok)
+    with pytest.raises(sa.SaError):
+        sa.check(sa.lib().sa_qwen3_decode_step(model.handle, cache.handle, None, 2, None, None, None))
+    big = torch.zeros(3, dtype=torch.int32, device="cuda")
+    good = sa.KVCache(SMALL["num_layers"], SMALL["n_kv_heads"], SMALL["head_dim"], 4, 2, 8)
+    with pytest.raises(sa.SaError, match="batch"):
+        model.decode_step(good, big)
+    d = sa.Qwen3Desc(1, 100, 64, 64, 2, 1, 64, 16, 1e-6, 1e6)   # hidden not a multiple of 64
+    h = C.c_void_p()
+    assert sa.lib().sa_qwen3_create(C.byref(d), 1, C.byref(h)) == sa.SA_EINVAL
+    cache.close()
+    good.close()
+    model.close()

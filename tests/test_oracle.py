@@ -42,6 +42,10 @@ def test_golden_inputs_unchanged():
     assert dg(*gi.decode_inputs()) == meta["inputs_sha256"]
     meta, _ = gi.load("layer")
     assert dg(*gi.layer_inputs()) == meta["inputs_sha256"]
+    meta, _ = gi.load("qwen3_forward")
+    for case, sha in zip(gi.MODEL_CASES, meta["inputs_sha256"]):
+        w, tokens = gi.model_inputs(case)
+        assert dg(tokens, w["embed"], w["lm_head"], *[v for L in w["layers"] for v in L.values()]) == sha
 
 
 def test_oracle_streaming_golden_cfg1(oracle):
@@ -334,3 +338,89 @@ def test_mistake_gqa_head_map_is_caught(oracle):
     kw = np.stack([k[:, h % 2] for h in range(4)], 1)
     vw = np.stack([v[:, h % 2] for h in range(4)], 1)
     assert np.abs(oracle.decode_gqa(q, kw, vw, sc) - g["standard"]).max() > 1e-2
+
+
+# ---------------------------------------------------------------- Qwen3 decoder
+
+def _decode_teacher_forced(oracle, case, w, tokens, mutate=None):
+    """The oracle decoder fed the case's tokens one at a time; logits at the
+    positions the reference golden stores (last prompt token, then each step)."""
+    from oracle.qwen3_model import KvStore, Qwen3Decoder
+    c = case["cfg"]
+    dec = Qwen3Decoder(w, c, oracle)
+    if mutate:
+        mutate(dec)
+    B = tokens.shape[0]
+    kv = KvStore(c["num_layers"], B, c["n_kv_heads"], c["head_dim"], tokens.shape[1])
+    out = []
+    for t in range(tokens.shape[1]):
+        lg = dec.step(tokens[:, t], kv)
+        if t >= case["prompt"] - 1:
+            out.append(lg)
+    return np.stack(out)
+
+
+@pytest.mark.parametrize("i", range(len(gi.MODEL_CASES)))
+def test_oracle_qwen3_decoder_golden(oracle, i):
+    """The oracle's decode step, token by token, equals the reference's
+    qwen3_forward_with_cache (prompt, then single-token steps) golden logits."""
+    case = gi.MODEL_CASES[i]
+    _, g = gi.load("qwen3_forward")
+    w, tokens = gi.model_inputs(case)
+    got = _decode_teacher_forced(oracle, case, w, tokens)
+    want = g[f"logits{i}"]
+    assert np.abs(got - want).max() <= 1e-4
+    assert np.linalg.norm(got - want) / np.linalg.norm(want) <= 1e-5
+    assert (got.argmax(-1) == want.argmax(-1)).all()
+
+
+def test_oracle_qwen3_decoder_matches_reference_random(oracle, ref, synth):
+    """A fresh weight draw, GQA 4:1, against the compiled reference."""
+    from oracle.qwen3_model import synth_weights
+    cfg = dict(num_layers=2, hidden=96, intermediate=160, vocab=300, n_q_heads=8, n_kv_heads=2,
+               head_dim=16, rms_eps=1e-6, rope_theta=1e6, max_pos=64)
+    case = dict(cfg=cfg, prompt=4, steps=6)
+    w = synth_weights(synth, cfg, seed=99, std=0.15)
+    tokens = ((np.arange(2 * 10).reshape(2, 10) * 53 + 11) % cfg["vocab"]).astype(np.int32)
+    want = ref.qwen3_forward(w, cfg, tokens, case["prompt"])
+    got = _decode_teacher_forced(oracle, case, w, tokens)
+    assert np.abs(got - want).max() <= 1e-4
+    assert np.linalg.norm(got - want) / np.linalg.norm(want) <= 1e-5
+
+
+def test_mistake_swapped_gate_up_is_caught(oracle):
+    """silu(up) * gate instead of silu(gate) * up fails the decoder golden."""
+    case = gi.MODEL_CASES[0]
+    _, g = gi.load("qwen3_forward")
+    w, tokens = gi.model_inputs(case)
+    I = case["cfg"]["intermediate"]
+    for L in w["layers"]:
+        L["gate_up"] = np.concatenate([L["gate_up"][I:], L["gate_up"][:I]])
+    got = _decode_teacher_forced(oracle, case, w, tokens)
+    assert np.abs(got - g["logits0"]).max() > 1e-3
+
+
+def test_mistake_rope_position_off_by_one_is_caught(oracle):
+    """Rotating q at position len + 1 while k sits at len fails the golden.
+    (Shifting every position alike would not: RoPE scores depend only on
+    position differences.)"""
+    case = gi.MODEL_CASES[0]
+    _, g = gi.load("qwen3_forward")
+    w, tokens = gi.model_inputs(case)
+    Hq = case["cfg"]["n_q_heads"]
+
+    class ShiftQ:
+        def __init__(self, inner):
+            self.inner = inner
+
+        def __getattr__(self, name):
+            return getattr(self.inner, name)
+
+        def apply_rope(self, x, pos, cos, sin):
+            return self.inner.apply_rope(x, pos + 1 if x.shape[1] == Hq else pos, cos, sin)
+
+    def shift_q(dec):
+        dec.or_ = ShiftQ(dec.or_)
+
+    got = _decode_teacher_forced(oracle, case, w, tokens, mutate=shift_q)
+    assert np.abs(got - g["logits0"]).max() > 1e-3
