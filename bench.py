@@ -235,6 +235,73 @@ def bench_paged_batch(torch, sa, synth, steps: int = 10, bf16: bool = True):
             "gbs": round(total / (ms * 1e-3) / 1e9, 1), "hbm_frac": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def bench_model_decode(torch, sa, synth, steps: int = 128, warmup: int = 2, B: int = 64):
+    """Greedy decode through the whole Qwen3-0.6B-shape model (28 layers,
+    hidden 1024, 16/8 heads, vocab 151936, weights N(0, 0.02) in bf16):
+    B=64 sequences with context lengths U[512, 32768], 64-token pages from a
+    seeded shuffle of the pool, bf16 KV synthesised as N(0,1) (no prefill
+    run).  Timed: `steps` consecutive greedy steps; tok/s = B * steps / wall."""
+    cfg = sa.QWEN3_0_6B
+    NL, HKV, D = cfg["num_layers"], cfg["n_kv_heads"], cfg["head_dim"]
+    lens = batch_lengths(synth, B)
+    pages_per = [(L + warmup + steps + 63) // 64 for L in lens]
+    n_pages = sum(pages_per)
+    cache = sa.KVCache(NL, HKV, D, B, max(pages_per), n_pages, sa.SA_DTYPE_BF16)
+    log(f"[bench] model decode: KV pool {cache.nbytes() / 1e9:.1f} GB, {n_pages} pages")
+    perm = synth.permutation(71, 2, n_pages)
+    off = 0
+    for s, (L, n) in enumerate(zip(lens, pages_per)):
+        cache.set_pages(s, perm[off:off + n])
+        cache.set_len(s, L)
+        off += n
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(71)
+    t0 = time.perf_counter()
+    for l in range(NL):
+        for pool in sa.kv_pool_views(cache, l):
+            pool.normal_(generator=gen)
+    torch.cuda.synchronize()
+    log(f"[bench] model decode: KV synthesised in {time.perf_counter() - t0:.1f} s")
+    model = sa.Qwen3(B, max(lens) + warmup + steps + 1)
+    model.init_random(71, 0.02)
+    tokens = torch.tensor([int(x * cfg["vocab"]) % cfg["vocab"] for x in synth.uniform(71, 3, B)],
+                          dtype=torch.int32, device="cuda")
+    cur = tokens
+    for _ in range(warmup):
+        cur = model.decode_step(cache, cur)
+    torch.cuda.synchronize()
+    for s, L in enumerate(lens):          # the timed steps start from the stated lengths
+        cache.set_len(s, L)
+    cur = tokens
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(steps):
+        cur = model.decode_step(cache, cur)
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_s = ev0.elapsed_time(ev1) * 1e-3
+    # HBM bytes the step cannot avoid: every K/V element of every layer once
+    # (committed tokens plus the new one), the projection weights and lm_head
+    # once, the appended K/V written once.
+    kv_token = NL * HKV * D * 2 * 2
+    kv_bytes = sum((L + t + 1) * kv_token for L in lens for t in range(steps))
+    H, I, V, HQ = cfg["hidden"], cfg["intermediate"], cfg["vocab"], cfg["n_q_heads"]
+    w_layer = 2 * ((HQ + 2 * HKV) * D * H + H * HQ * D + 2 * I * H + H * I)
+    w_bytes = steps * (NL * w_layer + 2 * V * H)
+    total = kv_bytes + w_bytes + steps * B * kv_token
+    cache.close()
+    model.close()
+    gbs = total / wall / 1e9
+    return {"batch": B, "steps": steps, "sum_len": sum(lens), "min_len": min(lens), "max_len": max(lens),
+            "kv": "bf16", "weights": "bf16", "wall_s": round(wall, 4), "gpu_s": round(gpu_s, 4),
+            "ms_per_step": round(wall * 1e3 / steps, 3), "tok_per_s": round(B * steps / wall, 1),
+            "bytes_per_step": int(total / steps), "gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "roofline_tok_per_s": round(B * steps / (total / (HBM_PEAK_GBS * 1e9)), 1)}
+
+
 def bench_prefill(torch, sa, synth, L: int, bf16: bool, steps: int = 5):
     HQ, HKV, D = 16, 8, 128
     dt = torch.bfloat16 if bf16 else torch.float32
@@ -317,6 +384,9 @@ def main() -> int:
             for bf in (True, False):
                 log(f"[bench] causal prefill L={L} {'bf16' if bf else 'fp32'} (config 4)")
                 extra[f"prefill_L{L}_{'bf16' if bf else 'f32'}"] = bench_prefill(torch, sa, synth, L, bf)
+        torch.cuda.empty_cache()
+        log("[bench] 28-layer Qwen3-0.6B-shape greedy decode, 64 sequences, bf16 KV (config 5)")
+        extra["qwen3_model_decode_b64"] = bench_model_decode(torch, sa, synth)
     log("[bench] CPU baseline (reference streaming_attention_omp)")
     cpu = cpu_baseline(Q, K, V, args.cpu_budget)
 

@@ -198,43 +198,88 @@ gemm_xwt_kernel(const float* __restrict__ X, int M, int K, const uint16_t* __res
     }
 }
 
-// Sum of the split-K partials of element (m, n), in split order.
-__device__ __forceinline__ float psum(const float* P, int S, int M, int N, int m, int n) {
-    float s = 0.f;
-    for (int i = 0; i < S; ++i) s += P[((size_t)i * M + m) * N + n];
+// Sum of the split-K partials of elements (m, n .. n+3), in split order; the
+// loads of 8 splits are issued together.
+__device__ __forceinline__ float4 psum4(const float* P, int S, int M, int N, int m, int n) {
+    const size_t split = (size_t)M * N;
+    const float* p = P + (size_t)m * N + n;
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    int i = 0;
+    for (; i + 8 <= S; i += 8) {
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const float4*>(p + (i + u) * split);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) { s.x += v[u].x; s.y += v[u].y; s.z += v[u].z; s.w += v[u].w; }
+    }
+    for (; i < S; ++i) {
+        const float4 v = *reinterpret_cast<const float4*>(p + i * split);
+        s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+    }
     return s;
 }
 
-// q | k | v rows of the fused projection into three token-major buffers.
-__global__ void qkv_split_kernel(const float* P, int S, int M, int Nq, int Nk, float* q, float* k, float* v) {
+// q | k | v columns of the fused projection into three token-major buffers.
+// Grid (M, N / 1024): a workgroup sums 1024 columns of one row.
+__global__ void __launch_bounds__(256)
+qkv_split_kernel(const float* P, int S, int M, int Nq, int Nk, float* q, float* k, float* v) {
     const int m = blockIdx.x, N = Nq + 2 * Nk;
-    for (int n = threadIdx.x; n < N; n += blockDim.x) {
-        const float y = psum(P, S, M, N, m, n);
-        if (n < Nq) q[(size_t)m * Nq + n] = y;
-        else if (n < Nq + Nk) k[(size_t)m * Nk + n - Nq] = y;
-        else v[(size_t)m * Nk + n - Nq - Nk] = y;
-    }
+    const int n = (blockIdx.y * 256 + threadIdx.x) * 4;
+    if (n >= N) return;
+    const float4 y = psum4(P, S, M, N, m, n);
+    // Nq and Nk are multiples of 64, so a group of 4 columns never straddles two outputs
+    float* dst = n < Nq ? q + (size_t)m * Nq + n
+                        : n < Nq + Nk ? k + (size_t)m * Nk + n - Nq : v + (size_t)m * Nk + n - Nq - Nk;
+    *reinterpret_cast<float4*>(dst) = y;
 }
 
 // x[m] += projection output; h[m] = rms_norm(x[m]) * w (the next block's norm).
+// One workgroup per row; H <= 4096 and a multiple of 4.
 __global__ void __launch_bounds__(256)
 residual_norm_kernel(const float* P, int S, int M, int H, float* x, const float* w, float eps, float* h) {
     __shared__ float red[4];
     const int m = blockIdx.x;
     float* xr = x + (size_t)m * H;
-    for (int j = threadIdx.x; j < H; j += blockDim.x) xr[j] += psum(P, S, M, H, m, j);
-    __syncthreads();
-    norm_row(xr, H, w, eps, h + (size_t)m * H, red);
+    float4 xv[4];
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int n = (c * 256 + threadIdx.x) * 4;
+        if (n < H) {
+            const float4 y = psum4(P, S, M, H, m, n);
+            float4 t = *reinterpret_cast<const float4*>(xr + n);
+            t.x += y.x; t.y += y.y; t.z += y.z; t.w += y.w;
+            *reinterpret_cast<float4*>(xr + n) = t;
+            xv[c] = t;
+            ss += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
+        }
+    }
+    ss = block_sum(ss, red);
+    const float rms = sqrtf(ss / (float)H + eps);
+    float* hr = h + (size_t)m * H;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int n = (c * 256 + threadIdx.x) * 4;
+        if (n < H) {
+            const float4 wv = *reinterpret_cast<const float4*>(w + n);
+            *reinterpret_cast<float4*>(hr + n) = make_float4((xv[c].x / rms) * wv.x, (xv[c].y / rms) * wv.y,
+                                                             (xv[c].z / rms) * wv.z, (xv[c].w / rms) * wv.w);
+        }
+    }
 }
 
 // act[m][i] = silu(gate) * up, silu(g) = g * (1 / (1 + exp(-g))) (qwen3_ops.cpp:287).
-__global__ void swiglu_kernel(const float* P, int S, int M, int I, float* act) {
-    const size_t total = (size_t)M * I;
-    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (size_t)gridDim.x * blockDim.x) {
-        const int m = (int)(e / I), i = (int)(e % I);
-        const float g = psum(P, S, M, 2 * I, m, i);
-        const float u = psum(P, S, M, 2 * I, m, I + i);
-        act[e] = g * (1.0f / (1.0f + expf(-g))) * u;
+__global__ void __launch_bounds__(256) swiglu_kernel(const float* P, int S, int M, int I, float* act) {
+    const size_t groups = (size_t)M * (I / 4);
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < groups; e += (size_t)gridDim.x * blockDim.x) {
+        const int m = (int)(e / (I / 4)), i = (int)(e % (I / 4)) * 4;
+        const float4 g = psum4(P, S, M, 2 * I, m, i);
+        const float4 u = psum4(P, S, M, 2 * I, m, I + i);
+        const float gv[4] = {g.x, g.y, g.z, g.w}, uv[4] = {u.x, u.y, u.z, u.w};
+        float r[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r[j] = gv[j] * (1.0f / (1.0f + expf(-gv[j]))) * uv[j];
+        *reinterpret_cast<float4*>(act + (size_t)m * I + i) = make_float4(r[0], r[1], r[2], r[3]);
     }
 }
 
@@ -369,6 +414,7 @@ extern "C" sa_status sa_qwen3_create(const sa_qwen3_desc* desc, int max_batch, s
     if (d.hidden % kGN || nq % kGN || nqkv % kGN || (2 * d.intermediate) % kGN || d.vocab % kGN ||
         d.hidden % kGK || nq % kGK || d.intermediate % kGK)
         return fail(SA_EINVAL, "projection sizes must be multiples of 64 (outputs) and 32 (inputs)");
+    if (d.hidden > 4096) return fail(SA_EINVAL, "hidden must be at most 4096");
     if (max_batch < 1 || max_batch > kMaxRows) return fail(SA_ERANGE, "max_batch must be in [1, 64]");
     sa_qwen3* m = new sa_qwen3();
     m->d = d;
@@ -510,13 +556,13 @@ extern "C" sa_status sa_qwen3_decode_step(sa_qwen3* m, sa_kvcache* cache, const 
     hipLaunchKernelGGL(embed_norm_kernel, dim3(M), dim3(256), 0, st, m->embed, tokens, s.V, s.H,
                        m->layers[0].in_norm, eps, m->x, m->h);
     SA_CHECK_LAUNCH();
-    const int ew_grid = std::min(4 * device_cu_count(), (M * s.I + 255) / 256);
+    const int ew_grid = std::min(4 * device_cu_count(), (M * s.I / 4 + 255) / 256);
     for (int l = 0; l < d.num_layers; ++l) {
         const sa_qwen3::Layer& L = m->layers[l];
         // ---- attention block ----
         SA_TRY(gemm(m->h, M, L.qkv, s.qkv, m->part, st));
-        hipLaunchKernelGGL(qkv_split_kernel, dim3(M), dim3(256), 0, st, m->part, s.qkv.S, M, s.Nq, s.Nk, m->q,
-                           m->k, m->v);
+        hipLaunchKernelGGL(qkv_split_kernel, dim3(M, (s.Nqkv + 1023) / 1024), dim3(256), 0, st, m->part, s.qkv.S,
+                           M, s.Nq, s.Nk, m->q, m->k, m->v);
         SA_CHECK_LAUNCH();
         SA_TRY(sa_qknorm_rope_append(cache, l, m->q, m->k, m->v, M, 1, nullptr, s.Hq, L.q_norm, L.k_norm, eps,
                                      m->rope_cos, m->rope_sin, d.max_pos, m->q_rope, stream));
