@@ -338,7 +338,9 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["headline", "all"], default="all")
+    ap.add_argument("--only", choices=["headline", "all", "single", "layer", "paged", "prefill", "model"],
+                    default="all",
+                    help="headline only, everything, or the headline plus one section")
     ap.add_argument("--T", type=int, default=262144)
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--profile-copy", action="store_true",
@@ -365,7 +367,8 @@ def main() -> int:
     log(f"[bench] headline: {head['gbs']:.1f} GB/s kernel, {head['wall_gbs']:.1f} GB/s wall, "
         f"err {head['max_abs_err']:.2e}")
     extra = {}
-    if args.only == "all":
+    run = (lambda name: True) if args.only == "all" else (lambda name: name == args.only)
+    if run("single"):
         log("[bench] single-head T=1024 (config 1)")
         c1, _ = bench_stream(torch, sa, synth, 1024, 200, 20, min_footprint=1.1e9)
         extra["single_head_T1024"] = {k: c1[k] for k in ("kernel_ms", "gbs", "max_abs_err", "rel_l2_err")}
@@ -376,14 +379,18 @@ def main() -> int:
             extra[f"single_head_T{T}"] = {"kernel_ms": c2["kernel_ms"], "gbs": round(c2["gbs"], 1),
                                           "hbm_frac": round(c2["gbs"] / HBM_PEAK_GBS, 4),
                                           "rel_l2_err": c2["rel_l2_err"]}
+    if run("layer"):
         log("[bench] one-layer Qwen3 decode loop (config 3)")
         extra["qwen3_layer_decode_loop"] = bench_cfg3(torch, sa, synth)
+    if run("paged"):
         log("[bench] batched paged GQA decode, 64 sequences, bf16 KV (config 5 attention)")
         extra["paged_decode_b64_bf16"] = bench_paged_batch(torch, sa, synth)
+    if run("prefill"):
         for L in (1024, 8192):
             for bf in (True, False):
                 log(f"[bench] causal prefill L={L} {'bf16' if bf else 'fp32'} (config 4)")
                 extra[f"prefill_L{L}_{'bf16' if bf else 'f32'}"] = bench_prefill(torch, sa, synth, L, bf)
+    if run("model"):
         torch.cuda.empty_cache()
         log("[bench] 28-layer Qwen3-0.6B-shape greedy decode, 64 sequences, bf16 KV (config 5)")
         extra["qwen3_model_decode_b64"] = bench_model_decode(torch, sa, synth)

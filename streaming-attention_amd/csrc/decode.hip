@@ -281,19 +281,19 @@ split_kv_decode_kernel(DecodeArgs a) {
     const int first = t_begin + wave * TILE;
     const int n_tiles = first < t_end ? (t_end - first + STRIDE - 1) / STRIDE : 0;   // wave-uniform
     if (n_tiles > 0) {
-        const int last = first + (n_tiles - 1) * STRIDE;
         if constexpr (kPrefetch) {
             // Two register tiles, alternating: the loads of tile i+1 are issued
-            // before tile i is reduced.  Past the end a load re-reads the
-            // wave's last tile (a cache hit) instead of branching.
+            // before tile i is reduced.  The conditions are wave-uniform
+            // (scalar branches); no tile is loaded twice (a repeated
+            // non-temporal load misses the cache and costs HBM bytes).
             TileRegs<G::R> ra, rb;
             walk.load(first, ra);
             for (int i = 0; i < n_tiles; i += 2) {
                 const int ta = first + i * STRIDE;
-                walk.load(min(ta + STRIDE, last), rb);
+                if (i + 1 < n_tiles) walk.load(ta + STRIDE, rb);
                 consume<D, NREP, BF16>(ra, t_end - ta, grp, qv, m, l, o);
                 if (i + 1 >= n_tiles) break;
-                walk.load(min(ta + 2 * STRIDE, last), ra);
+                if (i + 2 < n_tiles) walk.load(ta + 2 * STRIDE, ra);
                 consume<D, NREP, BF16>(rb, t_end - ta - STRIDE, grp, qv, m, l, o);
             }
         } else {
