@@ -145,17 +145,26 @@ embed_norm_kernel(const uint16_t* embed, const int32_t* tokens, int vocab, int H
 // ---------------------------------------------------------------------------
 // GEMM: P[s][m][n] = sum over k in split s of X[m][k] * W[n][k].
 // X fp32 [M][K] (M <= 64), W bf16 [N][K]; N % 64 == 0, split % 32 == 0.
-// A workgroup owns all M rows and 64 columns; thread (ty, tx) a 4 x 4 block.
+// A workgroup owns all 64 rows (rows past M read as zero) and 64 columns;
+// wave w computes the 32 x 32 block (rows 32 (w / 2), columns 32 (w % 2))
+// with v_mfma_f32_32x32x2f32: exact fp32 products of the activations and the
+// widened bf16 weights, fp32 accumulation.  32-wide k chunks go through LDS
+// k-major, so lane l's operands X[m = l % 32][k] and W[n = l % 32][k] for
+// k = l / 32 are consecutive words across lanes.
 // ---------------------------------------------------------------------------
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
 __global__ void __launch_bounds__(256)
 gemm_xwt_kernel(const float* __restrict__ X, int M, int K, const uint16_t* __restrict__ W, int N, int split,
                 float* __restrict__ P) {
     __shared__ __align__(16) float Xs[kGK][kMaxRows + 4];
     __shared__ __align__(16) float Ws[kGK][kGN + 4];
-    const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int mb = (wave >> 1) * 32, nb = (wave & 1) * 32;
+    const int row = lane & 31, kh = lane >> 5;
     const int n0 = blockIdx.x * kGN;
     const int k_begin = blockIdx.y * split;
-    float acc[4][4] = {};
+    f32x16_t acc = {};
     for (int k0 = k_begin; k0 < k_begin + split; k0 += kGK) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -177,24 +186,17 @@ gemm_xwt_kernel(const float* __restrict__ X, int M, int K, const uint16_t* __res
             }
         }
         __syncthreads();
-#pragma unroll 8
-        for (int kk = 0; kk < kGK; ++kk) {
-            const float4 a = *reinterpret_cast<const float4*>(&Xs[kk][ty * 4]);
-            const float4 b = *reinterpret_cast<const float4*>(&Ws[kk][tx * 4]);
-            const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(av[i], bv[j], acc[i][j]);
-        }
+        for (int kk = 0; kk < kGK; kk += 2)
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(Xs[kk + kh][mb + row], Ws[kk + kh][nb + row], acc, 0, 0, 0);
         __syncthreads();
     }
+    // element j of acc: row mb + 8 (j / 4) + 4 kh + j % 4, column nb + row
+    float* out = P + (size_t)blockIdx.y * M * N + n0 + nb + row;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int m = ty * 4 + i;
-        if (m < M)
-            *reinterpret_cast<float4*>(P + ((size_t)blockIdx.y * M + m) * N + n0 + tx * 4) =
-                make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+    for (int j = 0; j < 16; ++j) {
+        const int m = mb + 8 * (j >> 2) + 4 * kh + (j & 3);
+        if (m < M) out[(size_t)m * N] = acc[j];
     }
 }
 
