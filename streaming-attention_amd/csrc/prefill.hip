@@ -13,15 +13,18 @@
 // with c = scale * log2(e).  Tiles entirely above the diagonal are never
 // computed; only the tile that crosses a wave's diagonal applies the mask.
 //
-// bf16 inputs (v_mfma_f32_32x32x16_bf16, fp32 accumulation): a wave owns 64
-// queries as two 32-query blocks, a workgroup of 4 waves 256 queries.  The
-// running max is raised lazily: a wave rescales its accumulators only when
-// some score exceeds the current max by more than 2^8, so p stays below 256
-// and the common tile does no rescale at all.  P is rounded to bf16 for the
-// PV product; the row sums use the fp32 p.
+// bf16 inputs (v_mfma_f32_32x32x16_bf16, fp32 accumulation): a wave owns 32
+// queries; a workgroup of 8 waves serves the query heads of one KV group
+// (GQA 2: 4 waves x 32 queries for each of the two heads), so every K/V tile
+// staged in LDS feeds all of them.  The running max is raised lazily: a wave
+// rescales its accumulators only when some score exceeds the current max by
+// more than 2^8, and then after the PV product (exact), so the common tile
+// has no branch between softmax and PV.  P is rounded to bf16 for the PV
+// product; the row sums use the fp32 p.
 //
 // fp32 inputs (v_mfma_f32_16x16x4f32): a wave owns 32 queries as two
 // 16-query blocks, a workgroup 128 queries, eager rescale.
+#include <numeric>
 #include <type_traits>
 
 #include "sa_internal.h"
@@ -52,30 +55,33 @@ struct PrefillArgs {
     int Hq, Hkv, L;
     int n_qt;           // query tiles per head
     int xcd_groups;     // KV groups per XCD when the grid maps groups to XCDs, else 0
+    int gh;             // query heads per workgroup (divides Hq / Hkv)
     float sl2;          // |scale| * log2(e)
     uint32_t q_sign;    // 0x80008000 to negate bf16 q pairs (negative scale), else 0
     float scale;        // signed scale (fp32 kernel)
 };
 
 // Work mapping shared by both kernels.  A KV group is one (batch, kv head);
-// its G = Hq/Hkv query heads read the same K/V.  When the number of groups is
-// a multiple of 8, hardware workgroup i (dispatched to XCD i % 8) takes work
-// slot i / 8 of the groups owned by that XCD, so each XCD's L2 holds the K/V
-// of its own groups only.  Inside an XCD (or the whole grid otherwise) slots
-// run heaviest query tile first, which balances the causal triangle.
-struct Work { int b, h, kvh, qt; };
+// its G = Hq/Hkv query heads read the same K/V, and a workgroup serves gh of
+// them (so G/gh workgroups share each query tile).  When the number of groups
+// is a multiple of 8, hardware workgroup i (dispatched to XCD i % 8) takes
+// work slot i / 8 of the groups owned by that XCD, so each XCD's L2 holds the
+// K/V of its own groups only.  Inside an XCD (or the whole grid otherwise)
+// slots run heaviest query tile first, which balances the causal triangle.
+struct Work { int b, h0, kvh, qt; };
 __device__ __forceinline__ Work map_work(const PrefillArgs& pa, int i) {
     const int G = pa.Hq / pa.Hkv;
-    int x = 0, j = i, span = gridDim.x / (G * pa.n_qt);   // groups in this slot range
+    const int HS = G / pa.gh;                         // head sets per group
+    int x = 0, j = i, span = gridDim.x / (HS * pa.n_qt);   // groups in this slot range
     if (pa.xcd_groups) { x = i & 7; j = i >> 3; span = pa.xcd_groups; }
-    const int per_qt = span * G;
+    const int per_qt = span * HS;
     Work w;
     w.qt = pa.n_qt - 1 - j / per_qt;
     const int rem = j % per_qt;
-    const int group = x * span + rem / G;
+    const int group = x * span + rem / HS;
     w.b = group / pa.Hkv;
     w.kvh = group % pa.Hkv;
-    w.h = w.kvh * G + rem % G;
+    w.h0 = w.kvh * G + (rem % HS) * pa.gh;
     return w;
 }
 
@@ -85,6 +91,7 @@ __device__ __forceinline__ Work map_work(const PrefillArgs& pa, int i) {
 // A wave owns QB 32-query blocks; a workgroup of W waves owns W * QB * 32
 // queries and streams 64-key K/V tiles through two LDS stages.
 constexpr float kLazyRescale = 8.f;              // log2 headroom before a rescale
+constexpr float kHugeExcess = 64.f;              // beyond this the softmax waits for the rescale
 
 template <int D, int W>
 struct BfLds {
@@ -208,7 +215,6 @@ prefill_bf16_kernel(PrefillArgs pa) {
     constexpr int NKS = D / 16;     // k-steps of the score product
     constexpr int NDB = D / 32;     // 32-row d blocks of O^T
     constexpr int QWAVE = 32 * QB;  // queries per wave
-    constexpr int QTILE = W * QWAVE;
     extern __shared__ __align__(16) unsigned char smem[];
     uint16_t* stage_base = reinterpret_cast<uint16_t*>(smem);
 
@@ -220,21 +226,28 @@ prefill_bf16_kernel(PrefillArgs pa) {
     const int hh = lane >> 5;       // lane half
     const float sl2 = pa.sl2;
 
-    const uint16_t* Q = static_cast<const uint16_t*>(pa.q) + wk.b * pa.qs[0] + wk.h * pa.qs[1];
+    // The workgroup's gh query heads share every K/V tile: W / gh waves per
+    // head, each wave QWAVE consecutive queries of its head.
+    const int wph = W / pa.gh;
+    const int qtile = wph * QWAVE;                   // query positions per workgroup
+    const int h = wk.h0 + wave / wph;
+    const uint16_t* Q = static_cast<const uint16_t*>(pa.q) + wk.b * pa.qs[0] + h * pa.qs[1];
     const uint16_t* K = static_cast<const uint16_t*>(pa.k) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
     const uint16_t* V = static_cast<const uint16_t*>(pa.v) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
     const int kv_row = static_cast<int>(pa.kvs[2]);
 
-    const int q_wave0 = wk.qt * QTILE + wave * QWAVE;
-    const int n_kt = (min(L, (wk.qt + 1) * QTILE) - 1) / kKTile + 1;
+    const int q_wave0 = wk.qt * qtile + (wave % wph) * QWAVE;
+    const int n_kt = (min(L, (wk.qt + 1) * qtile) - 1) / kKTile + 1;
     // Tiles this wave computes: keys up to its last query.  The last one is
     // the diagonal tile; dq is the wave's first query relative to it.
     const int wave_kt = q_wave0 < L ? (q_wave0 + QWAVE - 1) / kKTile + 1 : 0;
     const int dq = q_wave0 - (wave_kt - 1) * kKTile;
 
     const BfLoadMap<D, W> mp;
-    BfStage<D, W> next;
-    bf_load<D, W>(next, mp, K, V, kv_row, 0, L);
+    // Tile registers: tile kt+1 waits in one set while tile kt+2 is in flight
+    // in the other, so a tile's global loads have two tiles of compute to land.
+    BfStage<D, W> ra, rb;
+    bf_load<D, W>(ra, mp, K, V, kv_row, 0, L);
 
     // Q^T fragments (B operand): lane holds q[n][16 ks + 8 hh .. + 7].
     bf16x8_t qf[QB][NKS];
@@ -264,120 +277,135 @@ prefill_bf16_kernel(PrefillArgs pa) {
     const int k_off = swap_bits23(n) * Lds::K_STRIDE + 8 * hh;
     const int v_off = Lds::K_ELEMS + n * Lds::V_STRIDE + 8 * hh;
 
-    bf_store<D, W>(next, mp, stage_base, stage_base + Lds::K_ELEMS);
+    bf_store<D, W>(ra, mp, stage_base, stage_base + Lds::K_ELEMS);
+    bf_load<D, W>(rb, mp, K, V, kv_row, kKTile, L);
+    bf_load<D, W>(ra, mp, K, V, kv_row, 2 * kKTile, L);
     __syncthreads();
 
-    for (int kt = 0; kt < n_kt; ++kt) {
+    // One iteration: compute tile kt from LDS stage kt & 1, move tile kt+1
+    // (held) into the other stage, and issue tile kt+3's loads into held.
+    // Past the last tile the loads read clamped, in-range rows into stages
+    // nobody reads.
+    auto step = [&](int kt, BfStage<D, W>& held) {
         const uint16_t* sK = stage_base + (kt & 1) * Lds::STAGE;
-        // Next tile's loads fly during this tile's MFMAs.  Past the last tile
-        // they read clamped, in-range rows into a stage nobody reads.
-        bf_load<D, W>(next, mp, K, V, kv_row, (kt + 1) * kKTile, L);
 
-        // One tile, as two 32-key halves kb.  Per half: the K fragments are
-        // read up front, the score MFMAs of all query blocks share them; the
-        // V fragments are issued next so their latency hides behind the
-        // softmax; the softmax assumes the running max holds and a rare fix-up
-        // handles a raised max; then the PV MFMAs.  DIAG instantiates the
-        // diagonal tile's mask.
+        // One tile, as two 32-key halves kb.  Per half, for each query block
+        // qb: scores, a softmax relative to the current running max m, the PV
+        // product.  A raised max is applied after the PV product: with
+        // p' = 2^(s c - m) and a = 2^(m - m_new), a O + PV(p' a) = a (O + PV(p')),
+        // exact as long as p' stays finite, so the common path has no branch
+        // between softmax and PV and the softmax of block 0 overlaps the score
+        // MFMAs of block 1, the softmax of block 1 the PV MFMAs of block 0.
+        // Only an excess above 2^kHugeExcess (a wave's first tile, in practice)
+        // rescales before the softmax.  DIAG instantiates the diagonal mask.
         auto tile = [&](auto diag_tag) {
             constexpr bool DIAG = decltype(diag_tag)::value;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
-                // ---- S^T = K Q^T for keys 32 kb .. 32 kb + 31 ----
                 bf16x8_t kf[NKS];
 #pragma unroll
                 for (int ks = 0; ks < NKS; ++ks) kf[ks] = lds_b128(sK + k_off + kb * 32 * Lds::K_STRIDE + ks * 16);
-                f32x16_t s[QB];
-#pragma unroll
-                for (int qb = 0; qb < QB; ++qb) s[qb] = f32x16_t{};
-#pragma unroll
-                for (int ks = 0; ks < NKS; ++ks)
-#pragma unroll
-                    for (int qb = 0; qb < QB; ++qb)
-                        s[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qf[qb][ks], s[qb], 0, 0, 0);
-                bf16x8_t vf[NDB][2];
-#pragma unroll
-                for (int db = 0; db < NDB; ++db)
-#pragma unroll
-                    for (int t = 0; t < 2; ++t)
-                        vf[db][t] = lds_b128(sK + v_off + db * 32 * Lds::V_STRIDE + kb * 32 + t * 16);
-
-                // Element j of s[qb] is key kt*64 + 32 kb + 16 (j/8) + 8 hh + j%8
+                // Element j of a score block is key kt*64 + 32 kb + 16 (j/8) + 8 hh + j%8
                 // for query q_wave0 + 32 qb + n.  On the diagonal tile keys past
                 // the query are removed (query - kt*64 = dq + 32 qb + n).
                 auto masked = [&](int qb, int j) {
                     return DIAG && 32 * kb + 16 * (j / 8) + 8 * hh + (j % 8) > dq + 32 * qb + n;
                 };
-                float mt[QB];
+                auto scores = [&](int qb) {
+                    f32x16_t sc = {};
 #pragma unroll
-                for (int qb = 0; qb < QB; ++qb) {
+                    for (int ks = 0; ks < NKS; ++ks)
+                        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qf[qb][ks], sc, 0, 0, 0);
                     if constexpr (DIAG) {
 #pragma unroll
                         for (int j = 0; j < 16; ++j)
-                            if (masked(qb, j)) s[qb][j] = -INFINITY;
+                            if (masked(qb, j)) sc[j] = -INFINITY;
                     }
-                    mt[qb] = s[qb][0];
+                    return sc;
+                };
+                auto row_max = [&](const f32x16_t& sc) {
+                    float mt = sc[0];
 #pragma unroll
-                    for (int j = 1; j < 16; ++j) mt[qb] = fmaxf(mt[qb], s[qb][j]);
-                }
-                bf16x8_t pb[QB][2];
-                float rs[QB];
-                auto softmax = [&](int qb) {
+                    for (int j = 1; j < 16; ++j) mt = fmaxf(mt, sc[j]);
+                    return mt;
+                };
+                // Raise m to this half's exact row max (both lane halves agree)
+                // and scale what was accumulated; returns the scale factor.
+                auto raise = [&](int qb, float mt) {
+                    const float mq = fmaxf(mt, __shfl_xor(mt, 32, 64));
+                    const float m_new = fmaxf(ms[qb], mq * sl2);
+                    const float alpha = ms[qb] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms[qb] - m_new);
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db) acc[qb][db] *= alpha;
+                    lp[qb] *= alpha;
+                    ms[qb] = m_new;
+                };
+                auto softmax = [&](int qb, const f32x16_t& sc, bf16x8_t (&pb)[2]) {
                     const float nm = -ms[qb];
                     float p[16];
-                    rs[qb] = 0.f;
+                    float rs = 0.f;
 #pragma unroll
                     for (int j = 0; j < 16; ++j) {
-                        p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][j], sl2, nm));
+                        p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[j], sl2, nm));
                         if (masked(qb, j)) p[j] = 0.f;   // exact zero also for a zero scale
-                        rs[qb] += p[j];
+                        rs += p[j];
                     }
+                    lp[qb] += rs;
 #pragma unroll
                     for (int t = 0; t < 2; ++t) {
                         const bf16x2_t p01 = __builtin_convertvector(f32x2_t{p[8 * t + 0], p[8 * t + 1]}, bf16x2_t);
                         const bf16x2_t p23 = __builtin_convertvector(f32x2_t{p[8 * t + 2], p[8 * t + 3]}, bf16x2_t);
                         const bf16x2_t p45 = __builtin_convertvector(f32x2_t{p[8 * t + 4], p[8 * t + 5]}, bf16x2_t);
                         const bf16x2_t p67 = __builtin_convertvector(f32x2_t{p[8 * t + 6], p[8 * t + 7]}, bf16x2_t);
-                        pb[qb][t] = __builtin_bit_cast(
+                        pb[t] = __builtin_bit_cast(
                             bf16x8_t, make_uint4(__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23),
                                                  __builtin_bit_cast(uint32_t, p45), __builtin_bit_cast(uint32_t, p67)));
                     }
                 };
-                bool up = false;
+                f32x16_t s[QB];
+                float mt[QB];
+                bf16x8_t pb[QB][2];
+                bf16x8_t vf[NDB][2];
+                auto load_v = [&]() {
 #pragma unroll
-                for (int qb = 0; qb < QB; ++qb) {
-                    softmax(qb);
-                    // Keep the common-case softmax ahead of the branch (the
-                    // compiler would otherwise sink it into the no-rescale path).
-                    asm volatile("" : "+v"(pb[qb][0]), "+v"(pb[qb][1]), "+v"(rs[qb]));
-                    up = up || mt[qb] * sl2 > ms[qb] + kLazyRescale;
-                }
-                if (__any(up)) {
-                    // Raise the max to the exact row max of this half (both
-                    // lane halves agree), rescale, redo the softmax.
+                    for (int db = 0; db < NDB; ++db)
 #pragma unroll
-                    for (int qb = 0; qb < QB; ++qb) {
-                        const float mq = fmaxf(mt[qb], __shfl_xor(mt[qb], 32, 64));
-                        const float m_new = fmaxf(ms[qb], mq * sl2);
-                        const float alpha = ms[qb] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms[qb] - m_new);
+                        for (int t = 0; t < 2; ++t)
+                            vf[db][t] = lds_b128(sK + v_off + db * 32 * Lds::V_STRIDE + kb * 32 + t * 16);
+                };
+                // ---- O^T += V^T P^T over these 32 keys ----
+                auto pv = [&](int qb) {
 #pragma unroll
-                        for (int db = 0; db < NDB; ++db) acc[qb][db] *= alpha;
-                        lp[qb] *= alpha;
-                        ms[qb] = m_new;
-                        softmax(qb);
-                    }
-                }
+                    for (int db = 0; db < NDB; ++db)
 #pragma unroll
-                for (int qb = 0; qb < QB; ++qb) lp[qb] += rs[qb];
-                // ---- O^T += V^T P^T over the same 32 keys ----
-#pragma unroll
-                for (int db = 0; db < NDB; ++db)
-#pragma unroll
-                    for (int t = 0; t < 2; ++t)
-#pragma unroll
-                        for (int qb = 0; qb < QB; ++qb)
+                        for (int t = 0; t < 2; ++t)
                             acc[qb][db] =
                                 __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][t], pb[qb][t], acc[qb][db], 0, 0, 0);
+                };
+                // Two waves share each SIMD; a wave raises its priority while it
+                // issues MFMAs, so the other wave's softmax fills the VALU.
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb) {
+                    __builtin_amdgcn_s_setprio(1);
+                    s[qb] = scores(qb);
+                    __builtin_amdgcn_s_setprio(0);
+                    mt[qb] = row_max(s[qb]);
+                    if (__any(mt[qb] * sl2 > ms[qb] + kHugeExcess)) raise(qb, mt[qb]);
+                    softmax(qb, s[qb], pb[qb]);
+                }
+                load_v();
+                __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb) pv(qb);
+                __builtin_amdgcn_s_setprio(0);
+                // A max that rose by more than 2^kLazyRescale: rescale now (after PV, exact).
+                bool up = false;
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb) up = up || mt[qb] * sl2 > ms[qb] + kLazyRescale;
+                if (__any(up)) {
+#pragma unroll
+                    for (int qb = 0; qb < QB; ++qb) raise(qb, mt[qb]);
+                }
             }
         };
         if (kt + 1 < wave_kt) tile(std::false_type{});
@@ -386,8 +414,13 @@ prefill_bf16_kernel(PrefillArgs pa) {
         // The other stage was last read before the barrier that ended the
         // previous iteration.
         uint16_t* nK = stage_base + ((kt + 1) & 1) * Lds::STAGE;
-        bf_store<D, W>(next, mp, nK, nK + Lds::K_ELEMS);
+        bf_store<D, W>(held, mp, nK, nK + Lds::K_ELEMS);
+        bf_load<D, W>(held, mp, K, V, kv_row, (kt + 3) * kKTile, L);
         __syncthreads();
+    };
+    for (int kt = 0; kt < n_kt; kt += 2) {
+        step(kt, rb);
+        if (kt + 1 < n_kt) step(kt + 1, ra);
     }
 
     // ---- normalise and store: element j of acc[qb][db] is
@@ -398,7 +431,7 @@ prefill_bf16_kernel(PrefillArgs pa) {
         const int qi = q_wave0 + qb * 32 + n;
         if (qi >= L) continue;
         const float inv = 1.0f / l;
-        float* orow = pa.out + wk.b * pa.os[0] + wk.h * pa.os[1] + qi * pa.os[2] + 4 * hh;
+        float* orow = pa.out + wk.b * pa.os[0] + h * pa.os[1] + qi * pa.os[2] + 4 * hh;
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -486,7 +519,7 @@ prefill_f32_kernel(PrefillArgs pa) {
     const int g = lane >> 4;                   // lane group 0..3
     const int c16 = lane & 15;
 
-    const float* Q = static_cast<const float*>(pa.q) + wk.b * pa.qs[0] + wk.h * pa.qs[1];
+    const float* Q = static_cast<const float*>(pa.q) + wk.b * pa.qs[0] + wk.h0 * pa.qs[1];
     const float* K = static_cast<const float*>(pa.k) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
     const float* V = static_cast<const float*>(pa.v) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
     const long long q_row = pa.qs[2], kv_row = pa.kvs[2];
@@ -601,7 +634,7 @@ prefill_f32_kernel(PrefillArgs pa) {
         const int qi = q_wave0 + gq * 16 + c16;
         if (qi >= L) continue;
         const float inv = 1.0f / l_run[gq];
-        float* orow = pa.out + wk.b * pa.os[0] + wk.h * pa.os[1] + qi * pa.os[2];
+        float* orow = pa.out + wk.b * pa.os[0] + wk.h0 * pa.os[1] + qi * pa.os[2];
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
             float4 o4 = make_float4(acc[gq][db][0] * inv, acc[gq][db][1] * inv, acc[gq][db][2] * inv,
@@ -629,11 +662,13 @@ sa_status opt_in_lds(Kernel* kernel, int bytes) {
     return SA_OK;
 }
 
-// bf16 shape: W waves of QB 32-query blocks each.  Measured at L = 8192 on
-// MI355X: 4 waves x 64 queries (one wave per SIMD) 0.383 ms, 8 waves x 32
-// queries (two per SIMD) 0.414 ms.
-constexpr int kBfQB = 2;
-constexpr int kBfW = 4;
+// bf16 shape: W waves of QB 32-query blocks each.  Measured at L = 8192
+// (16/8 heads) on MI355X: 8 waves x 32 queries (two waves per SIMD, MFMA
+// phases at raised priority, both query heads of a KV group per workgroup)
+// 0.355 ms; 4 waves x 64 queries (one wave per SIMD, softmax of one block
+// hand-interleaved with the other block's MFMAs) 0.365 ms.
+constexpr int kBfQB = 1;
+constexpr int kBfW = 8;
 
 template <int D, int QB, int W>
 sa_status launch_bf16(const PrefillArgs& pa, dim3 grid, hipStream_t st) {
@@ -645,11 +680,13 @@ sa_status launch_bf16(const PrefillArgs& pa, dim3 grid, hipStream_t st) {
 }
 
 sa_status launch(PrefillArgs pa, int B, bool bf16, int D, hipStream_t st) {
-    const int q_tile = bf16 ? kBfW * kBfQB * 32 : kFQTile;
+    // bf16: the workgroup's waves split over gh query heads of one KV group.
+    pa.gh = bf16 ? std::gcd(pa.Hq / pa.Hkv, kBfW) : 1;
+    const int q_tile = bf16 ? (kBfW / pa.gh) * kBfQB * 32 : kFQTile;
     pa.n_qt = (pa.L + q_tile - 1) / q_tile;
     const int groups = B * pa.Hkv;
     pa.xcd_groups = groups % 8 == 0 ? groups / 8 : 0;
-    const long long n_wg = (long long)B * pa.Hq * pa.n_qt;
+    const long long n_wg = (long long)B * (pa.Hq / pa.gh) * pa.n_qt;
     if (n_wg > 0x7fffffffLL) return fail(SA_ERANGE, "prefill grid too large");
     const dim3 grid(static_cast<unsigned>(n_wg));
     sa_status s = SA_OK;
