@@ -15,7 +15,9 @@ streaming_attention_omp (compiled from its own sources into oracle/_ref, or
 the oracle's restatement when that is absent) on this host's cores over a
 bounded sample of the same workload.  `extra` carries the other measured
 configurations (single-head T=1024, one-layer Qwen3 decode loop, causal
-prefill) with their own roofline fractions.
+prefill, batched paged decode, the 28-layer decode step) with their own
+roofline fractions, and each with the reference's own CPU path timed on this
+host beside it (the decoder layer, the AVX2 blockwise prefill).
 """
 from __future__ import annotations
 
@@ -120,10 +122,7 @@ def bench_stream(torch, sa, synth, T: int, steps: int, warmup: int, min_footprin
 def cpu_baseline(Q, K, V, budget_s: float = 10.0):
     """The reference's streaming_attention_omp on this host, bounded sample."""
     from oracle import Oracle, Reference
-    threads = os.cpu_count() or 1
-    omp = os.environ.get("OMP_NUM_THREADS")
-    if omp and omp.isdigit():
-        threads = int(omp)
+    threads = _cpu_threads()
     if Reference.available():
         impl, kind = Reference(), "reference"
     else:
@@ -142,6 +141,74 @@ def cpu_baseline(Q, K, V, budget_s: float = 10.0):
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": kind,
             "sample": f"streaming_attention_omp, T={T}, d=128, block 128, {len(times)} timed calls "
                       f"(median {med * 1e3:.2f} ms) after 2 warmups, {threads} OpenMP threads"}
+
+
+def _cpu_threads() -> int:
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit():
+        return int(omp)
+    return os.cpu_count() or 1
+
+
+def cpu_layer_decode(steps: int = 100, warm: int = 2):
+    """Config 3 on the CPU: the reference's qwen3_decoder_layer_avx_with_cache
+    (STREAMING) for 100 one-token steps after a 128-token cache, 16/8 heads,
+    D=128.  Hidden size and MLP width are 8, so the projections are negligible
+    and the call is the attention path: q/k norm, RoPE, the cache read + concat
+    + update, repeat_kv and self_attention_streaming."""
+    from oracle import Reference
+    threads = _cpu_threads()
+    secs = Reference().time_decode_layer(8, 8, 16, 8, 128, 1, 128 - warm, steps + warm, threads)[warm:]
+    total = float(secs.sum())
+    return {"value": round(steps / total, 1), "unit": "steps/s", "cores": threads, "kind": "reference",
+            "sample": f"qwen3_decoder_layer_avx_with_cache STREAMING, hidden 8, {steps} steps over "
+                      f"cached lengths 128..{127 + steps} after {warm} warmup steps; median "
+                      f"{float(np.median(secs)) * 1e6:.0f} us/step"}
+
+
+def cpu_prefill(L: int):
+    """Config 4 on the CPU: the reference's
+    self_attention_streaming_blockwise_avx2 with q and kv blocks of 128 (the
+    benchmark's setting), 16 heads over repeat_kv'd K/V, fp32."""
+    from oracle import Reference
+    threads = _cpu_threads()
+    ref = Reference()
+    ref.set_threads(threads)
+    HQ, D = 16, 128
+    rng = np.random.default_rng(61)       # timing inputs only: N(0,1), results unchecked
+    q, k, v = (rng.standard_normal((1, HQ, L, D), dtype=np.float32) for _ in range(3))
+    sc = float(1 / np.sqrt(D))
+    reps = 3 if L <= 2048 else 1
+    if L <= 2048:
+        ref.blockwise(q, k, v, sc, 128, 128, 1)
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        ref.blockwise(q, k, v, sc, 128, 128, 1)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    tf = 2.0 * HQ * D * L * (L + 1) / med / 1e12
+    return {"value": round(tf, 4), "unit": "TFLOP/s", "cores": threads, "kind": "reference",
+            "sample": f"self_attention_streaming_blockwise_avx2, L={L}, 16 heads, blocks 128/128, "
+                      f"{reps} timed call(s), median {med:.3f} s"}
+
+
+def cpu_model_decode(sum_len: int, B: int = 64, layers: int = 28, steps: int = 3):
+    """Config 5 on the CPU, extrapolated: one reference decoder layer
+    (qwen3_decoder_layer_avx_with_cache, STREAMING, Qwen3-0.6B shapes) on one
+    sequence at the batch's mean context length, times 28 layers.  The
+    reference's cache has one length for the whole batch, so the batch of
+    ragged sequences is priced as B such calls per layer.  Embedding, final
+    norm and lm_head are left out, which favours the CPU."""
+    from oracle import Reference
+    threads = _cpu_threads()
+    L = sum_len // B
+    secs = Reference().time_decode_layer(1024, 3072, 16, 8, 128, 1, L, steps + 1, threads)[1:]
+    med = float(np.median(secs))
+    return {"value": round(1.0 / (layers * med), 4), "unit": "tok/s", "cores": threads, "kind": "reference",
+            "sample": f"qwen3_decoder_layer_avx_with_cache STREAMING at hidden 1024, one sequence of "
+                      f"{L} cached tokens (the mean of the batch), {steps} timed calls after 1 warmup, "
+                      f"median {med * 1e3:.1f} ms per layer; tok/s = 1 / (28 x that), lm_head excluded"}
 
 
 # ---------------------------------------------------------------- extra configs
@@ -342,7 +409,9 @@ def main() -> int:
                     default="all",
                     help="headline only, everything, or the headline plus one section")
     ap.add_argument("--T", type=int, default=262144)
-    ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--cpu-budget", type=float, default=10.0,
+                    help="seconds of CPU-baseline sampling for the headline; below 1 also skips the "
+                         "per-configuration CPU baselines")
     ap.add_argument("--profile-copy", action="store_true",
                     help="also run a 1 GiB device copy (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -379,9 +448,14 @@ def main() -> int:
             extra[f"single_head_T{T}"] = {"kernel_ms": c2["kernel_ms"], "gbs": round(c2["gbs"], 1),
                                           "hbm_frac": round(c2["gbs"] / HBM_PEAK_GBS, 4),
                                           "rel_l2_err": c2["rel_l2_err"]}
+    from oracle import Reference
+    cpu_extra = args.cpu_budget >= 1.0 and Reference.available()
     if run("layer"):
         log("[bench] one-layer Qwen3 decode loop (config 3)")
         extra["qwen3_layer_decode_loop"] = bench_cfg3(torch, sa, synth)
+        if cpu_extra:
+            log("[bench] CPU: reference decoder layer, attention path, 100 steps")
+            extra["qwen3_layer_decode_loop"]["cpu_baseline"] = cpu_layer_decode()
     if run("paged"):
         log("[bench] batched paged GQA decode, 64 sequences, bf16 KV (config 5 attention)")
         extra["paged_decode_b64_bf16"] = bench_paged_batch(torch, sa, synth)
@@ -390,10 +464,16 @@ def main() -> int:
             for bf in (True, False):
                 log(f"[bench] causal prefill L={L} {'bf16' if bf else 'fp32'} (config 4)")
                 extra[f"prefill_L{L}_{'bf16' if bf else 'f32'}"] = bench_prefill(torch, sa, synth, L, bf)
+            if cpu_extra:
+                log(f"[bench] CPU: reference blockwise AVX2 prefill L={L}")
+                extra[f"prefill_L{L}_cpu_baseline"] = cpu_prefill(L)
     if run("model"):
         torch.cuda.empty_cache()
         log("[bench] 28-layer Qwen3-0.6B-shape greedy decode, 64 sequences, bf16 KV (config 5)")
         extra["qwen3_model_decode_b64"] = bench_model_decode(torch, sa, synth)
+        if cpu_extra:
+            log("[bench] CPU: reference decoder layer at the mean context length")
+            extra["qwen3_model_decode_b64"]["cpu_baseline"] = cpu_model_decode(sum(batch_lengths(synth, 64)))
     log("[bench] CPU baseline (reference streaming_attention_omp)")
     cpu = cpu_baseline(Q, K, V, args.cpu_budget)
 

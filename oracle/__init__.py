@@ -51,6 +51,8 @@ _REF_SIGS = {
     "ref_blockwise": (None, [_P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _I, _P]),
     "ref_layer_attention": (_I, [_I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _F, _I, _I, _I, _P, _P]),
     "ref_qwen3_forward": (_I, [_I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _I] + [_P] * 13),
+    "ref_set_threads": (None, [_I]),
+    "ref_time_decode_layer": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
 }
 
 
@@ -277,6 +279,21 @@ class Reference:
         if rc != 0:
             raise RuntimeError("reference layer raised")
         return attn, eff
+
+    def set_threads(self, n):
+        """omp_set_num_threads(n) for the reference's later OpenMP regions."""
+        self.lib.ref_set_threads(int(n))
+
+    def time_decode_layer(self, hidden, intermediate, Hq, Hkv, D, batch, L0, n_steps, nthreads):
+        """Wall seconds of n_steps one-token calls of the reference's
+        qwen3_decoder_layer_avx_with_cache (STREAMING) over a cache holding L0
+        tokens per sequence (timing only: LCG-filled weights and inputs)."""
+        secs = np.empty(n_steps, np.float64)
+        rc = self.lib.ref_time_decode_layer(hidden, intermediate, Hq, Hkv, D, batch, L0, n_steps, nthreads,
+                                            secs.ctypes.data)
+        if rc != 0:
+            raise RuntimeError("reference layer raised")
+        return secs
 
     def qwen3_forward(self, weights, cfg, tokens, prompt_len):
         """qwen3_forward_with_cache over tokens [B][P + n] (teacher forcing):

@@ -8,6 +8,8 @@
 // marshals plain arrays into the reference's API and back.
 #include <omp.h>
 
+#include <chrono>
+#include <cstdint>
 #include <cstring>
 #include <stdexcept>
 #include <vector>
@@ -30,6 +32,19 @@ Tensor make(const float* p, std::vector<size_t> dims) {
 }
 void put(const Tensor& t, float* out) { std::memcpy(out, t.data(), t.size() * sizeof(float)); }
 void put(const std::vector<float>& v, float* out) { std::memcpy(out, v.data(), v.size() * sizeof(float)); }
+
+// Timing fill: values uniform in [-amp, amp) from a 64-bit LCG (the values
+// only need to be finite and non-denormal; no result is checked).
+Tensor filled(std::vector<size_t> dims, float amp, uint64_t& state) {
+    size_t n = 1;
+    for (size_t d : dims) n *= d;
+    std::vector<float> v(n);
+    for (auto& x : v) {
+        state = state * 6364136223846793005ULL + 1442695040888963407ULL;
+        x = amp * (2.0f * (float)(state >> 40) / 16777216.0f - 1.0f);
+    }
+    return Tensor(std::move(v), Shape(dims));
+}
 }  // namespace
 
 extern "C" {
@@ -52,6 +67,8 @@ void ref_naive_omp(const float* Q, const float* K, const float* V, int T, int d,
                    float* O) {
     put(naive_attention_omp(Q, K, V, T, d, nthreads), O);
 }
+
+void ref_set_threads(int n) { omp_set_num_threads(n); }
 
 float ref_l2_error(const float* a, const float* b, int n) { return compute_l2_error(a, b, n); }
 float ref_max_error(const float* a, const float* b, int n) { return compute_max_error(a, b, n); }
@@ -200,6 +217,55 @@ int ref_layer_attention(int Hq, int Hkv, int D, int prompt_len, int n_steps, con
             cache.increment_seq_len(S);
             t0 += S;
         }
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+// Timing only (the CPU baseline of the decode benchmarks): n_steps one-token
+// forwards of one reference decoder layer,
+// qwen3_decoder_layer_avx_with_cache (tensor_cpp/src/qwen3_ops_avx.cpp:469-754)
+// with AttentionType::STREAMING, for B sequences whose KVCache already holds
+// L0 tokens (written with KVCache::update, then increment_seq_len(L0)).
+// Hidden size H, MLP width I; weights and inputs are LCG fill.  Each call
+// does everything the reference does per layer and token: RMSNorm, q/k/v
+// projections, q/k RMSNorm, RoPE, the cache read, concat and update,
+// repeat_kv, self_attention_streaming, o_proj and the MLP.  The RoPE table is
+// built once beforehand (the reference rebuilds it once per forward, outside
+// the layer).  secs[i] = wall seconds of call i.  Returns 0, or -1 on a
+// reference exception.
+int ref_time_decode_layer(int H, int I, int Hq, int Hkv, int D, int B, int L0, int n_steps,
+                          int nthreads, double* secs) {
+    try {
+        const int saved = omp_get_max_threads();
+        if (nthreads > 0) omp_set_num_threads(nthreads);
+        uint64_t st = 0x5eed0001ULL;
+        const size_t qd = (size_t)Hq * D, kd = (size_t)Hkv * D;
+        Tensor ones_h(std::vector<float>((size_t)H, 1.0f), Shape({(size_t)H}));
+        Tensor ones_d(std::vector<float>((size_t)D, 1.0f), Shape({(size_t)D}));
+        Tensor qp = filled({qd, (size_t)H}, 0.02f, st), kp = filled({kd, (size_t)H}, 0.02f, st);
+        Tensor vp = filled({kd, (size_t)H}, 0.02f, st), op = filled({(size_t)H, qd}, 0.02f, st);
+        Tensor gate = filled({(size_t)I, (size_t)H}, 0.02f, st), up = filled({(size_t)I, (size_t)H}, 0.02f, st);
+        Tensor down = filled({(size_t)H, (size_t)I}, 0.02f, st);
+        q3::KVCache cache(1, B, Hkv, D, L0 + n_steps + 1);
+        if (L0 > 0) {
+            cache.update(0, filled({(size_t)B, (size_t)Hkv, (size_t)L0, (size_t)D}, 1.0f, st),
+                         filled({(size_t)B, (size_t)Hkv, (size_t)L0, (size_t)D}, 1.0f, st));
+            cache.increment_seq_len(L0);
+        }
+        auto cs = q3::compute_rope_freqs(cache.max_seq_len, D, 1000000.0f);
+        for (int i = 0; i < n_steps; ++i) {
+            Tensor hidden = filled({(size_t)B, 1, (size_t)H}, 1.0f, st);
+            const auto t0 = std::chrono::steady_clock::now();
+            Tensor out = tensor_cpp::qwen3::avx2::qwen3_decoder_layer_avx_with_cache(
+                hidden, &cache, 0, Hq, Hkv, D, 1e-6f, ones_h, qp, kp, vp, op, ones_d, ones_d, ones_h,
+                gate, up, down, cs.first, cs.second, q3::AttentionType::STREAMING);
+            const auto t1 = std::chrono::steady_clock::now();
+            secs[i] = std::chrono::duration<double>(t1 - t0).count();
+            cache.increment_seq_len(1);
+        }
+        omp_set_num_threads(saved);
         return 0;
     } catch (const std::exception&) {
         return -1;
