@@ -225,6 +225,11 @@ prefill_bf16_kernel(PrefillArgs pa) {
     const int n = lane & 31;        // query column inside a 32-query block
     const int hh = lane >> 5;       // lane half
     const float sl2 = pa.sl2;
+    // Waves w and w + W/2 share a SIMD.  The first of each pair runs at a
+    // raised priority throughout, so when both are ready to issue it goes
+    // first and the pair drifts out of phase: one wave's MFMAs overlap the
+    // other's softmax instead of the two interleaving MFMA for MFMA.
+    if (__builtin_amdgcn_readfirstlane(wave) < W / 2) __builtin_amdgcn_s_setprio(1);
 
     // The workgroup's gh query heads share every K/V tile: W / gh waves per
     // head, each wave QWAVE consecutive queries of its head.
@@ -298,13 +303,16 @@ prefill_bf16_kernel(PrefillArgs pa) {
         // MFMAs of block 1, the softmax of block 1 the PV MFMAs of block 0.
         // Only an excess above 2^kHugeExcess (a wave's first tile, in practice)
         // rescales before the softmax.  DIAG instantiates the diagonal mask.
+        // LDS fragment reads run ahead of their use: the V fragments of a half
+        // are read before its softmax, the K fragments of the second half
+        // before the first half's PV product.
         auto tile = [&](auto diag_tag) {
             constexpr bool DIAG = decltype(diag_tag)::value;
+            bf16x8_t kf[NKS];
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) kf[ks] = lds_b128(sK + k_off + ks * 16);
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
-                bf16x8_t kf[NKS];
-#pragma unroll
-                for (int ks = 0; ks < NKS; ++ks) kf[ks] = lds_b128(sK + k_off + kb * 32 * Lds::K_STRIDE + ks * 16);
                 // Element j of a score block is key kt*64 + 32 kb + 16 (j/8) + 8 hh + j%8
                 // for query q_wave0 + 32 qb + n.  On the diagonal tile keys past
                 // the query are removed (query - kt*64 = dq + 32 qb + n).
@@ -382,22 +390,20 @@ prefill_bf16_kernel(PrefillArgs pa) {
                             acc[qb][db] =
                                 __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][t], pb[qb][t], acc[qb][db], 0, 0, 0);
                 };
-                // Two waves share each SIMD; a wave raises its priority while it
-                // issues MFMAs, so the other wave's softmax fills the VALU.
 #pragma unroll
                 for (int qb = 0; qb < QB; ++qb) {
-                    __builtin_amdgcn_s_setprio(1);
                     s[qb] = scores(qb);
-                    __builtin_amdgcn_s_setprio(0);
+                    if (qb == QB - 1) load_v();
                     mt[qb] = row_max(s[qb]);
                     if (__any(mt[qb] * sl2 > ms[qb] + kHugeExcess)) raise(qb, mt[qb]);
                     softmax(qb, s[qb], pb[qb]);
                 }
-                load_v();
-                __builtin_amdgcn_s_setprio(1);
+                if (kb == 0) {
+#pragma unroll
+                    for (int ks = 0; ks < NKS; ++ks) kf[ks] = lds_b128(sK + k_off + 32 * Lds::K_STRIDE + ks * 16);
+                }
 #pragma unroll
                 for (int qb = 0; qb < QB; ++qb) pv(qb);
-                __builtin_amdgcn_s_setprio(0);
                 // A max that rose by more than 2^kLazyRescale: rescale now (after PV, exact).
                 bool up = false;
 #pragma unroll
@@ -663,10 +669,14 @@ sa_status opt_in_lds(Kernel* kernel, int bytes) {
 }
 
 // bf16 shape: W waves of QB 32-query blocks each.  Measured at L = 8192
-// (16/8 heads) on MI355X: 8 waves x 32 queries (two waves per SIMD, MFMA
-// phases at raised priority, both query heads of a KV group per workgroup)
-// 0.355 ms; 4 waves x 64 queries (one wave per SIMD, softmax of one block
-// hand-interleaved with the other block's MFMAs) 0.365 ms.
+// (16/8 heads) on MI355X, steady-state clocks: 8 waves x 32 queries (two
+// waves per SIMD, both query heads of a KV group per workgroup) 0.281 ms.
+// Slower alternatives: 4 waves x 64 queries with one block's softmax
+// hand-interleaved with the other's MFMAs; a phase-locked schedule in which
+// the two waves of a SIMD alternate between MFMA and softmax phases at
+// workgroup barriers (0.29-0.30 ms even without staging); a third LDS stage
+// for cross-tile fragment prefetch; the score product split into two
+// independent MFMA chains.
 constexpr int kBfQB = 1;
 constexpr int kBfW = 8;
 
