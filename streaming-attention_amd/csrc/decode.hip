@@ -385,6 +385,17 @@ lse_merge_kernel(DecodeArgs a) {
     __shared__ float sh_scr[MT / kWave];
     const float* ml = a.part_ml + (size_t)bh * a.n_split * 2;
     const float4* po = reinterpret_cast<const float4*>(a.part_o + (size_t)bh * a.n_split * D);
+    const int j = threadIdx.x % V4;
+    const int part = threadIdx.x / V4;
+    // The first NPRE partial rows of this thread are loaded before the
+    // reductions, so their latency overlaps that of the (m, l) loads.
+    constexpr int NPRE = 8;
+    float4 pre[NPRE];
+#pragma unroll
+    for (int k = 0; k < NPRE; ++k) {
+        const int c = part + k * PARTS;
+        pre[k] = c < n_active ? po[(size_t)c * V4 + j] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     float mx = -INFINITY;
     for (int c = threadIdx.x; c < n_active; c += MT) mx = fmaxf(mx, ml[2 * c]);
     mx = block_reduce<OpMax, MT / kWave>(mx, sh_scr);
@@ -395,11 +406,18 @@ lse_merge_kernel(DecodeArgs a) {
         ls = fmaf(w, ml[2 * c + 1], ls);
     }
     ls = block_reduce<OpSum, MT / kWave>(ls, sh_scr);   // also orders the sh_w writes
-    const int j = threadIdx.x % V4;
-    const int part = threadIdx.x / V4;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int k = 0; k < NPRE; ++k) {
+        const int c = part + k * PARTS;
+        if (c < n_active) {
+            const float w = sh_w[c];
+            acc.x = fmaf(w, pre[k].x, acc.x); acc.y = fmaf(w, pre[k].y, acc.y);
+            acc.z = fmaf(w, pre[k].z, acc.z); acc.w = fmaf(w, pre[k].w, acc.w);
+        }
+    }
 #pragma unroll 4
-    for (int c = part; c < n_active; c += PARTS) {
+    for (int c = part + NPRE * PARTS; c < n_active; c += PARTS) {
         const float4 x = po[(size_t)c * V4 + j];
         const float w = sh_w[c];
         acc.x = fmaf(w, x.x, acc.x); acc.y = fmaf(w, x.y, acc.y);
