@@ -29,7 +29,8 @@ typedef enum sa_status {
     SA_ENOMEM = -2,   /* device allocation failed / workspace too small      */
     SA_EFULL = -3,    /* KV cache has no room for the requested tokens       */
     SA_EHIP = -4,     /* a HIP runtime call failed                           */
-    SA_ERANGE = -5    /* index (layer, sequence, length) out of range        */
+    SA_ERANGE = -5,   /* index (layer, sequence, length) out of range        */
+    SA_EIO = -6       /* a file could not be read or is malformed            */
 } sa_status;
 
 typedef enum sa_dtype {

@@ -62,6 +62,9 @@ typedef enum sa_qwen3_tensor {
 sa_status sa_qwen3_create(const sa_qwen3_desc* desc, int max_batch, sa_qwen3** out);
 sa_status sa_qwen3_destroy(sa_qwen3* model);
 
+/* The desc the model was created with (an accessor; no reference counterpart). */
+sa_status sa_qwen3_get_desc(const sa_qwen3* model, sa_qwen3_desc* desc);
+
 /* Device pointer, element count and dtype of one weight tensor. */
 sa_status sa_qwen3_tensor_ptr(sa_qwen3* model, int layer, sa_qwen3_tensor which, void** ptr,
                               size_t* count, sa_dtype* dtype);
@@ -73,6 +76,30 @@ sa_status sa_qwen3_tensor_ptr(sa_qwen3* model, int layer, sa_qwen3_tensor which,
  * on draws 2i and 2i+1, rounded to fp32), so any tensor can be rebuilt on a
  * host from (seed, stream). */
 sa_status sa_qwen3_init_random(sa_qwen3* model, uint64_t seed, float std, sa_stream_t stream);
+
+/* ---- Checkpoints in safetensors format (Hugging Face Qwen3 tensor names) ----
+ * Replace load_qwen3_weights (reference tensor_cpp/src/qwen3_loader.cpp:
+ * 188-296, declared in tensor_cpp/include/tensor_cpp/qwen3_loader.h:80-85).
+ * Names read: model.embed_tokens.weight, model.norm.weight, lm_head.weight
+ * (absent when the checkpoint ties it to the embedding: the embedding is
+ * used), and per layer i model.layers.i.{input_layernorm, post_attention_
+ * layernorm, self_attn.{q,k,v,o}_proj, self_attn.{q,k}_norm,
+ * mlp.{gate,up,down}_proj}.weight.  Tensors may be BF16 or F32; matrices are
+ * stored on the device in bf16 (F32 rounded to nearest even), norm weights
+ * in fp32.  Host only, no GPU needed: */
+
+/* The model shape the checkpoint holds: layer count from the layer names,
+ * hidden and vocab from the embedding, head_dim from q_norm, head counts
+ * from q_proj / k_proj rows, intermediate from gate_proj.  rms_eps = 1e-6
+ * and rope_theta = 1e6 (Qwen3's values; the file does not carry them) and
+ * max_pos = 0, for the caller to set.  SA_EIO: unreadable or malformed file;
+ * SA_EINVAL: a tensor missing or of a shape that does not fit the others. */
+sa_status sa_qwen3_desc_from_safetensors(const char* path, sa_qwen3_desc* desc);
+
+/* Upload a checkpoint into a model created with a matching desc (same
+ * layers, hidden, intermediate, vocab, heads and head_dim): q/k/v rows
+ * fused q | k | v, gate/up fused gate | up.  Synchronous. */
+sa_status sa_qwen3_load_safetensors(sa_qwen3* model, const char* path);
 
 /* One greedy decode step for sequences 0 .. batch-1 of the cache.
  * tokens: device int32 [batch] input ids; token i is appended to sequence i

@@ -52,6 +52,7 @@ _REF_SIGS = {
     "ref_layer_attention": (_I, [_I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _F, _I, _I, _I, _P, _P]),
     "ref_qwen3_forward": (_I, [_I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _I] + [_P] * 13),
     "ref_set_threads": (None, [_I]),
+    "ref_qwen3_forward_file": (_I, [C.c_char_p, _F, _I, _I, _I, _P, _P]),
     "ref_time_decode_layer": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
 }
 
@@ -279,6 +280,20 @@ class Reference:
         if rc != 0:
             raise RuntimeError("reference layer raised")
         return attn, eff
+
+    def qwen3_forward_file(self, path, vocab, tokens, prompt_len, eps=1e-6):
+        """qwen3_forward_with_cache (teacher forcing, as qwen3_forward) on the
+        weights the reference's load_qwen3_weights reads from a safetensors
+        file.  Returns logits [n + 1][B][vocab]."""
+        import os
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        B, N = tokens.shape
+        logits = np.empty((N - prompt_len + 1, B, vocab), np.float32)
+        rc = self.lib.ref_qwen3_forward_file(os.fsencode(str(path)), eps, B, prompt_len, N - prompt_len,
+                                             _p(tokens), _p(logits))
+        if rc != 0:
+            raise RuntimeError("reference loader or forward raised")
+        return logits
 
     def set_threads(self, n):
         """omp_set_num_threads(n) for the reference's later OpenMP regions."""

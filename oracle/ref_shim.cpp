@@ -18,6 +18,7 @@
 #include "tensor_cpp/kv_cache.h"
 #include "tensor_cpp/ops.h"
 #include "tensor_cpp/qwen3_ops.h"
+#include "tensor_cpp/qwen3_loader.h"
 #include "tensor_cpp/qwen3_ops_avx.h"
 
 using tensor_cpp::Shape;
@@ -44,6 +45,30 @@ Tensor filled(std::vector<size_t> dims, float amp, uint64_t& state) {
         x = amp * (2.0f * (float)(state >> 40) / 16777216.0f - 1.0f);
     }
     return Tensor(std::move(v), Shape(dims));
+}
+
+// Teacher-forced forwards through qwen3_forward_with_cache (STANDARD
+// attention, dense KVCache): a P-token prompt, then n_steps one-token
+// forwards; logits [n_steps + 1][B][V] at the last position of each.
+void run_forward(const std::vector<q3::Qwen3LayerWeights>& layers, const Tensor& embed, const Tensor& norm,
+                 const Tensor& head, int nl, int Hq, int Hkv, int D, float eps, int B, int P, int n_steps,
+                 const int* tokens, int V, float* logits) {
+    q3::KVCache cache(nl, B, Hkv, D, P + n_steps + 1);
+    const int N = P + n_steps;
+    int t0 = 0;
+    for (int call = 0; call <= n_steps; ++call) {
+        const int S = call == 0 ? P : 1;
+        std::vector<long> ids((size_t)B * S);
+        for (int b = 0; b < B; ++b)
+            for (int s = 0; s < S; ++s) ids[(size_t)b * S + s] = tokens[(size_t)b * N + t0 + s];
+        TensorL input(ids, Shape({(size_t)B, (size_t)S}));
+        Tensor out = q3::qwen3_forward_with_cache(input, &cache, embed, layers, norm, head, nl, Hq, Hkv, D, eps,
+                                                  q3::AttentionType::STANDARD);
+        for (int b = 0; b < B; ++b)
+            std::memcpy(logits + ((size_t)call * B + b) * V, out.data() + ((size_t)b * S + S - 1) * V,
+                        (size_t)V * sizeof(float));
+        t0 += S;
+    }
 }
 }  // namespace
 
@@ -305,22 +330,25 @@ int ref_qwen3_forward(int nl, int H, int I, int V, int Hq, int Hkv, int D, float
         Tensor t_embed = make(embed, {(size_t)V, (size_t)H});
         Tensor t_norm = make(final_norm, {(size_t)H});
         Tensor t_head = make(lm_head, {(size_t)V, (size_t)H});
-        q3::KVCache cache(nl, B, Hkv, D, P + n_steps + 1);
-        const int N = P + n_steps;
-        int t0 = 0;
-        for (int call = 0; call <= n_steps; ++call) {
-            const int S = call == 0 ? P : 1;
-            std::vector<long> ids((size_t)B * S);
-            for (int b = 0; b < B; ++b)
-                for (int s = 0; s < S; ++s) ids[(size_t)b * S + s] = tokens[(size_t)b * N + t0 + s];
-            TensorL input(ids, Shape({(size_t)B, (size_t)S}));
-            Tensor out = q3::qwen3_forward_with_cache(input, &cache, t_embed, layers, t_norm, t_head, nl, Hq,
-                                                      Hkv, D, eps, q3::AttentionType::STANDARD);
-            for (int b = 0; b < B; ++b)
-                std::memcpy(logits + ((size_t)call * B + b) * V, out.data() + ((size_t)b * S + S - 1) * V,
-                            (size_t)V * sizeof(float));
-            t0 += S;
-        }
+        run_forward(layers, t_embed, t_norm, t_head, nl, Hq, Hkv, D, eps, B, P, n_steps, tokens, V, logits);
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+// The same forwards with the weights read by the reference's own loader,
+// load_qwen3_weights (tensor_cpp/src/qwen3_loader.cpp:188-296), from a
+// safetensors file.  That loader assumes 28 layers, 16/8 heads and head_dim
+// 128 and takes hidden and vocab from the embedding.  Returns -1 on a
+// reference exception (for example a missing tensor).
+int ref_qwen3_forward_file(const char* path, float eps, int B, int P, int n_steps, const int* tokens,
+                           float* logits) {
+    try {
+        q3::Qwen3Weights w = q3::load_qwen3_weights(path);
+        run_forward(w.layers, w.embed_tokens, w.norm_weight, w.lm_head, (int)w.num_layers,
+                    (int)w.num_attention_heads, (int)w.num_key_value_heads, (int)w.head_dim, eps, B, P, n_steps,
+                    tokens, (int)w.vocab_size, logits);
         return 0;
     } catch (const std::exception&) {
         return -1;

@@ -26,12 +26,13 @@ SA_ENOMEM = -2
 SA_EFULL = -3
 SA_EHIP = -4
 SA_ERANGE = -5
+SA_EIO = -6
 SA_DTYPE_F32 = 0
 SA_DTYPE_BF16 = 1
 PAGE_TOKENS = 64
 
 _STATUS_NAMES = {0: "SA_OK", -1: "SA_EINVAL", -2: "SA_ENOMEM", -3: "SA_EFULL",
-                 -4: "SA_EHIP", -5: "SA_ERANGE"}
+                 -4: "SA_EHIP", -5: "SA_ERANGE", -6: "SA_EIO"}
 
 
 class SaError(RuntimeError):
@@ -90,7 +91,10 @@ SIGNATURES = {
     "sa_prefill_causal_strided": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _F, _P, _P]),
     "sa_qwen3_create": (_I, [C.POINTER(Qwen3Desc), _I, C.POINTER(_P)]),
     "sa_qwen3_destroy": (_I, [_P]),
+    "sa_qwen3_get_desc": (_I, [_P, C.POINTER(Qwen3Desc)]),
     "sa_qwen3_tensor_ptr": (_I, [_P, _I, _I, C.POINTER(_P), C.POINTER(_SZ), C.POINTER(_I)]),
+    "sa_qwen3_desc_from_safetensors": (_I, [C.c_char_p, C.POINTER(Qwen3Desc)]),
+    "sa_qwen3_load_safetensors": (_I, [_P, C.c_char_p]),
     "sa_qwen3_init_random": (_I, [_P, C.c_uint64, _F, _P]),
     "sa_qwen3_decode_step": (_I, [_P, _P, _P, _I, _P, _P, _P]),
 }
@@ -323,6 +327,24 @@ class Qwen3:
         check(lib().sa_qwen3_create(C.byref(self.desc), max_batch, C.byref(h)))
         self.handle = h
         self.max_batch = max_batch
+
+    @staticmethod
+    def checkpoint_shape(path) -> dict:
+        """The model shape a safetensors checkpoint holds (host only)."""
+        d = Qwen3Desc()
+        check(lib().sa_qwen3_desc_from_safetensors(os.fsencode(path), C.byref(d)))
+        return {f: getattr(d, f) for f, _ in Qwen3Desc._fields_ if f != "max_pos"}
+
+    @classmethod
+    def from_safetensors(cls, path, max_batch: int, max_pos: int) -> "Qwen3":
+        """A model of the checkpoint's shape with its weights uploaded."""
+        m = cls(max_batch, max_pos, **cls.checkpoint_shape(path))
+        m.load_safetensors(path)
+        return m
+
+    def load_safetensors(self, path) -> None:
+        """Upload a checkpoint of this model's shape (synchronous)."""
+        check(lib().sa_qwen3_load_safetensors(self.handle, os.fsencode(path)))
 
     def close(self) -> None:
         if self.handle:

@@ -472,6 +472,13 @@ extern "C" sa_status sa_qwen3_destroy(sa_qwen3* m) {
     return SA_OK;
 }
 
+extern "C" sa_status sa_qwen3_get_desc(const sa_qwen3* m, sa_qwen3_desc* desc) {
+    clear_error();
+    if (!m || !desc) return fail(SA_EINVAL, "null argument");
+    *desc = m->d;
+    return SA_OK;
+}
+
 extern "C" sa_status sa_qwen3_tensor_ptr(sa_qwen3* m, int layer, sa_qwen3_tensor which, void** ptr, size_t* count,
                                          sa_dtype* dtype) {
     clear_error();
