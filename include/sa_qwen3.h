@@ -101,6 +101,19 @@ sa_status sa_qwen3_desc_from_safetensors(const char* path, sa_qwen3_desc* desc);
  * fused q | k | v, gate/up fused gate | up.  Synchronous. */
 sa_status sa_qwen3_load_safetensors(sa_qwen3* model, const char* path);
 
+/* Prefill: a prompt of L tokens for each of sequences 0 .. batch-1, which
+ * must be empty, in one forward (qwen3_forward_with_cache on an empty cache
+ * with input [batch, L]; reference tensor_cpp/src/qwen3_ops.cpp:936-1014).
+ * tokens: device int32 [batch][L].  Every layer appends the prompt's K/V
+ * (positions 0 .. L-1) and attends causally over it; afterwards each
+ * sequence's length is L.  next_tokens: device int32 [batch], the argmax of
+ * the last position's logits; logits: device fp32 [batch][vocab] (that
+ * position) or NULL.  The caller must have reserved L tokens of pages.
+ * Activations of batch * L rows live in a grow-only device buffer of the
+ * model (allocated on the first call of a larger size).  Asynchronous. */
+sa_status sa_qwen3_prefill(sa_qwen3* model, sa_kvcache* cache, const int32_t* tokens, int batch, int L,
+                           int32_t* next_tokens, float* logits, sa_stream_t stream);
+
 /* One greedy decode step for sequences 0 .. batch-1 of the cache.
  * tokens: device int32 [batch] input ids; token i is appended to sequence i
  * at position sa_kvcache_len(cache, i), every layer attends over that

@@ -97,6 +97,7 @@ SIGNATURES = {
     "sa_qwen3_load_safetensors": (_I, [_P, C.c_char_p]),
     "sa_qwen3_init_random": (_I, [_P, C.c_uint64, _F, _P]),
     "sa_qwen3_decode_step": (_I, [_P, _P, _P, _I, _P, _P, _P]),
+    "sa_qwen3_prefill": (_I, [_P, _P, _P, _I, _I, _P, _P, _P]),
 }
 
 _lib = None
@@ -371,6 +372,19 @@ class Qwen3:
 
     def init_random(self, seed: int, std: float = 0.02, stream=None) -> None:
         check(lib().sa_qwen3_init_random(self.handle, seed, std, _stream(stream)))
+
+    def prefill(self, cache: "KVCache", tokens, next_tokens=None, logits=None, stream=None):
+        """tokens: int32 CUDA [B][L] prompts of empty sequences 0..B-1 -> next
+        tokens int32 CUDA [B] (and the last position's logits if given)."""
+        import torch
+        if tokens.dtype != torch.int32 or not tokens.is_cuda or tokens.dim() != 2:
+            raise ValueError("tokens must be an int32 CUDA tensor [B][L]")
+        tokens = tokens.contiguous()
+        B, L = tokens.shape
+        next_tokens = torch.empty(B, dtype=torch.int32, device=tokens.device) if next_tokens is None else next_tokens
+        check(lib().sa_qwen3_prefill(self.handle, cache.handle, _ptr(tokens), B, L, _ptr(next_tokens), _ptr(logits),
+                                     _stream(stream)))
+        return next_tokens
 
     def decode_step(self, cache: "KVCache", tokens, next_tokens=None, logits=None, stream=None):
         """tokens: int32 CUDA [B] -> next tokens int32 CUDA [B] (and logits if given)."""

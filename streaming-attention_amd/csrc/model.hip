@@ -56,6 +56,8 @@ struct sa_qwen3 {
     int32_t* am_idx = nullptr;
     void* ws = nullptr;        // paged decode workspace (grow-only)
     size_t ws_bytes = 0;
+    void* pf = nullptr;        // prefill activations for batch x prompt rows (grow-only)
+    size_t pf_bytes = 0;
 };
 
 namespace sa {
@@ -144,8 +146,9 @@ embed_norm_kernel(const uint16_t* embed, const int32_t* tokens, int vocab, int H
 
 // ---------------------------------------------------------------------------
 // GEMM: P[s][m][n] = sum over k in split s of X[m][k] * W[n][k].
-// X fp32 [M][K] (M <= 64), W bf16 [N][K]; N % 64 == 0, split % 32 == 0.
-// A workgroup owns all 64 rows (rows past M read as zero) and 64 columns;
+// X fp32 [M][K], W bf16 [N][K]; N % 64 == 0, split % 32 == 0.
+// Workgroup (x, y, z) owns rows 64 z .. 64 z + 63 (rows past M read as zero),
+// columns 64 x .. 64 x + 63 and split y;
 // wave w computes the 32 x 32 block (rows 32 (w / 2), columns 32 (w % 2))
 // with v_mfma_f32_32x32x2f32: exact fp32 products of the activations and the
 // widened bf16 weights, fp32 accumulation.  32-wide k chunks go through LDS
@@ -164,13 +167,16 @@ gemm_xwt_kernel(const float* __restrict__ X, int M, int K, const uint16_t* __res
     const int row = lane & 31, kh = lane >> 5;
     const int n0 = blockIdx.x * kGN;
     const int k_begin = blockIdx.y * split;
+    const int m0 = blockIdx.z * kMaxRows;
+    const float* Xt = X + (size_t)m0 * K;
+    const int Mt = M - m0;   // rows of this tile that exist
     f32x16_t acc = {};
     for (int k0 = k_begin; k0 < k_begin + split; k0 += kGK) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int idx = tid + i * 256, r = idx >> 3, c = (idx & 7) * 4;
             float4 xv = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (r < M) xv = *reinterpret_cast<const float4*>(X + (size_t)r * K + k0 + c);
+            if (r < Mt) xv = *reinterpret_cast<const float4*>(Xt + (size_t)r * K + k0 + c);
             Xs[c + 0][r] = xv.x;
             Xs[c + 1][r] = xv.y;
             Xs[c + 2][r] = xv.z;
@@ -192,11 +198,11 @@ gemm_xwt_kernel(const float* __restrict__ X, int M, int K, const uint16_t* __res
         __syncthreads();
     }
     // element j of acc: row mb + 8 (j / 4) + 4 kh + j % 4, column nb + row
-    float* out = P + (size_t)blockIdx.y * M * N + n0 + nb + row;
+    float* out = P + (size_t)blockIdx.y * M * N + (size_t)m0 * N + n0 + nb + row;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
         const int m = mb + 8 * (j >> 2) + 4 * kh + (j & 3);
-        if (m < M) out[(size_t)m * N] = acc[j];
+        if (m < Mt) out[(size_t)m * N] = acc[j];
     }
 }
 
@@ -331,6 +337,12 @@ __global__ void argmax_final_kernel(const float* pv, const int32_t* pi, int nb, 
     out[m] = idx == 0x7fffffff ? 0 : idx;
 }
 
+// pos[r] = position of row r of a token-major [B][L][heads] layout: (r / heads) % L.
+__global__ void prompt_pos_kernel(int32_t* pos, long long n_rows, int heads, int L) {
+    const long long r = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r < n_rows) pos[r] = (int32_t)((r / heads) % L);
+}
+
 // ---------------------------------------------------------------------------
 // Host helpers
 // ---------------------------------------------------------------------------
@@ -344,7 +356,8 @@ int pick_split(int N, int K, int cus) {
 struct Gemm { int N, K, S; };
 
 sa_status gemm(const float* X, int M, const uint16_t* W, const Gemm& g, float* P, hipStream_t st) {
-    hipLaunchKernelGGL(gemm_xwt_kernel, dim3(g.N / kGN, g.S), dim3(256), 0, st, X, M, g.K, W, g.N, g.K / g.S, P);
+    hipLaunchKernelGGL(gemm_xwt_kernel, dim3(g.N / kGN, g.S, (M + kMaxRows - 1) / kMaxRows), dim3(256), 0, st, X, M,
+                       g.K, W, g.N, g.K / g.S, P);
     SA_CHECK_LAUNCH();
     return SA_OK;
 }
@@ -393,6 +406,8 @@ void release(sa_qwen3* m) {
     m->allocs.clear();
     if (m->ws) (void)hipFree(m->ws);
     m->ws = nullptr;
+    if (m->pf) (void)hipFree(m->pf);
+    m->pf = nullptr;
 }
 
 }  // namespace
@@ -530,6 +545,119 @@ extern "C" sa_status sa_qwen3_init_random(sa_qwen3* m, uint64_t seed, float stde
         }
     }
     return SA_OK;
+}
+
+// A prompt of L tokens for each of sequences 0 .. batch-1 (all empty), run
+// as one causal prefill: the activations are batch * L token rows, the
+// projections the same GEMMs over row tiles (no split-K), the attention
+// block q/k RMSNorm + RoPE at positions 0 .. L-1, the K/V append, and the
+// causal prefill kernel over the dense token-major q/k/v.  Reference:
+// qwen3_forward_with_cache with an empty cache and S = L
+// (tensor_cpp/src/qwen3_ops.cpp:936-1014, layer :620-934; the prefill attention
+// there is self_attention with a causal mask or
+// self_attention_streaming_blockwise, :894-909).
+extern "C" sa_status sa_qwen3_prefill(sa_qwen3* m, sa_kvcache* cache, const int32_t* tokens, int batch, int L,
+                                      int32_t* next_tokens, float* logits, sa_stream_t stream) {
+    clear_error();
+    if (!m || !cache || !tokens || !next_tokens) return fail(SA_EINVAL, "null argument");
+    if (batch < 1 || batch > m->max_batch) return fail(SA_ERANGE, "batch outside [1, max_batch]");
+    const sa_qwen3_desc& d = m->d;
+    if (L < 1 || L > d.max_pos) return fail(SA_ERANGE, "prompt length outside [1, max_pos]");
+    sa_kv_desc kd;
+    SA_TRY(sa_kvcache_get_desc(cache, &kd));
+    if (kd.num_layers != d.num_layers || kd.num_kv_heads != d.n_kv_heads || kd.head_dim != d.head_dim)
+        return fail(SA_EINVAL, "cache geometry does not match the model");
+    if (batch > kd.max_seqs) return fail(SA_ERANGE, "batch exceeds the cache's sequences");
+    if ((long long)L > (long long)kd.max_pages_per_seq * 64)
+        return fail(SA_EFULL, "prompt longer than a sequence's page table");
+    for (int i = 0; i < batch; ++i)
+        if (sa_kvcache_len(cache, i) != 0) return fail(SA_EINVAL, "prefill needs empty sequences");
+    hipStream_t st = as_stream(stream);
+    const Shapes s = shapes_of(d, device_cu_count());
+    const long long M = (long long)batch * L;
+    if (M > 0x7fffffffLL / std::max({s.Nqkv, 2 * s.I, s.H}))
+        return fail(SA_ERANGE, "batch * prompt too large");
+    const Gemm g_qkv{s.Nqkv, s.H, 1}, g_o{s.H, s.Nq, 1}, g_gu{2 * s.I, s.H, 1}, g_down{s.H, s.I, 1};
+
+    // activations of the M token rows, carved from one grow-only buffer
+    const size_t f_x = M * s.H, f_q = M * s.Nq, f_k = M * s.Nk, f_act = M * s.I;
+    const size_t f_part = M * std::max({s.Nqkv, 2 * s.I, s.H});
+    const size_t n_pos = M * s.Hq + M * s.Hkv;
+    const size_t floats = 2 * f_x + 2 * f_q + 2 * f_k + f_act + f_part + (size_t)batch * s.H;
+    const size_t need = floats * sizeof(float) + n_pos * sizeof(int32_t);
+    if (need > m->pf_bytes) {
+        if (m->pf) SA_HIP_TRY(hipFree(m->pf));
+        m->pf = nullptr;
+        m->pf_bytes = 0;
+        if (hipMalloc(&m->pf, need) != hipSuccess) return fail(SA_ENOMEM, "prefill activations");
+        m->pf_bytes = need;
+    }
+    float* x = static_cast<float*>(m->pf);
+    float* h = x + f_x;
+    float* q = h + f_x;
+    float* attn = q + f_q;
+    float* k = attn + f_q;
+    float* v = k + f_k;
+    float* act = v + f_k;
+    float* part = act + f_act;
+    float* h_last = part + f_part;
+    int32_t* pos_q = reinterpret_cast<int32_t*>(h_last + (size_t)batch * s.H);
+    int32_t* pos_k = pos_q + M * s.Hq;
+    const float eps = d.rms_eps;
+    const float scale = 1.0f / sqrtf((float)d.head_dim);
+    float* out_logits = logits ? logits : m->logits;
+
+    hipLaunchKernelGGL(prompt_pos_kernel, dim3((M * s.Hq + 255) / 256), dim3(256), 0, st, pos_q, M * s.Hq, s.Hq, L);
+    hipLaunchKernelGGL(prompt_pos_kernel, dim3((M * s.Hkv + 255) / 256), dim3(256), 0, st, pos_k, M * s.Hkv, s.Hkv,
+                       L);
+    hipLaunchKernelGGL(embed_norm_kernel, dim3((unsigned)M), dim3(256), 0, st, m->embed, tokens, s.V, s.H,
+                       m->layers[0].in_norm, eps, x, h);
+    SA_CHECK_LAUNCH();
+    const int ew_grid = (int)std::min<long long>(4LL * device_cu_count(), (M * s.I / 4 + 255) / 256);
+    const int64_t q_str[3] = {(int64_t)L * s.Nq, s.D, s.Nq};
+    const int64_t kv_str[3] = {(int64_t)L * s.Nk, s.D, s.Nk};
+    for (int l = 0; l < d.num_layers; ++l) {
+        const sa_qwen3::Layer& Ly = m->layers[l];
+        // ---- attention block ----
+        SA_TRY(gemm(h, (int)M, Ly.qkv, g_qkv, part, st));
+        hipLaunchKernelGGL(qkv_split_kernel, dim3((unsigned)M, (s.Nqkv + 1023) / 1024), dim3(256), 0, st, part, 1,
+                           (int)M, s.Nq, s.Nk, q, k, v);
+        SA_CHECK_LAUNCH();
+        SA_TRY(sa_qk_norm_rope(q, (int)(M * s.Hq), s.D, pos_q, Ly.q_norm, eps, m->rope_cos, m->rope_sin, d.max_pos,
+                               q, stream));
+        SA_TRY(sa_qk_norm_rope(k, (int)(M * s.Hkv), s.D, pos_k, Ly.k_norm, eps, m->rope_cos, m->rope_sin,
+                               d.max_pos, k, stream));
+        // k is normed and rotated already: append it (and v) as they are
+        SA_TRY(sa_qknorm_rope_append(cache, l, nullptr, k, v, batch, L, nullptr, s.Hq, nullptr, nullptr, eps,
+                                     nullptr, nullptr, 0, nullptr, stream));
+        SA_TRY(sa_prefill_causal_strided(q, k, v, SA_DTYPE_F32, batch, s.Hq, s.Hkv, L, s.D, q_str, kv_str, q_str,
+                                         scale, attn, stream));
+        SA_TRY(gemm(attn, (int)M, Ly.o, g_o, part, st));
+        hipLaunchKernelGGL(residual_norm_kernel, dim3((unsigned)M), dim3(256), 0, st, part, 1, (int)M, s.H, x,
+                           Ly.post_norm, eps, h);
+        SA_CHECK_LAUNCH();
+        // ---- MLP ----
+        SA_TRY(gemm(h, (int)M, Ly.gate_up, g_gu, part, st));
+        hipLaunchKernelGGL(swiglu_kernel, dim3(ew_grid), dim3(256), 0, st, part, 1, (int)M, s.I, act);
+        SA_CHECK_LAUNCH();
+        SA_TRY(gemm(act, (int)M, Ly.down, g_down, part, st));
+        const float* next_norm = l + 1 < d.num_layers ? m->layers[l + 1].in_norm : m->final_norm;
+        hipLaunchKernelGGL(residual_norm_kernel, dim3((unsigned)M), dim3(256), 0, st, part, 1, (int)M, s.H, x,
+                           next_norm, eps, h);
+        SA_CHECK_LAUNCH();
+    }
+    // ---- the last position of each sequence: lm_head, greedy argmax ----
+    SA_HIP_TRY(hipMemcpy2DAsync(h_last, (size_t)s.H * sizeof(float), h + (size_t)(L - 1) * s.H,
+                                (size_t)L * s.H * sizeof(float), (size_t)s.H * sizeof(float), batch,
+                                hipMemcpyDeviceToDevice, st));
+    SA_TRY(gemm(h_last, batch, m->lm_head, s.lm, out_logits, st));
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgBlocks, batch), dim3(256), 0, st, out_logits, s.V, m->am_val,
+                       m->am_idx);
+    SA_CHECK_LAUNCH();
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(batch), dim3(64), 0, st, m->am_val, m->am_idx, kArgBlocks,
+                       next_tokens);
+    SA_CHECK_LAUNCH();
+    return sa_kvcache_commit(cache, nullptr, batch, L, stream);
 }
 
 extern "C" sa_status sa_qwen3_decode_step(sa_qwen3* m, sa_kvcache* cache, const int32_t* tokens, int batch,
