@@ -109,6 +109,27 @@ def build_cpp_tests(verbose: bool = True) -> list[Path]:
     return outs
 
 
+CLI_DIR = PKG / "cli"
+BIN_DIR = PKG / "bin"
+
+
+def build_cli(verbose: bool = True) -> list[Path]:
+    """Host programs over the C ABI (cli/*.cpp -> bin/), linked to lib/libsa_amd.so."""
+    BIN_DIR.mkdir(exist_ok=True)
+    outs = []
+    for src in sorted(CLI_DIR.glob("*.cpp")):
+        exe = BIN_DIR / src.stem
+        cmd = [HIPCC, "-O2", "-std=c++17", "-Wall", "-D__HIP_PLATFORM_AMD__", f"-I{ROOT / 'include'}", str(src),
+               "-o", str(exe), f"-L{LIB_DIR}", "-lsa_amd", "-Wl,-rpath,$ORIGIN/../lib"]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"CLI build failed: {src}\n{res.stdout}\n{res.stderr}")
+        outs.append(exe)
+    if verbose and outs:
+        print("built CLI:", ", ".join(p.name for p in outs))
+    return outs
+
+
 def clean() -> None:
     shutil.rmtree(BUILD, ignore_errors=True)
 
@@ -123,6 +144,7 @@ if __name__ == "__main__":
         clean()
     try:
         build_library(args.j)
+        build_cli()
         if args.tests:
             build_cpp_tests()
     except RuntimeError as e:
