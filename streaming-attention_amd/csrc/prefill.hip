@@ -14,9 +14,10 @@
 // computed; only the tile that crosses a wave's diagonal applies the mask.
 //
 // bf16 inputs (v_mfma_f32_32x32x16_bf16, fp32 accumulation): a wave owns 32
-// queries; a workgroup of 8 waves serves the query heads of one KV group
-// (GQA 2: 4 waves x 32 queries for each of the two heads), so every K/V tile
-// staged in LDS feeds all of them.  The running max is raised lazily: a wave
+// queries; a workgroup of 8 waves (4 when the grid would not fill the CUs
+// twice) serves the query heads of one KV group (GQA 2 with 8 waves: 4 waves
+// x 32 queries for each of the two heads), so every K/V tile staged in LDS
+// feeds all of them.  The running max is raised lazily: a wave
 // rescales its accumulators only when some score exceeds the current max by
 // more than 2^8, and then after the PV product (exact), so the common tile
 // has no branch between softmax and PV.  P is rounded to bf16 for the PV
@@ -24,6 +25,7 @@
 //
 // fp32 inputs (v_mfma_f32_16x16x4f32): a wave owns 32 queries as two
 // 16-query blocks, a workgroup 128 queries, eager rescale.
+#include <cstdlib>
 #include <numeric>
 #include <type_traits>
 
@@ -225,11 +227,11 @@ prefill_bf16_kernel(PrefillArgs pa) {
     const int n = lane & 31;        // query column inside a 32-query block
     const int hh = lane >> 5;       // lane half
     const float sl2 = pa.sl2;
-    // Waves w and w + W/2 share a SIMD.  The first of each pair runs at a
-    // raised priority throughout, so when both are ready to issue it goes
+    // In an 8-wave workgroup waves w and w + 4 share a SIMD.  The first of
+    // each pair runs at a raised priority throughout, so when both are ready to issue it goes
     // first and the pair drifts out of phase: one wave's MFMAs overlap the
     // other's softmax instead of the two interleaving MFMA for MFMA.
-    if (__builtin_amdgcn_readfirstlane(wave) < W / 2) __builtin_amdgcn_s_setprio(1);
+    if (W >= 8 && __builtin_amdgcn_readfirstlane(wave) < W / 2) __builtin_amdgcn_s_setprio(1);
 
     // The workgroup's gh query heads share every K/V tile: W / gh waves per
     // head, each wave QWAVE consecutive queries of its head.
@@ -679,6 +681,7 @@ sa_status opt_in_lds(Kernel* kernel, int bytes) {
 // independent MFMA chains.
 constexpr int kBfQB = 1;
 constexpr int kBfW = 8;
+constexpr int kBfWSmall = 4;
 
 template <int D, int QB, int W>
 sa_status launch_bf16(const PrefillArgs& pa, dim3 grid, hipStream_t st) {
@@ -689,10 +692,26 @@ sa_status launch_bf16(const PrefillArgs& pa, dim3 grid, hipStream_t st) {
     return SA_OK;
 }
 
+// Workgroups of W waves serve gh = gcd(Hq / Hkv, W) query heads, W / gh
+// waves of 32 queries per head.
+long long bf16_grid(const PrefillArgs& pa, int B, int W) {
+    const int gh = std::gcd(pa.Hq / pa.Hkv, W);
+    const int q_tile = (W / gh) * kBfQB * 32;
+    return (long long)B * (pa.Hq / gh) * ((pa.L + q_tile - 1) / q_tile);
+}
+
 sa_status launch(PrefillArgs pa, int B, bool bf16, int D, hipStream_t st) {
-    // bf16: the workgroup's waves split over gh query heads of one KV group.
-    pa.gh = bf16 ? std::gcd(pa.Hq / pa.Hkv, kBfW) : 1;
-    const int q_tile = bf16 ? (kBfW / pa.gh) * kBfQB * 32 : kFQTile;
+    // bf16: 8-wave workgroups while they give every CU two of them; below
+    // that, 4-wave workgroups (one wave per SIMD) spread the same waves over
+    // twice as many CUs.  Measured (16/8 heads, D = 128): 4 waves are faster
+    // for L = 128 .. 4096 (1.06x .. 1.40x), 8 waves at L = 8192.
+    // SA_PREFILL_WAVES=4 or 8 forces the workgroup size (tests cover both).
+    const char* forced = std::getenv("SA_PREFILL_WAVES");
+    const int fw = forced ? std::atoi(forced) : 0;
+    const int W = fw == kBfW || fw == kBfWSmall ? fw
+                  : bf16 && bf16_grid(pa, B, kBfW) < 2LL * device_cu_count() ? kBfWSmall : kBfW;
+    pa.gh = bf16 ? std::gcd(pa.Hq / pa.Hkv, W) : 1;
+    const int q_tile = bf16 ? (W / pa.gh) * kBfQB * 32 : kFQTile;
     pa.n_qt = (pa.L + q_tile - 1) / q_tile;
     const int groups = B * pa.Hkv;
     pa.xcd_groups = groups % 8 == 0 ? groups / 8 : 0;
@@ -700,8 +719,11 @@ sa_status launch(PrefillArgs pa, int B, bool bf16, int D, hipStream_t st) {
     if (n_wg > 0x7fffffffLL) return fail(SA_ERANGE, "prefill grid too large");
     const dim3 grid(static_cast<unsigned>(n_wg));
     sa_status s = SA_OK;
-    if (bf16) {
+    if (bf16 && W == kBfW) {
         s = D == 64 ? launch_bf16<64, kBfQB, kBfW>(pa, grid, st) : launch_bf16<128, kBfQB, kBfW>(pa, grid, st);
+    } else if (bf16) {
+        s = D == 64 ? launch_bf16<64, kBfQB, kBfWSmall>(pa, grid, st)
+                    : launch_bf16<128, kBfQB, kBfWSmall>(pa, grid, st);
     } else if (D == 64) {
         s = opt_in_lds(&prefill_f32_kernel<64>, F32Lds<64>::BYTES);
         if (s == SA_OK)
