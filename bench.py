@@ -215,7 +215,11 @@ def cpu_model_decode(sum_len: int, B: int = 64, layers: int = 28, steps: int = 3
 
 def bench_cfg3(torch, sa, synth, steps_timed: int = 3):
     """One layer, B=1, 16 q / 8 KV heads, D=128: 128-token prompt, 100 steps of
-    fused norm + RoPE + append, paged decode, commit."""
+    fused norm + RoPE + append, paged decode, commit.  Eager: every step's
+    launches issued from the host.  Graph: the 100 steps captured once into a
+    HIP graph (each step's launch parameters are the ones the eager loop
+    uses) and replayed from the 128-token cache; every replay's per-step
+    outputs must equal the eager ones bit for bit."""
     HQ, HKV, D, P, N = 16, 8, 128, 128, 100
     res = {}
     for name, dt in (("fp32", sa.SA_DTYPE_F32), ("bf16", sa.SA_DTYPE_BF16)):
@@ -229,30 +233,59 @@ def bench_cfg3(torch, sa, synth, steps_timed: int = 3):
         kp = torch.from_numpy(synth.normal(40, 3, (1, P, HKV, D))).cuda()
         vp = torch.from_numpy(synth.normal(40, 4, (1, P, HKV, D))).cuda()
         ws = torch.zeros(max(cache.decode_ws_bytes(1, HQ), 1), dtype=torch.uint8, device="cuda")
-        out = torch.empty(1, HQ, D, device="cuda")
+        outs_e = torch.empty(N, 1, HQ, D, device="cuda")
+        outs_g = torch.empty(N, 1, HQ, D, device="cuda")
         qo = torch.empty(1, 1, HQ, D, device="cuda")
         sc = float(1 / np.sqrt(D))
-        walls = []
-        for rep in range(steps_timed + 1):
+
+        def prompt():
             cache.reset()
             cache.reserve(0, P + N)
             cache.append(0, None, kp, vp, None, wk, 1e-6, rope=(cos, sin))
             cache.commit(P, n_seqs=1)
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
+
+        def steps(outs):
             for t in range(N):
                 cache.append(0, q[t], k[t], v[t], wq, wk, 1e-6, rope=(cos, sin), q_out=qo)
-                cache.decode(0, qo.view(1, HQ, D), sc, n_pending=1, out=out, ws=ws)
+                cache.decode(0, qo.view(1, HQ, D), sc, n_pending=1, out=outs[t], ws=ws)
                 cache.commit(1, n_seqs=1)
+
+        walls = []
+        for rep in range(steps_timed + 1):
+            prompt()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            steps(outs_e)
             torch.cuda.synchronize()
             if rep:
                 walls.append(time.perf_counter() - t0)
-        cache.close()
         wall = statistics.median(walls)
+
+        prompt()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            steps(outs_g)
+        g_walls, exact = [], True
+        for rep in range(steps_timed + 1):
+            outs_g.zero_()
+            cache.set_len(0, P)          # the captured steps start from the prompt
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            graph.replay()
+            torch.cuda.synchronize()
+            if rep:
+                g_walls.append(time.perf_counter() - t0)
+            exact = exact and bool(torch.equal(outs_g, outs_e))
+        del graph
+        cache.close()
+        g_wall = statistics.median(g_walls)
         kv_bytes = sum(HKV * (P + t + 1) * D * 2 * (4 if name == "fp32" else 2) for t in range(N))
         res[name] = {"steps_per_s": round(N / wall, 1), "us_per_step": round(wall / N * 1e6, 2),
+                     "graph_steps_per_s": round(N / g_wall, 1), "graph_us_per_step": round(g_wall / N * 1e6, 2),
+                     "graph_equals_eager": exact,
                      "kv_read_bytes_100_steps": kv_bytes,
-                     "hbm_frac": round(kv_bytes / wall / 1e9 / HBM_PEAK_GBS, 5)}
+                     "hbm_frac": round(kv_bytes / g_wall / 1e9 / HBM_PEAK_GBS, 5)}
     return res
 
 
