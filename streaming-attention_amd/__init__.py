@@ -282,6 +282,22 @@ def rope_tables(max_pos: int, head_dim: int, theta: float = 1e6, device="cuda"):
     return cos, sin
 
 
+def qk_norm_rope(x, pos, norm_w=None, eps: float = 1e-6, rope=None, out=None, stream=None):
+    """Per-row RMSNorm (weights norm_w [D], or none) and rotate-half RoPE (rope =
+    (cos, sin) tables, or none) of x [..., D] fp32 at positions pos (int32
+    [rows]); out may alias x."""
+    import torch
+    D = x.shape[-1]
+    rows = x.numel() // D
+    if pos.dtype != torch.int32 or pos.numel() != rows:
+        raise ValueError("pos must be int32 with one entry per row")
+    out = torch.empty_like(x) if out is None else out
+    cos, sin = rope if rope is not None else (None, None)
+    check(lib().sa_qk_norm_rope(_ptr(_f32(x, "x")), rows, D, _ptr(pos), _ptr(norm_w), eps, _ptr(cos), _ptr(sin),
+                                cos.shape[0] if cos is not None else 0, _ptr(out), _stream(stream)))
+    return out
+
+
 # ---------------------------------------------------------------- prefill
 
 def prefill_causal(q, k, v, scale: float, out=None, stream=None):

@@ -300,3 +300,35 @@ def test_cache_errors(sa):
     assert cache.length(0) == 0
     cache.reserve(1, 6 * 64 - 64 * 2)              # pages are back after reset
     cache.close()
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("norm,rope", [(True, True), (True, False), (False, True), (False, False)])
+def test_qk_norm_rope_standalone(sa, oracle, synth, d, norm, rope):
+    """sa_qk_norm_rope against the oracle's RMSNorm and rotate-half RoPE; rows
+    whose position is outside the table stay unrotated; out may alias x."""
+    rows, max_pos = 300, 96
+    x = synth.normal(95, d, (rows, d))
+    w = (1 + synth.normal(95, d + 1, d, 0.1)).astype(np.float32)
+    pos = (np.arange(rows) * 7 % (max_pos + 20)).astype(np.int32)   # some beyond the table
+    cos, sin = sa.rope_tables(max_pos, d, 1e6)
+    ocos, osin = oracle.rope_tables(max_pos, d, 1e6)
+    want = oracle.rms_norm_rows(x, w, 1e-6) if norm else x.copy()
+    if rope:
+        inside = pos < max_pos
+        want[inside] = oracle.apply_rope(want[inside], pos[inside], ocos, osin)
+    xd = dev(x)
+    got = sa.qk_norm_rope(xd, dev(pos, np.int32), dev(w) if norm else None, 1e-6,
+                          rope=(cos, sin) if rope else None)
+    assert_f32(host(got), want)
+    sa.qk_norm_rope(xd, dev(pos, np.int32), dev(w) if norm else None, 1e-6,
+                    rope=(cos, sin) if rope else None, out=xd)
+    assert np.array_equal(host(xd), host(got))
+
+
+def test_qk_norm_rope_rejects(sa):
+    x = torch.zeros(4, 128, device="cuda")
+    with pytest.raises(ValueError):
+        sa.qk_norm_rope(x, torch.zeros(3, dtype=torch.int32, device="cuda"))
+    with pytest.raises(sa.SaError):
+        sa.qk_norm_rope(torch.zeros(4, 96, device="cuda"), torch.zeros(4, dtype=torch.int32, device="cuda"))
