@@ -451,6 +451,262 @@ prefill_bf16_kernel(PrefillArgs pa) {
 }
 
 // ===========================================================================
+// bf16 kernel, head_dim 128, tiles moved by the load unit
+// ===========================================================================
+// Same per-wave work as prefill_bf16_kernel (one 32-query block per wave, a
+// lazily raised running max), but tiles go from global memory straight into
+// LDS with global_load_lds_dwordx4: no staging registers, no LDS stores, no
+// V transposition on the way in.  K and V sit row-major in LDS (256-byte
+// rows) with the 16-byte chunks of row r permuted by dma_swz(r); the V^T
+// fragments of the PV product come from ds_read_b64_tr_b16.  NS stages: tile
+// kt + NS - 1 is loaded while tile kt is computed.  Tiles past the last one
+// are never loaded, so the stages of the last NS - 1 tiles are intact after
+// the loop; every wave's diagonal tile is among them (the launch checks that
+// a workgroup's queries span at most NS - 1 tiles) and is processed there,
+// which keeps the mask out of the main loop.
+constexpr int kDmaRowBytes = 256;                     // one row of 128 bf16
+constexpr int kDmaTileBytes = kKTile * kDmaRowBytes;  // one tensor's tile
+constexpr int kDmaStageBytes = 2 * kDmaTileBytes;     // K, then V
+
+// Chunk c (16 bytes) of tile row r sits at chunk position c ^ dma_swz(r) of
+// the row.  Exhaustive check over the lane patterns: the K fragment reads (16
+// lanes, 16 rows, one chunk) and the V transpose reads (32 lanes, 2 x 4 rows,
+// 4 chunks) touch 64 distinct banks per cycle.
+__device__ __forceinline__ int dma_swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) unsigned char lds_u8_t;
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+
+template <int W, int NS>
+__global__ void __launch_bounds__(W * 64)
+prefill_bf16_dma_kernel(PrefillArgs pa) {
+    constexpr int NKS = 8;          // k-steps of the score product
+    constexpr int NDB = 4;          // 32-row d blocks of O^T
+    constexpr int NI = 16 / W;      // loads per wave, tensor and tile (64 lanes x 16 bytes each)
+    extern __shared__ __align__(16) unsigned char smem[];
+    lds_u8_t* const lsm = (lds_u8_t*)smem;
+
+    const int L = pa.L;
+    const Work wk = map_work(pa, blockIdx.x);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = lane & 31;
+    const int hh = lane >> 5;
+    const float sl2 = pa.sl2;
+    if (W >= 8 && wave < W / 2) __builtin_amdgcn_s_setprio(1);   // as in prefill_bf16_kernel
+
+    const int wph = W / pa.gh;
+    const int qtile = wph * 32;
+    const int h = wk.h0 + wave / wph;
+    const uint16_t* Q = static_cast<const uint16_t*>(pa.q) + wk.b * pa.qs[0] + h * pa.qs[1];
+    const uint16_t* K = static_cast<const uint16_t*>(pa.k) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
+    const uint16_t* V = static_cast<const uint16_t*>(pa.v) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
+    const int kv_row = static_cast<int>(pa.kvs[2]);
+
+    const int q_wave0 = wk.qt * qtile + (wave % wph) * 32;
+    const int n_kt = (min(L, (wk.qt + 1) * qtile) - 1) / kKTile + 1;
+    const int wave_kt = q_wave0 < L ? (q_wave0 + 31) / kKTile + 1 : 0;
+
+    // Load i of this wave fills chunk positions 64 (wave NI + i) + lane of a
+    // tensor tile: row r = 4 (wave NI + i) + lane / 16, position lane % 16,
+    // which holds global chunk (lane % 16) ^ dma_swz(r).
+    int d_row[NI], d_col[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int r = 4 * (wave * NI + i) + lane / 16;
+        d_row[i] = r;
+        d_col[i] = 8 * ((lane % 16) ^ dma_swz(r & 15));
+    }
+    // Rows past the end of the sequence are clamped to the last row: they
+    // only feed keys that the causal mask removes.
+    auto dma_tile = [&](int kt, int stage) {
+        const int key0 = kt * kKTile;
+        lds_u8_t* sb = lsm + stage * kDmaStageBytes;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const long long e = (long long)min(key0 + d_row[i], L - 1) * kv_row + d_col[i];
+            lds_u8_t* dst = sb + (wave * NI + i) * 1024;
+            __builtin_amdgcn_global_load_lds(K + e, dst, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(V + e, dst + kDmaTileBytes, 16, 0, 0);
+        }
+    };
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s) dma_tile(s, s);
+
+    bf16x8_t qf[NKS];
+    {
+        const int qi = min(q_wave0 + n, L - 1);
+        const uint16_t* qrow = Q + qi * pa.qs[2] + 8 * hh;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+            const u32x4_t raw = *reinterpret_cast<const u32x4_t*>(qrow + ks * 16) ^ pa.q_sign;
+            qf[ks] = __builtin_bit_cast(bf16x8_t, raw);
+            asm("" : "+a"(qf[ks]));
+        }
+    }
+    f32x16_t acc[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) acc[db] = f32x16_t{};
+    float ms = -INFINITY, lp = 0.f;
+
+    // Fragment offsets (bytes within a stage).  K (score A operand): lane
+    // (n, hh) reads row swap_bits23(n) (+ 32 kb), chunk 2 ks + hh.  V^T (PV A
+    // operand): transpose read u of d block db; lane j of 16-lane group g
+    // addresses 4 bf16 of row 8 hh + 4 u + j / 4 (+ 16 t + 32 kb), columns
+    // 32 db + 16 (g % 2) + 4 (j % 4) .. + 3, and receives 4 consecutive keys
+    // of column 32 db + 16 (g % 2) + j.
+    int k_off[NKS];
+    {
+        const int r = swap_bits23(n);
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) k_off[ks] = r * kDmaRowBytes + (((2 * ks + hh) ^ dma_swz(r & 15)) << 4);
+    }
+    int v_off[2][NDB];
+    {
+        const int g = lane >> 4, j = lane & 15;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int r = 8 * hh + 4 * u + j / 4;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) {
+                const int col = 32 * db + 16 * (g & 1) + 4 * (j & 3);
+                v_off[u][db] = kDmaTileBytes + r * kDmaRowBytes + (((col >> 3) ^ dma_swz(r & 15)) << 4) + (col & 7) * 2;
+            }
+        }
+    }
+    auto lds_k = [&](const lds_u8_t* sb, int kb, int ks) {
+        return *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(sb + kb * 32 * kDmaRowBytes +
+                                                                                     k_off[ks]);
+    };
+    auto lds_vt = [&](const lds_u8_t* sb, int kb, int t, int db) {
+        const lds_u8_t* p = sb + (kb * 32 + t * 16) * kDmaRowBytes;
+        const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(p + v_off[0][db]));
+        const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(p + v_off[1][db]));
+        return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    };
+
+    // After this every wave has finished reading tile kt and tile kt + 1 is in
+    // LDS for all of them; tiles kt + 2 .. kt + NS - 1 (NS - 2 tiles of 2 NI
+    // loads per wave, issued later) may still be in flight.  The memory
+    // clobber keeps LDS accesses on their side of the barrier.
+    constexpr int VM = (NS - 2) * 2 * NI;
+    static_assert(VM == 0 || VM == 4 || VM == 8, "vmcnt literal");
+    auto next_tile_ready = [&]() {
+        if constexpr (VM == 0) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        else if constexpr (VM == 4) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+    next_tile_ready();   // tile 0
+
+    // One tile from stage sb, as two 32-key halves: scores, raise of the
+    // running max when it grew by more than 2^kHugeExcess, softmax, PV, lazy
+    // raise after the PV (exact, as in prefill_bf16_kernel).
+    auto tile = [&](int kt, const lds_u8_t* sb, auto diag_tag) {
+        constexpr bool DIAG = decltype(diag_tag)::value;
+        bf16x8_t kf[NKS];
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) kf[ks] = lds_k(sb, 0, ks);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            // element j of the score block: key kt*64 + 32 kb + 16 (j/8) + 8 hh + j%8, query q_wave0 + n
+            auto masked = [&](int j) {
+                return DIAG && kt * kKTile + 32 * kb + 16 * (j / 8) + 8 * hh + (j % 8) > q_wave0 + n;
+            };
+            f32x16_t s = {};
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qf[ks], s, 0, 0, 0);
+            if constexpr (DIAG) {
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    if (masked(j)) s[j] = -INFINITY;
+            }
+            bf16x8_t vf[NDB][2];
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int t = 0; t < 2; ++t) vf[db][t] = lds_vt(sb, kb, t, db);
+            float mt = s[0];
+#pragma unroll
+            for (int j = 1; j < 16; ++j) mt = fmaxf(mt, s[j]);
+            auto raise = [&]() {
+                // the other lane half holds the same query's other 16 keys
+                const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+                const float mq = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+                const float m_new = fmaxf(ms, mq * sl2);
+                const float alpha = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - m_new);
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) acc[db] *= alpha;
+                lp *= alpha;
+                ms = m_new;
+            };
+            if (__any(mt * sl2 > ms + kHugeExcess)) raise();
+            const float nm = -ms;
+            float p[16];
+            float rs = 0.f;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j], sl2, nm));
+                if (masked(j)) p[j] = 0.f;   // exact zero also for a zero scale
+                rs += p[j];
+            }
+            lp += rs;
+            bf16x8_t pb[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const bf16x2_t p01 = __builtin_convertvector(f32x2_t{p[8 * t + 0], p[8 * t + 1]}, bf16x2_t);
+                const bf16x2_t p23 = __builtin_convertvector(f32x2_t{p[8 * t + 2], p[8 * t + 3]}, bf16x2_t);
+                const bf16x2_t p45 = __builtin_convertvector(f32x2_t{p[8 * t + 4], p[8 * t + 5]}, bf16x2_t);
+                const bf16x2_t p67 = __builtin_convertvector(f32x2_t{p[8 * t + 6], p[8 * t + 7]}, bf16x2_t);
+                pb[t] = __builtin_bit_cast(
+                    bf16x8_t, make_uint4(__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23),
+                                         __builtin_bit_cast(uint32_t, p45), __builtin_bit_cast(uint32_t, p67)));
+            }
+            if (kb == 0) {
+#pragma unroll
+                for (int ks = 0; ks < NKS; ++ks) kf[ks] = lds_k(sb, 1, ks);
+            }
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+                    acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][t], pb[t], acc[db], 0, 0, 0);
+            if (__any(mt * sl2 > ms + kLazyRescale)) raise();
+        }
+    };
+
+    auto step = [&](int kt, int stage) {
+        const bool more = kt + NS - 1 < n_kt;
+        if (more) dma_tile(kt + NS - 1, (stage + NS - 1) % NS);   // into the stage tile kt - 1 used
+        if (kt + 1 < wave_kt) tile(kt, lsm + stage * kDmaStageBytes, std::false_type{});
+        if (more) next_tile_ready();
+        else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+    // Whole rounds of NS steps keep every stage index a constant; the extra
+    // steps past n_kt only synchronise.
+    const int n_steps = (n_kt + NS - 1) / NS * NS;
+    for (int kt = 0; kt < n_steps; kt += NS) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) step(kt + s, s);
+    }
+    if (wave_kt > 0) tile(wave_kt - 1, lsm + ((wave_kt - 1) % NS) * kDmaStageBytes, std::true_type{});
+
+    const float l = lp + __shfl_xor(lp, 32, 64);
+    const int qi = q_wave0 + n;
+    if (qi < L) {
+        const float inv = 1.0f / l;
+        float* orow = pa.out + wk.b * pa.os[0] + h * pa.os[1] + qi * pa.os[2] + 4 * hh;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+                *reinterpret_cast<float4*>(orow + 32 * db + 8 * jj) =
+                    make_float4(acc[db][4 * jj] * inv, acc[db][4 * jj + 1] * inv, acc[db][4 * jj + 2] * inv,
+                                acc[db][4 * jj + 3] * inv);
+    }
+}
+
+// ===========================================================================
 // fp32 kernel
 // ===========================================================================
 constexpr int kFQTile = 128;    // queries per workgroup
@@ -655,15 +911,15 @@ prefill_f32_kernel(PrefillArgs pa) {
 // ===========================================================================
 // Launch
 // ===========================================================================
-template <class Kernel>
-sa_status opt_in_lds(Kernel* kernel, int bytes) {
+// Dynamic LDS above 64 KiB needs a per-kernel, per-device opt-in.
+template <auto KERNEL>
+sa_status opt_in_lds(int bytes) {
     if (bytes <= 65536) return SA_OK;
-    // Tiles above 64 KiB of LDS need the per-device opt-in.
     static thread_local int opted_device = -1;
     int dev = 0;
     SA_HIP_TRY(hipGetDevice(&dev));
     if (opted_device != dev) {
-        SA_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+        SA_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(KERNEL),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
         opted_device = dev;
     }
@@ -673,12 +929,12 @@ sa_status opt_in_lds(Kernel* kernel, int bytes) {
 // bf16 shape: W waves of QB 32-query blocks each.  Measured at L = 8192
 // (16/8 heads) on MI355X, steady-state clocks: 8 waves x 32 queries (two
 // waves per SIMD, both query heads of a KV group per workgroup) 0.281 ms.
-// Slower alternatives: 4 waves x 64 queries with one block's softmax
-// hand-interleaved with the other's MFMAs; a phase-locked schedule in which
-// the two waves of a SIMD alternate between MFMA and softmax phases at
-// workgroup barriers (0.29-0.30 ms even without staging); a third LDS stage
-// for cross-tile fragment prefetch; the score product split into two
-// independent MFMA chains.
+// Slower alternatives: 4 waves x 64 queries (also with the O accumulators in
+// AGPRs); a phase-locked schedule in which the two waves of a SIMD alternate
+// between MFMA and softmax phases at workgroup barriers; the next half's
+// score MFMAs software-pipelined under the current half's softmax (with
+// sched_group_barrier interleaving, three LDS stages); the score product
+// split into two independent MFMA chains.
 constexpr int kBfQB = 1;
 constexpr int kBfW = 8;
 constexpr int kBfWSmall = 4;
@@ -686,9 +942,24 @@ constexpr int kBfWSmall = 4;
 template <int D, int QB, int W>
 sa_status launch_bf16(const PrefillArgs& pa, dim3 grid, hipStream_t st) {
     constexpr int bytes = BfLds<D, W>::BYTES;
-    sa_status s = opt_in_lds(&prefill_bf16_kernel<D, QB, W>, bytes);
+    sa_status s = opt_in_lds<&prefill_bf16_kernel<D, QB, W>>(bytes);
     if (s != SA_OK) return s;
     hipLaunchKernelGGL((prefill_bf16_kernel<D, QB, W>), grid, dim3(W * 64), bytes, st, pa);
+    return SA_OK;
+}
+
+// LDS stages of the load-unit kernel: three with 8 waves (one workgroup per
+// CU), two with 4 (two workgroups per CU fit in LDS).
+template <int W>
+constexpr int dma_stages() { return W == 8 ? 3 : 2; }
+
+template <int W>
+sa_status launch_bf16_dma(const PrefillArgs& pa, dim3 grid, hipStream_t st) {
+    constexpr int NS = dma_stages<W>();
+    constexpr int bytes = NS * kDmaStageBytes;
+    sa_status s = opt_in_lds<&prefill_bf16_dma_kernel<W, NS>>(bytes);
+    if (s != SA_OK) return s;
+    hipLaunchKernelGGL((prefill_bf16_dma_kernel<W, NS>), grid, dim3(W * 64), bytes, st, pa);
     return SA_OK;
 }
 
@@ -718,18 +989,26 @@ sa_status launch(PrefillArgs pa, int B, bool bf16, int D, hipStream_t st) {
     const long long n_wg = (long long)B * (pa.Hq / pa.gh) * pa.n_qt;
     if (n_wg > 0x7fffffffLL) return fail(SA_ERANGE, "prefill grid too large");
     const dim3 grid(static_cast<unsigned>(n_wg));
+    // head_dim 128 in bf16 uses the load-unit kernel when a workgroup's
+    // queries end in at most NS - 1 tiles (its diagonal tiles stay resident):
+    // GQA groups of 2 or more.  Measured against the register-staged kernel
+    // (16/8 heads): 1.01x at L = 8192, 1.08x .. 1.14x at L = 1024 .. 4096.
+    const bool dma = bf16 && D == 128 &&
+                     q_tile <= ((W == kBfW ? dma_stages<kBfW>() : dma_stages<kBfWSmall>()) - 1) * kKTile;
     sa_status s = SA_OK;
-    if (bf16 && W == kBfW) {
+    if (dma) {
+        s = W == kBfW ? launch_bf16_dma<kBfW>(pa, grid, st) : launch_bf16_dma<kBfWSmall>(pa, grid, st);
+    } else if (bf16 && W == kBfW) {
         s = D == 64 ? launch_bf16<64, kBfQB, kBfW>(pa, grid, st) : launch_bf16<128, kBfQB, kBfW>(pa, grid, st);
     } else if (bf16) {
         s = D == 64 ? launch_bf16<64, kBfQB, kBfWSmall>(pa, grid, st)
                     : launch_bf16<128, kBfQB, kBfWSmall>(pa, grid, st);
     } else if (D == 64) {
-        s = opt_in_lds(&prefill_f32_kernel<64>, F32Lds<64>::BYTES);
+        s = opt_in_lds<&prefill_f32_kernel<64>>(F32Lds<64>::BYTES);
         if (s == SA_OK)
             hipLaunchKernelGGL(prefill_f32_kernel<64>, grid, dim3(kFThreads), F32Lds<64>::BYTES, st, pa);
     } else {
-        s = opt_in_lds(&prefill_f32_kernel<128>, F32Lds<128>::BYTES);
+        s = opt_in_lds<&prefill_f32_kernel<128>>(F32Lds<128>::BYTES);
         if (s == SA_OK)
             hipLaunchKernelGGL(prefill_f32_kernel<128>, grid, dim3(kFThreads), F32Lds<128>::BYTES, st, pa);
     }

@@ -106,12 +106,15 @@ def test_prefill_last_row_is_decode(sa, synth):
 
 @pytest.mark.parametrize("waves", ["4", "8"])
 @pytest.mark.parametrize("Hq,Hkv,D,L", [(4, 4, 128, 300), (8, 2, 128, 513), (16, 8, 64, 300),
-                                        (2, 1, 64, 700), (16, 16, 128, 257)])
+                                        (2, 1, 64, 700), (16, 16, 128, 257), (16, 8, 128, 300),
+                                        (32, 4, 128, 200)])
 def test_prefill_bf16_shapes(sa, oracle, synth, monkeypatch, Hq, Hkv, D, L, waves):
     """bf16 at other head layouts, D = 64, batch 2, L off the tile sizes; 16/8
     heads at batch 2 also exercise the per-XCD mapping of KV groups.  Both
     workgroup sizes (the launch picks 4 waves for grids that would not fill
-    the CUs twice, 8 otherwise) run every shape."""
+    the CUs twice, 8 otherwise) run every shape.  D = 128 with GQA groups of
+    2 or more runs the kernel that loads tiles straight into LDS; D = 64 and
+    the group of 1 run the register-staged one."""
     monkeypatch.setenv("SA_PREFILL_WAVES", waves)
     q, k, v = inputs(synth, L, Hq, Hkv, D, seed=55)
     q2 = synth.bf16_round(np.concatenate([q, synth.normal(56, 1, q.shape)], 0))
