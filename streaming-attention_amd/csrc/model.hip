@@ -148,61 +148,113 @@ embed_norm_kernel(const uint16_t* embed, const int32_t* tokens, int vocab, int H
 // GEMM: P[s][m][n] = sum over k in split s of X[m][k] * W[n][k].
 // X fp32 [M][K], W bf16 [N][K]; N % 64 == 0, split % 32 == 0.
 // Workgroup (x, y, z) owns rows 64 z .. 64 z + 63 (rows past M read as zero),
-// columns 64 x .. 64 x + 63 and split y;
-// wave w computes the 32 x 32 block (rows 32 (w / 2), columns 32 (w % 2))
-// with v_mfma_f32_32x32x2f32: exact fp32 products of the activations and the
-// widened bf16 weights, fp32 accumulation.  32-wide k chunks go through LDS
-// k-major, so lane l's operands X[m = l % 32][k] and W[n = l % 32][k] for
-// k = l / 32 are consecutive words across lanes.
+// columns 64 x .. 64 x + 63 and split y; wave w computes columns
+// 64 x + 16 w .. + 15 for all 64 rows with v_mfma_f32_16x16x32_bf16.
+//
+// The bf16 MFMA takes fp32 X as kGemmTerms bf16 terms: t_0 = rne(x),
+// t_i = rne(x - t_0 - ... - t_{i-1}) (each difference is exact in fp32), so
+// |x - sum t_i| <= 2^-9(kGemmTerms) |x|.  Every product t_i * w is exact in
+// fp32 (the weights are bf16) and accumulates in fp32: the result is the fp32
+// GEMM's to within that truncation of X.  Per 32-wide k step the workgroup
+// converts its 64 x 32 block of X into LDS (double-buffered, one barrier per
+// step); W fragments stream from global memory into registers kGemmRing steps
+// ahead of their use.
 // ---------------------------------------------------------------------------
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kGemmTerms = 3;     // bf16 terms of each activation (2^-27 |x| left over)
+constexpr int kGemmRing = 8;      // W fragments in flight per wave (k steps)
+constexpr int kGemmXStride = kGK + 8;   // bf16 per LDS row of X: conflict-free fragment reads
 
 __global__ void __launch_bounds__(256)
 gemm_xwt_kernel(const float* __restrict__ X, int M, int K, const uint16_t* __restrict__ W, int N, int split,
                 float* __restrict__ P) {
-    __shared__ __align__(16) float Xs[kGK][kMaxRows + 4];
-    __shared__ __align__(16) float Ws[kGK][kGN + 4];
+    __shared__ __align__(16) uint16_t Xb[2][kGemmTerms][kMaxRows][kGemmXStride];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int mb = (wave >> 1) * 32, nb = (wave & 1) * 32;
-    const int row = lane & 31, kh = lane >> 5;
-    const int n0 = blockIdx.x * kGN;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.x * kGN + 16 * wave;
     const int k_begin = blockIdx.y * split;
     const int m0 = blockIdx.z * kMaxRows;
-    const float* Xt = X + (size_t)m0 * K;
-    const int Mt = M - m0;   // rows of this tile that exist
-    f32x16_t acc = {};
-    for (int k0 = k_begin; k0 < k_begin + split; k0 += kGK) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int idx = tid + i * 256, r = idx >> 3, c = (idx & 7) * 4;
-            float4 xv = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (r < Mt) xv = *reinterpret_cast<const float4*>(Xt + (size_t)r * K + k0 + c);
-            Xs[c + 0][r] = xv.x;
-            Xs[c + 1][r] = xv.y;
-            Xs[c + 2][r] = xv.z;
-            Xs[c + 3][r] = xv.w;
+    const int Mt = min(M - m0, kMaxRows);
+    const int nsteps = split / kGK;
+
+    // W fragment of step j (A operand): lane (r16, g) holds W[n0 + r16][k + 8 g .. + 7].
+    const uint16_t* Wl = W + (size_t)(n0 + r16) * K + k_begin + 8 * g;
+    auto load_w = [&](int j) { return *reinterpret_cast<const bf16x8_t*>(Wl + j * kGK); };
+    // X block of step j: thread t converts X[m0 + t / 4][k + 8 (t % 4) .. + 7].
+    const int xr = tid >> 2, xc = 8 * (tid & 3);
+    const bool x_on = xr < Mt;
+    const float* Xl = X + (size_t)(m0 + xr) * K + k_begin + xc;
+    auto load_x = [&](int j, f32x4_t& a, f32x4_t& b) {
+        if (x_on) {
+            a = *reinterpret_cast<const f32x4_t*>(Xl + j * kGK);
+            b = *reinterpret_cast<const f32x4_t*>(Xl + j * kGK + 4);
+        } else {
+            a = f32x4_t{};
+            b = f32x4_t{};
         }
-        {
-            const int nn = tid >> 2, c = (tid & 3) * 8;
-            const u32x4_t wv = *reinterpret_cast<const u32x4_t*>(W + (size_t)(n0 + nn) * K + k0 + c);
+    };
+    auto store_x = [&](int buf, f32x4_t a, f32x4_t b) {
+        f32x2_t v[4] = {{a[0], a[1]}, {a[2], a[3]}, {b[0], b[1]}, {b[2], b[3]}};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                Ws[c + 2 * j][nn] = bf16_lo(wv[j]);
-                Ws[c + 2 * j + 1][nn] = bf16_hi(wv[j]);
+        for (int t = 0; t < kGemmTerms; ++t) {
+            u32x4_t packed;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const bf16x2_t h = __builtin_convertvector(v[e], bf16x2_t);
+                const uint32_t bits = __builtin_bit_cast(uint32_t, h);
+                packed[e] = bits;
+                v[e] -= f32x2_t{bf16_lo(bits), bf16_hi(bits)};
+            }
+            *reinterpret_cast<u32x4_t*>(&Xb[buf][t][xr][xc]) = packed;
+        }
+    };
+
+    bf16x8_t ring[kGemmRing];
+#pragma unroll
+    for (int u = 0; u < kGemmRing; ++u)
+        if (u < nsteps) ring[u] = load_w(u);
+    // acc[mt]: element i is row m0 + 16 mt + r16, column n0 + 4 g + i
+    f32x4_t acc[kMaxRows / 16] = {};
+    auto mfma_step = [&](const bf16x8_t& wf, int buf) {
+#pragma unroll
+        for (int mt = 0; mt < kMaxRows / 16; ++mt)
+#pragma unroll
+            for (int t = 0; t < kGemmTerms; ++t) {
+                const bf16x8_t xf = *reinterpret_cast<const bf16x8_t*>(&Xb[buf][t][16 * mt + r16][8 * g]);
+                acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf, xf, acc[mt], 0, 0, 0);
+            }
+    };
+    f32x4_t xa, xb;
+    load_x(0, xa, xb);
+    store_x(0, xa, xb);
+    __syncthreads();
+
+    for (int j0 = 0; j0 < nsteps; j0 += kGemmRing) {
+#pragma unroll
+        for (int u = 0; u < kGemmRing; ++u) {
+            const int j = j0 + u;
+            if (j < nsteps) {
+                const int buf = u & 1;   // kGemmRing is even, so j & 1 == u & 1
+                if (j + 1 < nsteps) load_x(j + 1, xa, xb);
+                const bf16x8_t wf = ring[u];
+                if (j + kGemmRing < nsteps) ring[u] = load_w(j + kGemmRing);
+                mfma_step(wf, buf);
+                // the other buffer was last read before the previous barrier
+                if (j + 1 < nsteps) store_x(buf ^ 1, xa, xb);
+                __syncthreads();
             }
         }
-        __syncthreads();
-#pragma unroll
-        for (int kk = 0; kk < kGK; kk += 2)
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(Xs[kk + kh][mb + row], Ws[kk + kh][nb + row], acc, 0, 0, 0);
-        __syncthreads();
     }
-    // element j of acc: row mb + 8 (j / 4) + 4 kh + j % 4, column nb + row
-    float* out = P + (size_t)blockIdx.y * M * N + (size_t)m0 * N + n0 + nb + row;
+    float* out = P + (size_t)blockIdx.y * M * N + (size_t)m0 * N + n0 + 4 * g;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const int m = mb + 8 * (j >> 2) + 4 * kh + (j & 3);
-        if (m < Mt) out[(size_t)m * N] = acc[j];
+    for (int mt = 0; mt < kMaxRows / 16; ++mt) {
+        const int m = 16 * mt + r16;
+        if (m < Mt) *reinterpret_cast<f32x4_t*>(out + (size_t)m * N) = acc[mt];
     }
 }
 
