@@ -499,7 +499,7 @@ def copy_calibration(torch, nbytes: int = 1 << 30, steps: int = 5):
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", choices=["headline", "all", "single", "layer", "paged", "prefill", "model"],
                     default="all",
