@@ -117,6 +117,10 @@ sa_status sa_kvcache_set_pages(sa_kvcache* cache, int seq, const int32_t* pages,
 sa_status sa_kvcache_set_len(sa_kvcache* cache, int seq, int len, sa_stream_t stream);
 /* Committed length of seq as tracked on the host, or -1. */
 int sa_kvcache_len(const sa_kvcache* cache, int seq);
+/* Tokens the pages assigned to seq can hold (64 per page), or -1.  No
+ * counterpart in the reference, whose dense cache has one fixed capacity
+ * (tensor_cpp/include/tensor_cpp/kv_cache.h:47-86). */
+int sa_kvcache_capacity(const sa_kvcache* cache, int seq);
 /* Add n to the committed length of seqs[0..n_seqs) (host ids; NULL = 0..n_seqs-1). */
 sa_status sa_kvcache_commit(sa_kvcache* cache, const int32_t* seqs, int n_seqs, int n,
                             sa_stream_t stream);

@@ -73,6 +73,7 @@ SIGNATURES = {
     "sa_kvcache_set_pages": (_I, [_P, _I, _P, _I]),
     "sa_kvcache_set_len": (_I, [_P, _I, _I, _P]),
     "sa_kvcache_len": (_I, [_P, _I]),
+    "sa_kvcache_capacity": (_I, [_P, _I]),
     "sa_kvcache_commit": (_I, [_P, _P, _I, _I, _P]),
     "sa_kvcache_k_pool": (_P, [_P, _I]),
     "sa_kvcache_v_pool": (_P, [_P, _I]),
@@ -215,6 +216,10 @@ class KVCache:
 
     def length(self, seq: int) -> int:
         return lib().sa_kvcache_len(self.handle, seq)
+
+    def capacity(self, seq: int) -> int:
+        """Tokens the pages assigned to seq can hold, or -1."""
+        return lib().sa_kvcache_capacity(self.handle, seq)
 
     def commit(self, n: int, seqs=None, n_seqs: int | None = None, stream=None) -> None:
         if seqs is None:

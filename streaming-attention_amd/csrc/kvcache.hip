@@ -423,6 +423,11 @@ extern "C" int sa_kvcache_len(const sa_kvcache* c, int seq) {
     return c->h_lens[seq];
 }
 
+extern "C" int sa_kvcache_capacity(const sa_kvcache* c, int seq) {
+    if (!valid_cache(c) || seq < 0 || seq >= c->desc.max_seqs) return -1;
+    return c->h_npages[seq] * 64;
+}
+
 extern "C" sa_status sa_kvcache_commit(sa_kvcache* c, const int32_t* seqs, int n_seqs, int n,
                                        sa_stream_t stream) {
     clear_error();

@@ -726,6 +726,7 @@ extern "C" sa_status sa_qwen3_decode_step(sa_qwen3* m, sa_kvcache* cache, const 
     for (int i = 0; i < batch; ++i) {
         const int len = sa_kvcache_len(cache, i);
         if (len < 0 || len >= d.max_pos) return fail(SA_ERANGE, "position outside the RoPE table");
+        if (len + 1 > sa_kvcache_capacity(cache, i)) return fail(SA_EFULL, "KV cache full, cannot append more tokens");
     }
     hipStream_t st = as_stream(stream);
     const size_t need = sa_paged_decode_ws_bytes(cache, batch, d.n_q_heads);

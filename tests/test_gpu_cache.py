@@ -282,6 +282,8 @@ def test_cache_errors(sa):
         cache.reserve(0, 4 * 64 + 1)               # beyond the table row
     assert e.value.status == sa.SA_EFULL
     cache.reserve(0, 4 * 64)
+    assert cache.capacity(0) == 4 * 64 and cache.capacity(1) == 0
+    assert cache.capacity(2) == -1                 # no such sequence
     with pytest.raises(sa.SaError) as e:
         cache.reserve(1, 3 * 64)                   # only 2 pages left in the pool
     assert e.value.status == sa.SA_EFULL
@@ -297,7 +299,7 @@ def test_cache_errors(sa):
     with pytest.raises(sa.SaError):
         cache.set_pages(1, [99])                   # page id out of range
     cache.reset()
-    assert cache.length(0) == 0
+    assert cache.length(0) == 0 and cache.capacity(0) == 0
     cache.reserve(1, 6 * 64 - 64 * 2)              # pages are back after reset
     cache.close()
 

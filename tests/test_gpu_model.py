@@ -169,6 +169,10 @@ def test_model_rejects_bad_calls(sa):
     good = sa.KVCache(SMALL["num_layers"], SMALL["n_kv_heads"], SMALL["head_dim"], 4, 2, 8)
     with pytest.raises(sa.SaError, match="batch"):
         model.decode_step(good, big)
+    good.reserve(0, 64)                                    # seq 1 has no page for its token
+    with pytest.raises(sa.SaError, match="full") as e:
+        model.decode_step(good, tok)
+    assert e.value.status == sa.SA_EFULL and good.length(0) == 0 and good.length(1) == 0
     d = sa.Qwen3Desc(1, 100, 64, 64, 2, 1, 64, 16, 1e-6, 1e6)   # hidden not a multiple of 64
     h = C.c_void_p()
     assert sa.lib().sa_qwen3_create(C.byref(d), 1, C.byref(h)) == sa.SA_EINVAL
