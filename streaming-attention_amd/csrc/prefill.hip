@@ -478,6 +478,18 @@ typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) unsigned char lds_u8_t;
 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 
+// One global_load_lds_dwordx4: lane l copies 16 bytes from g into LDS at dst
+// + 16 l.  Issued as inline assembly so that the compiler does not track it:
+// its wait-count pass makes every LDS read after a load-to-LDS wait for all
+// of them (vmcnt(0)), which would drain the tile prefetched NS - 1 tiles ahead
+// in the middle of each tile.  The kernel waits for these loads itself
+// (s_waitcnt vmcnt before each tile barrier).  m0 holds the LDS address; the
+// s_nop covers the m0-write-to-load-to-LDS hazard.
+__device__ __forceinline__ void dma16(const uint16_t* g, lds_u8_t* dst) {
+    const uint32_t m = static_cast<uint32_t>(reinterpret_cast<size_t>(dst));
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m) : "memory", "m0");
+}
+
 template <int W, int NS>
 __global__ void __launch_bounds__(W * 64)
 prefill_bf16_dma_kernel(PrefillArgs pa) {
@@ -527,8 +539,8 @@ prefill_bf16_dma_kernel(PrefillArgs pa) {
         for (int i = 0; i < NI; ++i) {
             const long long e = (long long)min(key0 + d_row[i], L - 1) * kv_row + d_col[i];
             lds_u8_t* dst = sb + (wave * NI + i) * 1024;
-            __builtin_amdgcn_global_load_lds(K + e, dst, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(V + e, dst + kDmaTileBytes, 16, 0, 0);
+            dma16(K + e, dst);
+            dma16(V + e, dst + kDmaTileBytes);
         }
     };
 #pragma unroll
@@ -540,9 +552,10 @@ prefill_bf16_dma_kernel(PrefillArgs pa) {
         const uint16_t* qrow = Q + qi * pa.qs[2] + 8 * hh;
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) {
+            // Q stays in arch VGPRs: any AGPR use caps arch VGPRs at 128 and
+            // the LDS addresses would then be kept in AGPRs.
             const u32x4_t raw = *reinterpret_cast<const u32x4_t*>(qrow + ks * 16) ^ pa.q_sign;
             qf[ks] = __builtin_bit_cast(bf16x8_t, raw);
-            asm("" : "+a"(qf[ks]));
         }
     }
     f32x16_t acc[NDB];
