@@ -55,9 +55,6 @@ struct Geo {
 template <int D, int NREP>
 constexpr int waves_for() { return 4; }
 constexpr int kWavesOneRound = 8;
-// Workgroups per (sequence, head) of the merge when the heads alone leave
-// most CUs idle (single-head decode).
-constexpr int kMergeSlices = 8;
 
 struct DecodeArgs {
     const float* q;          // [n_seq][n_q_heads][D]
@@ -369,15 +366,11 @@ split_kv_decode_kernel(DecodeArgs a) {
 // need a device-scope fence per workgroup (measured at ~57 ns each,
 // serialised across the device).  MT threads read the partials as float4
 // columns, PARTS chunks at a time, so one round trip covers up to MT/(D/4)
-// chunks.  With DS > 1, workgroup (bh, y) merges only the float4 columns of
-// slice y of D: DS workgroups share one (sequence, head) when there are too
-// few of those to occupy the device, and each reads 1/DS of the partials.
-template <int D, bool PAGED, int MT, int DS>
+// chunks.
+template <int D, bool PAGED, int MT>
 __global__ void __launch_bounds__(MT)
 lse_merge_kernel(DecodeArgs a) {
-    static_assert(D % (4 * DS) == 0, "slice of whole float4 columns");
-    constexpr int ROW4 = D / 4;          // float4 per partial row
-    constexpr int V4 = ROW4 / DS;        // float4 columns of this workgroup
+    constexpr int V4 = D / 4;
     constexpr int PARTS = MT / V4;
     const int bh = blockIdx.x;
     const int seq = bh / a.n_q;
@@ -394,7 +387,7 @@ lse_merge_kernel(DecodeArgs a) {
     __shared__ float4 sh_red[PARTS][V4];
     __shared__ float sh_scr[MT / kWave];
     const float* ml = a.part_ml + (size_t)bh * a.n_split * 2;
-    const float4* po = reinterpret_cast<const float4*>(a.part_o + (size_t)bh * a.n_split * D) + blockIdx.y * V4;
+    const float4* po = reinterpret_cast<const float4*>(a.part_o + (size_t)bh * a.n_split * D);
     const int j = threadIdx.x % V4;
     const int part = threadIdx.x / V4;
     // The first NPRE partial rows of this thread are loaded before the
@@ -404,7 +397,7 @@ lse_merge_kernel(DecodeArgs a) {
 #pragma unroll
     for (int k = 0; k < NPRE; ++k) {
         const int c = part + k * PARTS;
-        pre[k] = c < n_active ? po[(size_t)c * ROW4 + j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        pre[k] = c < n_active ? po[(size_t)c * V4 + j] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     float mx = -INFINITY;
     for (int c = threadIdx.x; c < n_active; c += MT) mx = fmaxf(mx, ml[2 * c]);
@@ -428,7 +421,7 @@ lse_merge_kernel(DecodeArgs a) {
     }
 #pragma unroll 4
     for (int c = part + NPRE * PARTS; c < n_active; c += PARTS) {
-        const float4 x = po[(size_t)c * ROW4 + j];
+        const float4 x = po[(size_t)c * V4 + j];
         const float w = sh_w[c];
         acc.x = fmaf(w, x.x, acc.x); acc.y = fmaf(w, x.y, acc.y);
         acc.z = fmaf(w, x.z, acc.z); acc.w = fmaf(w, x.w, acc.w);
@@ -443,7 +436,7 @@ lse_merge_kernel(DecodeArgs a) {
             t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
         }
         const float inv = 1.0f / ls;
-        reinterpret_cast<float4*>(a.out + (size_t)bh * D)[blockIdx.y * V4 + j] =
+        reinterpret_cast<float4*>(a.out + (size_t)bh * D)[j] =
             make_float4(t.x * inv, t.y * inv, t.z * inv, t.w * inv);
     }
 }
@@ -522,14 +515,11 @@ sa_status launch_decode(const DecodeArgs& a, int n_seq, hipStream_t st) {
     }
     SA_CHECK_LAUNCH();
     if (a.n_split > 1) {
-        const int bh = n_seq * a.n_q;
-        if ((long long)bh * kMergeSlices <= device_cu_count())
-            hipLaunchKernelGGL((lse_merge_kernel<D, PAGED, 256, kMergeSlices>), dim3(bh, kMergeSlices), dim3(256), 0,
-                               st, a);
-        else if (a.n_split >= 64)
-            hipLaunchKernelGGL((lse_merge_kernel<D, PAGED, 1024, 1>), dim3(bh), dim3(1024), 0, st, a);
+        const dim3 mgrid(n_seq * a.n_q);
+        if (a.n_split >= 64)
+            hipLaunchKernelGGL((lse_merge_kernel<D, PAGED, 1024>), mgrid, dim3(1024), 0, st, a);
         else
-            hipLaunchKernelGGL((lse_merge_kernel<D, PAGED, 256, 1>), dim3(bh), dim3(256), 0, st, a);
+            hipLaunchKernelGGL((lse_merge_kernel<D, PAGED, 256>), mgrid, dim3(256), 0, st, a);
         SA_CHECK_LAUNCH();
     }
     return SA_OK;
