@@ -41,7 +41,8 @@ DEVICE = [
 
 
 # Per-file device flags.  The prefill kernels keep MFMA accumulators in arch
-# VGPRs (their softmax rescales them with VALU ops) and park Q in AGPRs.
+# VGPRs (their softmax rescales them with VALU ops); the register-staged bf16
+# kernel parks Q in AGPRs.
 EXTRA = {
     "prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
