@@ -183,7 +183,7 @@ def _cpu_threads() -> int:
 
 
 def cpu_layer_decode(steps: int = 100, warm: int = 2):
-    """Config 3 on the CPU: the reference's qwen3_decoder_layer_avx_with_cache
+    """The one-layer decode loop on the CPU: the reference's qwen3_decoder_layer_avx_with_cache
     (STREAMING) for 100 one-token steps after a 128-token cache, 16/8 heads,
     D=128.  Hidden size and MLP width are 8, so the projections are negligible
     and the call is the attention path: q/k norm, RoPE, the cache read + concat
@@ -199,7 +199,7 @@ def cpu_layer_decode(steps: int = 100, warm: int = 2):
 
 
 def cpu_prefill(L: int):
-    """Config 4 on the CPU: the reference's
+    """Causal prefill on the CPU: the reference's
     self_attention_streaming_blockwise_avx2 with q and kv blocks of 128 (the
     benchmark's setting), 16 heads over repeat_kv'd K/V, fp32."""
     from oracle import Reference
@@ -226,7 +226,7 @@ def cpu_prefill(L: int):
 
 
 def cpu_model_decode(sum_len: int, B: int = 64, layers: int = 28, steps: int = 3):
-    """Config 5 on the CPU, extrapolated: one reference decoder layer
+    """The 28-layer batched decode on the CPU, extrapolated: one reference decoder layer
     (qwen3_decoder_layer_avx_with_cache, STREAMING, Qwen3-0.6B shapes) on one
     sequence at the batch's mean context length, times 28 layers.  The
     reference's cache has one length for the whole batch, so the batch of
@@ -245,7 +245,7 @@ def cpu_model_decode(sum_len: int, B: int = 64, layers: int = 28, steps: int = 3
 
 # ---------------------------------------------------------------- extra configs
 
-def bench_cfg3(torch, sa, synth, steps_timed: int = 3):
+def bench_layer_decode_loop(torch, sa, synth, steps_timed: int = 3):
     """One layer, B=1, 16 q / 8 KV heads, D=128: 128-token prompt, 100 steps of
     fused norm + RoPE + append, paged decode, commit.  Eager: every step's
     launches issued from the host.  Graph: the 100 steps captured once into a
@@ -537,7 +537,7 @@ def main() -> int:
     extra = {}
     run = (lambda name: True) if args.only == "all" else (lambda name: name == args.only)
     if run("single"):
-        log("[bench] single-head T=1024 (config 1)")
+        log("[bench] single-head T=1024")
         c1, _ = bench_stream(torch, sa, synth, 1024, 200, 20, min_footprint=1.1e9)
         extra["single_head_T1024"] = {k: c1[k] for k in ("kernel_ms", "gbs", "max_abs_err", "rel_l2_err")}
         extra["single_head_T1024"]["hbm_frac"] = round(c1["gbs"] / HBM_PEAK_GBS, 5)
@@ -550,25 +550,25 @@ def main() -> int:
     from oracle import Reference
     cpu_extra = args.cpu_budget >= 1.0 and Reference.available()
     if run("layer"):
-        log("[bench] one-layer Qwen3 decode loop (config 3)")
-        extra["qwen3_layer_decode_loop"] = bench_cfg3(torch, sa, synth)
+        log("[bench] one-layer Qwen3 decode loop")
+        extra["qwen3_layer_decode_loop"] = bench_layer_decode_loop(torch, sa, synth)
         if cpu_extra:
             log("[bench] CPU: reference decoder layer, attention path, 100 steps")
             extra["qwen3_layer_decode_loop"]["cpu_baseline"] = cpu_layer_decode()
     if run("paged"):
-        log("[bench] batched paged GQA decode, 64 sequences, bf16 KV (config 5 attention)")
+        log("[bench] batched paged GQA decode, 64 sequences, bf16 KV")
         extra["paged_decode_b64_bf16"] = bench_paged_batch(torch, sa, synth)
     if run("prefill"):
         for L in (int(x) for x in args.prefill_lens.split(",")):
             for bf in (d == "bf16" for d in args.prefill_dtypes.split(",")):
-                log(f"[bench] causal prefill L={L} {'bf16' if bf else 'fp32'} (config 4)")
+                log(f"[bench] causal prefill L={L} {'bf16' if bf else 'fp32'}, 16/8 heads, D=128")
                 extra[f"prefill_L{L}_{'bf16' if bf else 'f32'}"] = bench_prefill(torch, sa, synth, L, bf)
             if cpu_extra:
                 log(f"[bench] CPU: reference blockwise AVX2 prefill L={L}")
                 extra[f"prefill_L{L}_cpu_baseline"] = cpu_prefill(L)
     if run("model"):
         torch.cuda.empty_cache()
-        log("[bench] 28-layer Qwen3-0.6B-shape greedy decode, 64 sequences, bf16 KV (config 5)")
+        log("[bench] 28-layer Qwen3-0.6B-shape greedy decode, 64 sequences, bf16 KV")
         extra["qwen3_model_decode_b64"] = bench_model_decode(torch, sa, synth)
         if cpu_extra:
             log("[bench] CPU: reference decoder layer at the mean context length")

@@ -44,9 +44,9 @@ def save(name: str, meta: dict, **arrays) -> None:
 def main() -> None:
     ref = Reference()
 
-    # Single-query streaming attention, BASELINE config 1 and the reference's
+    # Single-query streaming attention (T = 1024, d = 128) and the reference's
     # unit-test grid (tensor_cpp/tests/unit/test_streaming_attention.cpp:65-108).
-    Q, K, V = gi.cfg1_inputs()
+    Q, K, V = gi.t1024_inputs()
     scale = np.float32(1.0 / np.sqrt(128.0))
     out = {}
     for blk in (64, 128):
@@ -54,7 +54,7 @@ def main() -> None:
         out[f"serial_scaled_b{blk}"] = ref.streaming_serial(Q * scale, K, V, blk)
     out["naive"] = ref.naive_serial(Q, K, V)
     out["omp_b64_t4"] = ref.streaming_omp(Q, K, V, 64, 4)
-    save("stream_cfg1", {"inputs_sha256": digest(Q, K, V), "T": 1024, "d": 128}, **out)
+    save("stream_t1024", {"inputs_sha256": digest(Q, K, V), "T": 1024, "d": 128}, **out)
 
     out = {}
     for T, d in gi.UNIT_GRID:
@@ -64,11 +64,11 @@ def main() -> None:
 
     out, sha = {}, {}
     for T in (8192, 65536):
-        Q2, K2, V2 = gi.cfg2_inputs(T)
+        Q2, K2, V2 = gi.long_inputs(T)
         sha[str(T)] = digest(Q2, K2, V2)
         for blk in (64, 128):
             out[f"serial_T{T}_b{blk}"] = ref.streaming_serial(Q2, K2, V2, blk)
-    save("stream_cfg2", {"inputs_sha256": sha}, **out)
+    save("stream_long", {"inputs_sha256": sha}, **out)
 
     # RoPE tables at theta 1e6 (tensor_cpp/src/qwen3_ops.cpp:70-104), sampled rows.
     cos, sin = ref.rope_freqs(gi.ROPE_MAX_POS, 128, 1e6)

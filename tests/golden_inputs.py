@@ -18,12 +18,12 @@ PREFILL_ROWS = [0, 1, 2, 31, 32, 33, 63, 64, 65, 127, 128, 150, 191, 199]
 LAYER_PROMPT = 8
 
 
-def cfg1_inputs():
+def t1024_inputs():
     """Single head, T=1024, d=128, i.i.d. N(0,1)."""
     return synth.stream_inputs(1024, 128, seed=1)
 
 
-def cfg2_inputs(T: int):
+def long_inputs(T: int):
     """d=128, 0.5 N(0,1), 1% of K rows x8 (the long-context outlier workload)."""
     return synth.stream_inputs(T, 128, seed=2, scale=0.5, outlier_frac=0.01)
 

@@ -153,7 +153,7 @@ def test_paged_decode_seq_ids_subset(sa, oracle, synth):
     cache.close()
 
 
-def run_cfg3(sa, synth, bf16, steps=100, prompt=128, seed=40):
+def run_layer_decode_loop(sa, synth, bf16, steps=100, prompt=128, seed=40):
     """One layer, B=1, 16q/8kv, D=128: prompt append, then `steps` decode steps.
     Returns (GPU outputs [steps, 16, 128], the dense fp32 K/V the oracle needs,
     the roped q of each step)."""
@@ -185,9 +185,9 @@ def run_cfg3(sa, synth, bf16, steps=100, prompt=128, seed=40):
             (kp, vp, q_all, k_all, v_all, host(wq), host(wk)))
 
 
-def test_cfg3_decode_loop_fp32(sa, oracle, synth):
+def test_layer_decode_loop_fp32(sa, oracle, synth):
     prompt, steps = 128, 100
-    outs, gk, gv, qs, raw = run_cfg3(sa, synth, False, steps, prompt)
+    outs, gk, gv, qs, raw = run_layer_decode_loop(sa, synth, False, steps, prompt)
     kp, vp, q_all, k_all, v_all, wq, wk = raw
     cos, sin = oracle.rope_tables(prompt + steps, D, 1e6)
     # oracle K/V: normed + roped keys at their positions, raw values
@@ -207,12 +207,12 @@ def test_cfg3_decode_loop_fp32(sa, oracle, synth):
         assert_f32(outs[t], want)
 
 
-def test_cfg3_decode_loop_bf16(sa, oracle, synth):
+def test_layer_decode_loop_bf16(sa, oracle, synth):
     """bf16 KV: relative L2 <= 2e-2 per step, and a greedy readout of the
     attention output (fixed random projection to 512 logits) picks the same
     token as the oracle on the same bf16 K/V for 32 steps."""
     prompt, steps = 128, 32
-    outs, gk, gv, qs, raw = run_cfg3(sa, synth, True, steps, prompt)
+    outs, gk, gv, qs, raw = run_layer_decode_loop(sa, synth, True, steps, prompt)
     kp, vp, q_all, k_all, v_all, wq, wk = raw
     cos, sin = oracle.rope_tables(prompt + steps, D, 1e6)
     N = prompt + steps

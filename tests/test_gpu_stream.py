@@ -39,10 +39,10 @@ def assert_f32_parity(out, want):
     assert rel_l2(out, want) <= REL_L2, rel_l2(out, want)
 
 
-def test_cfg1_golden(sa):
+def test_t1024_golden(sa):
     """T=1024, d=128, N(0,1), blocks 64/128, scale 1/sqrt(128) vs the reference."""
-    _, g = gi.load("stream_cfg1")
-    Q, K, V = gi.cfg1_inputs()
+    _, g = gi.load("stream_t1024")
+    Q, K, V = gi.t1024_inputs()
     dQ, dK, dV = dev(Q), dev(K), dev(V)
     for blk in (64, 128):
         assert_f32_parity(host(sa.stream_attn(dQ, dK, dV, blk, float(SCALE128))), g[f"serial_scaled_b{blk}"])
@@ -60,13 +60,13 @@ def test_unit_grid_golden(sa):
 
 
 @pytest.mark.parametrize("T", [8192, 65536, 262144])
-def test_cfg2_long_context(sa, oracle, T):
+def test_long_context(sa, oracle, T):
     """0.5 N(0,1) with 1% of K rows x8; blocks 64 and 128."""
-    print(f"cfg2 T={T}", flush=True)
-    Q, K, V = gi.cfg2_inputs(T)
+    print(f"long context T={T}", flush=True)
+    Q, K, V = gi.long_inputs(T)
     dQ, dK, dV = dev(Q), dev(K), dev(V)
     f64 = oracle.sdpa_f64(Q[None], K, V, 1.0)[0]
-    golden = gi.load("stream_cfg2")[1] if T <= 65536 else None
+    golden = gi.load("stream_long")[1] if T <= 65536 else None
     for blk in (64, 128):
         out = host(sa.stream_attn(dQ, dK, dV, blk, 1.0))
         want = golden[f"serial_T{T}_b{blk}"] if golden else oracle.streaming_serial(Q, K, V, blk)
@@ -92,7 +92,7 @@ def test_zero_length(sa):
 
 def test_chunk_override_matches(sa, oracle, monkeypatch):
     """Every split count gives the same answer (SA_DECODE_CHUNK forces it)."""
-    Q, K, V = gi.cfg2_inputs(8192)
+    Q, K, V = gi.long_inputs(8192)
     want = oracle.streaming_serial(Q, K, V, 64)
     dQ, dK, dV = dev(Q), dev(K), dev(V)
     for chunk in ("64", "256", "1024", "8192"):
@@ -136,7 +136,7 @@ def test_argument_errors(sa):
     with pytest.raises(sa.SaError):
         sa.stream_attn(Q100, K100, K100, 64)
     # workspace too small for a split run
-    Q, K, V = gi.cfg2_inputs(8192)
+    Q, K, V = gi.long_inputs(8192)
     with pytest.raises(sa.SaError) as e:
         sa.stream_attn(dev(Q), dev(K), dev(V), 64, ws=torch.empty(16, dtype=torch.uint8, device="cuda"))
     assert e.value.status == sa.SA_ENOMEM

@@ -34,10 +34,10 @@ def test_golden_inputs_unchanged():
             h.update(np.ascontiguousarray(a).tobytes())
         return h.hexdigest()
 
-    meta, _ = gi.load("stream_cfg1")
-    assert dg(*gi.cfg1_inputs()) == meta["inputs_sha256"]
-    meta, _ = gi.load("stream_cfg2")
-    assert dg(*gi.cfg2_inputs(8192)) == meta["inputs_sha256"]["8192"]
+    meta, _ = gi.load("stream_t1024")
+    assert dg(*gi.t1024_inputs()) == meta["inputs_sha256"]
+    meta, _ = gi.load("stream_long")
+    assert dg(*gi.long_inputs(8192)) == meta["inputs_sha256"]["8192"]
     meta, _ = gi.load("decode")
     assert dg(*gi.decode_inputs()) == meta["inputs_sha256"]
     meta, _ = gi.load("layer")
@@ -48,9 +48,9 @@ def test_golden_inputs_unchanged():
         assert dg(tokens, w["embed"], w["lm_head"], *[v for L in w["layers"] for v in L.values()]) == sha
 
 
-def test_oracle_streaming_golden_cfg1(oracle):
-    _, g = gi.load("stream_cfg1")
-    Q, K, V = gi.cfg1_inputs()
+def test_oracle_streaming_golden_t1024(oracle):
+    _, g = gi.load("stream_t1024")
+    Q, K, V = gi.t1024_inputs()
     for blk in (64, 128):
         np.testing.assert_allclose(oracle.streaming_serial(Q, K, V, blk), g[f"serial_b{blk}"], atol=2e-6)
         np.testing.assert_allclose(oracle.streaming_serial(Q * SCALE128, K, V, blk),
@@ -66,10 +66,10 @@ def test_oracle_streaming_golden_unit_grid(oracle):
         np.testing.assert_allclose(oracle.streaming_serial(Q, K, V, 64), g[f"serial_T{T}_d{d}"], atol=1e-6)
 
 
-def test_oracle_streaming_golden_cfg2(oracle):
-    _, g = gi.load("stream_cfg2")
+def test_oracle_streaming_golden_long(oracle):
+    _, g = gi.load("stream_long")
     for T in (8192, 65536):
-        Q, K, V = gi.cfg2_inputs(T)
+        Q, K, V = gi.long_inputs(T)
         for blk in (64, 128):
             out = oracle.streaming_serial(Q, K, V, blk)
             assert rel_l2(out, g[f"serial_T{T}_b{blk}"]) < 2e-6
@@ -188,11 +188,11 @@ def test_oracle_matches_reference_random(oracle, ref, synth):
 # ------------------------------------------------------------------ fp64 and closed forms
 
 def test_streaming_vs_fp64(oracle, synth):
-    Q, K, V = gi.cfg1_inputs()
+    Q, K, V = gi.t1024_inputs()
     f = oracle.sdpa_f64(Q[None] * SCALE128, K, V, 1.0)[0]
     out = oracle.streaming_serial(Q * SCALE128, K, V, 64)
     assert rel_l2(out, f) < 1e-6
-    Q, K, V = gi.cfg2_inputs(8192)
+    Q, K, V = gi.long_inputs(8192)
     f = oracle.sdpa_f64(Q[None], K, V, 1.0)[0]
     assert rel_l2(oracle.streaming_serial(Q, K, V, 128), f) < 5e-6
 
