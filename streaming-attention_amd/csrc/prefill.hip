@@ -506,7 +506,6 @@ prefill_bf16_dma_kernel(PrefillArgs pa) {
     const int n = lane & 31;
     const int hh = lane >> 5;
     const float sl2 = pa.sl2;
-    if (W >= 8 && wave < W / 2) __builtin_amdgcn_s_setprio(1);   // as in prefill_bf16_kernel
 
     const int wph = W / pa.gh;
     const int qtile = wph * 32;
@@ -544,7 +543,7 @@ prefill_bf16_dma_kernel(PrefillArgs pa) {
         }
     };
 #pragma unroll
-    for (int s = 0; s < NS - 1; ++s) dma_tile(s, s);
+    for (int s = 0; s < (W == 8 ? NS : NS - 1); ++s) dma_tile(s, s);
 
     bf16x8_t qf[NKS];
     {
@@ -610,7 +609,8 @@ prefill_bf16_dma_kernel(PrefillArgs pa) {
         else if constexpr (VM == 4) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
         else asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     };
-    next_tile_ready();   // tile 0
+    if constexpr (W == 8) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else next_tile_ready();   // tile 0
 
     // One tile from stage sb, as two 32-key halves: scores, raise of the
     // running max when it grew by more than 2^kHugeExcess, softmax, PV, lazy
@@ -688,19 +688,126 @@ prefill_bf16_dma_kernel(PrefillArgs pa) {
         }
     };
 
-    auto step = [&](int kt, int stage) {
-        const bool more = kt + NS - 1 < n_kt;
-        if (more) dma_tile(kt + NS - 1, (stage + NS - 1) % NS);   // into the stage tile kt - 1 used
-        if (kt + 1 < wave_kt) tile(kt, lsm + stage * kDmaStageBytes, std::false_type{});
-        if (more) next_tile_ready();
-        else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    };
-    // Whole rounds of NS steps keep every stage index a constant; the extra
-    // steps past n_kt only synchronise.
-    const int n_steps = (n_kt + NS - 1) / NS * NS;
-    for (int kt = 0; kt < n_steps; kt += NS) {
+    if constexpr (W == 8) {
+        // Ping-pong: waves w and w + 4 share a SIMD.  Each 32-key half is an
+        // MFMA block (the previous half's PV, then this half's scores) and a
+        // softmax block.  Waves 4-7 take the half's barrier between their two
+        // blocks, waves 0-3 after both, so on every SIMD one wave's softmax
+        // runs while the other issues MFMAs.  The previous half's P and V^T
+        // fragments stay in registers across the barrier.  The loop covers
+        // the tiles [0, kt_pp) that every wave computes off its diagonal,
+        // without per-wave branches (with them the compiler spilled); the
+        // remaining tiles and each wave's diagonal run one tile per barrier.
+        // Tile kt + 2 loads once every wave is done with tile kt.
+        static_assert(NS == 2 && NI == 2, "ping-pong schedule: two stages, two loads per tensor tile");
+        const bool late = wave >= W / 2;
+        auto raise_to = [&](float mt) {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+            const float mq = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+            const float m_new = fmaxf(ms, mq * sl2);
+            const float alpha = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - m_new);
 #pragma unroll
-        for (int s = 0; s < NS; ++s) step(kt + s, s);
+            for (int db = 0; db < NDB; ++db) acc[db] *= alpha;
+            lp *= alpha;
+            ms = m_new;
+        };
+        // The pending half starts as zeros: its PV adds exact zeros, and its
+        // lazy-raise test is false (sl2 >= 0: -inf * sl2 is -inf or NaN).
+        bf16x8_t pv_v[NDB][2];
+        bf16x8_t pv_p[2];
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) pv_v[db][0] = pv_v[db][1] = bf16x8_t{};
+        pv_p[0] = pv_p[1] = bf16x8_t{};
+        float pv_mt = -INFINITY;
+        auto flush = [&]() {
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+                    acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pv_v[db][t], pv_p[t], acc[db], 0, 0, 0);
+            if (__any(pv_mt * sl2 > ms + kLazyRescale)) raise_to(pv_mt);
+        };
+        // End of tile kt: tile kt + 1 resident for all waves, then tile kt + 2
+        // loads into the stage tile kt used.
+        auto end_tile = [&](int kt, int stage) {
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            if (kt + NS < n_kt) dma_tile(kt + NS, stage);
+        };
+        auto half = [&](int kt, int stage, int kb) {
+            const lds_u8_t* sb = lsm + stage * kDmaStageBytes;
+            bf16x8_t kf[NKS];
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) kf[ks] = lds_k(sb, kb, ks);
+            flush();
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int t = 0; t < 2; ++t) pv_v[db][t] = lds_vt(sb, kb, t, db);
+            f32x16_t s = {};
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qf[ks], s, 0, 0, 0);
+            auto sync = [&]() {
+                __builtin_amdgcn_sched_barrier(0);
+                if (kb == 0) asm volatile("s_barrier" ::: "memory");
+                else end_tile(kt, stage);
+                __builtin_amdgcn_sched_barrier(0);
+            };
+            if (late) sync();
+            float mt = s[0];
+#pragma unroll
+            for (int j = 1; j < 16; ++j) mt = fmaxf(mt, s[j]);
+            if (__any(mt * sl2 > ms + kHugeExcess)) raise_to(mt);
+            const float nm = -ms;
+            float p[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j], sl2, nm));
+            float rs = p[0];
+#pragma unroll
+            for (int j = 1; j < 16; ++j) rs += p[j];
+            lp += rs;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const bf16x2_t p01 = __builtin_convertvector(f32x2_t{p[8 * t + 0], p[8 * t + 1]}, bf16x2_t);
+                const bf16x2_t p23 = __builtin_convertvector(f32x2_t{p[8 * t + 2], p[8 * t + 3]}, bf16x2_t);
+                const bf16x2_t p45 = __builtin_convertvector(f32x2_t{p[8 * t + 4], p[8 * t + 5]}, bf16x2_t);
+                const bf16x2_t p67 = __builtin_convertvector(f32x2_t{p[8 * t + 6], p[8 * t + 7]}, bf16x2_t);
+                pv_p[t] = __builtin_bit_cast(
+                    bf16x8_t, make_uint4(__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23),
+                                         __builtin_bit_cast(uint32_t, p45), __builtin_bit_cast(uint32_t, p67)));
+            }
+            pv_mt = mt;
+            if (!late) sync();
+        };
+        // Tiles every wave computes off its diagonal, in whole rounds of NS.
+        const int kt_pp = (wk.qt * qtile + 31) / kKTile / NS * NS;
+        for (int kt = 0; kt < kt_pp; kt += NS) {
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                half(kt + s, s, 0);
+                half(kt + s, s, 1);
+            }
+        }
+        flush();
+        for (int kt = kt_pp; kt < n_kt; ++kt) {
+            const int stage = kt % NS;
+            if (kt + 1 < wave_kt) tile(kt, lsm + stage * kDmaStageBytes, std::false_type{});
+            end_tile(kt, stage);
+        }
+    } else {
+        auto step = [&](int kt, int stage) {
+            const bool more = kt + NS - 1 < n_kt;
+            if (more) dma_tile(kt + NS - 1, (stage + NS - 1) % NS);   // into the stage tile kt - 1 used
+            if (kt + 1 < wave_kt) tile(kt, lsm + stage * kDmaStageBytes, std::false_type{});
+            if (more) next_tile_ready();
+            else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        };
+        // Whole rounds of NS steps keep every stage index a constant; the extra
+        // steps past n_kt only synchronise.
+        const int n_steps = (n_kt + NS - 1) / NS * NS;
+        for (int kt = 0; kt < n_steps; kt += NS) {
+    #pragma unroll
+            for (int s = 0; s < NS; ++s) step(kt + s, s);
+        }
     }
     if (wave_kt > 0) tile(wave_kt - 1, lsm + ((wave_kt - 1) % NS) * kDmaStageBytes, std::true_type{});
 
@@ -961,10 +1068,11 @@ sa_status launch_bf16(const PrefillArgs& pa, dim3 grid, hipStream_t st) {
     return SA_OK;
 }
 
-// LDS stages of the load-unit kernel: three with 8 waves (one workgroup per
-// CU), two with 4 (two workgroups per CU fit in LDS).
+// LDS stages of the load-unit kernel: two (with 4 waves, two workgroups per
+// CU fit in LDS; with 8, the ping-pong schedule loads tile kt + 2 once tile kt
+// is done, and three stages measured 1 % slower).
 template <int W>
-constexpr int dma_stages() { return W == 8 ? 3 : 2; }
+constexpr int dma_stages() { return 2; }
 
 template <int W>
 sa_status launch_bf16_dma(const PrefillArgs& pa, dim3 grid, hipStream_t st) {
@@ -1003,11 +1111,12 @@ sa_status launch(PrefillArgs pa, int B, bool bf16, int D, hipStream_t st) {
     if (n_wg > 0x7fffffffLL) return fail(SA_ERANGE, "prefill grid too large");
     const dim3 grid(static_cast<unsigned>(n_wg));
     // head_dim 128 in bf16 uses the load-unit kernel when a workgroup's
-    // queries end in at most NS - 1 tiles (its diagonal tiles stay resident):
-    // GQA groups of 2 or more.  Measured against the register-staged kernel
-    // (16/8 heads): 1.01x at L = 8192, 1.08x .. 1.14x at L = 1024 .. 4096.
+    // queries end within the tiles its schedule keeps resident (two with 8
+    // waves, one with 4), so every wave's diagonal tile is still in LDS after
+    // the loop: GQA groups of 2 or more.  Measured against the register-staged
+    // kernel (16/8 heads): 1.04x at L = 8192, 1.08x .. 1.14x at L = 1024 .. 4096.
     const bool dma = bf16 && D == 128 &&
-                     q_tile <= ((W == kBfW ? dma_stages<kBfW>() : dma_stages<kBfWSmall>()) - 1) * kKTile;
+                     q_tile <= (W == kBfW ? 2 : 1) * kKTile;
     sa_status s = SA_OK;
     if (dma) {
         s = W == kBfW ? launch_bf16_dma<kBfW>(pa, grid, st) : launch_bf16_dma<kBfWSmall>(pa, grid, st);

@@ -147,10 +147,13 @@ def test_prefill_bf16_short(sa, oracle, synth, monkeypatch, L, waves):
         np.testing.assert_allclose(out[:, :, 0], np.repeat(vb[:, :, 0], 2, axis=1), rtol=0, atol=1e-6)
 
 
+@pytest.mark.parametrize("waves", ["4", "8"])
 @pytest.mark.parametrize("scale", [-0.3, 0.0])
 @pytest.mark.parametrize("bf16", [False, True])
-def test_prefill_scale_sign(sa, oracle, synth, scale, bf16):
-    """Negative and zero scales (zero: uniform average over the prefix)."""
+def test_prefill_scale_sign(sa, oracle, synth, monkeypatch, scale, bf16, waves):
+    """Negative and zero scales (zero: uniform average over the prefix), at
+    both bf16 workgroup sizes."""
+    monkeypatch.setenv("SA_PREFILL_WAVES", waves)
     L = 200
     q, k, v = inputs(synth, L, 4, 2, 128, seed=57)
     if bf16:
