@@ -1047,14 +1047,15 @@ sa_status opt_in_lds(int bytes) {
 }
 
 // bf16 shape: W waves of QB 32-query blocks each.  Measured at L = 8192
-// (16/8 heads) on MI355X, steady-state clocks: 8 waves x 32 queries (two
-// waves per SIMD, both query heads of a KV group per workgroup) 0.281 ms.
-// Slower alternatives: 4 waves x 64 queries (also with the O accumulators in
-// AGPRs); a phase-locked schedule in which the two waves of a SIMD alternate
-// between MFMA and softmax phases at workgroup barriers; the next half's
-// score MFMAs software-pipelined under the current half's softmax (with
-// sched_group_barrier interleaving, three LDS stages); the score product
-// split into two independent MFMA chains.
+// (16/8 heads) on MI355X, steady-state clocks, with the register-staged
+// kernel: 8 waves x 32 queries (two waves per SIMD, both query heads of a KV
+// group per workgroup) 0.281 ms.  Slower there: 4 waves x 64 queries (also
+// with the O accumulators in AGPRs); a phase-locked schedule in which the two
+// waves of a SIMD alternate between MFMA and softmax phases at workgroup
+// barriers (the load-to-LDS kernel's ping-pong schedule is that idea without
+// the register spills); the next half's score MFMAs software-pipelined under
+// the current half's softmax (sched_group_barrier interleaving, three LDS
+// stages); the score product split into two independent MFMA chains.
 constexpr int kBfQB = 1;
 constexpr int kBfW = 8;
 constexpr int kBfWSmall = 4;
