@@ -622,8 +622,10 @@ extern "C" sa_status sa_qwen3_prefill(sa_qwen3* m, sa_kvcache* cache, const int3
     if (batch > kd.max_seqs) return fail(SA_ERANGE, "batch exceeds the cache's sequences");
     if ((long long)L > (long long)kd.max_pages_per_seq * 64)
         return fail(SA_EFULL, "prompt longer than a sequence's page table");
-    for (int i = 0; i < batch; ++i)
+    for (int i = 0; i < batch; ++i) {
         if (sa_kvcache_len(cache, i) != 0) return fail(SA_EINVAL, "prefill needs empty sequences");
+        if (sa_kvcache_capacity(cache, i) < L) return fail(SA_EFULL, "KV cache full, reserve pages for the prompt");
+    }
     hipStream_t st = as_stream(stream);
     const Shapes s = shapes_of(d, device_cu_count());
     const long long M = (long long)batch * L;

@@ -100,5 +100,10 @@ def test_prefill_rejects_bad_calls(sa):
     model.prefill(cache, toks[:, :4].contiguous())
     with pytest.raises(sa.SaError, match="empty"):
         model.prefill(cache, toks[:, :4].contiguous())
+    bare = sa.KVCache(CFG["num_layers"], CFG["n_kv_heads"], CFG["head_dim"], 2, 1, 2, sa.SA_DTYPE_F32)
+    with pytest.raises(sa.SaError, match="full") as e:   # no pages reserved
+        model.prefill(bare, toks[:, :4].contiguous())
+    assert e.value.status == sa.SA_EFULL and bare.length(0) == 0
+    bare.close()
     cache.close()
     model.close()
