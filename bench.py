@@ -323,8 +323,7 @@ def bench_layer_decode_loop(torch, sa, synth, steps_timed: int = 3):
 
 def batch_lengths(synth, B: int = 64, lo: int = 512, hi: int = 32768, seed: int = 70):
     """Per-sequence context lengths ~ U[lo, hi] (seeded)."""
-    u = synth.uniform(seed, 1, B)
-    return [int(lo + min(int(x * (hi - lo + 1)), hi - lo)) for x in u]
+    return synth.batch_lengths(B, lo, hi, seed)
 
 
 def bench_paged_batch(torch, sa, synth, steps: int = 10, bf16: bool = True):
@@ -344,7 +343,7 @@ def bench_paged_batch(torch, sa, synth, steps: int = 10, bf16: bool = True):
     for s, L in enumerate(lens):
         cache.set_pages(s, perm[off:off + pages_per[s]])
         off += pages_per[s]
-        ids = torch.tensor([s], dtype=torch.int32, device="cuda")
+        ids = [s]
         for t0 in range(0, L, 4096):
             n = min(4096, L - t0)
             k = torch.randn(1, n, HKV, D, device="cuda", generator=gen)
@@ -361,10 +360,27 @@ def bench_paged_batch(torch, sa, synth, steps: int = 10, bf16: bool = True):
     elem = 2 if bf16 else 4
     kv_bytes = sum(lens) * HKV * D * 2 * elem
     total = kv_bytes + 2 * B * HQ * D * 4
+    # Outside the timed region: the last timed call's output for the shortest,
+    # the longest and 8 seeded random sequences against the oracle's STANDARD
+    # decode on the K/V the cache holds (gathered as fp32).
+    from oracle import Oracle
+    oracle = Oracle()
+    got, qh = out.cpu().numpy(), q.cpu().numpy()
+    order = np.argsort(lens)
+    check = [int(order[0]), int(order[-1])] + [int(x) for x in synth.permutation(70, 3, B)
+                                               if x not in (order[0], order[-1])][:8]
+    errs, rl2s = [], []
+    for s in check:
+        gk, gv = cache.gather(0, s, lens[s])
+        want = oracle.decode_gqa(qh[s][None], gk.cpu().numpy()[None], gv.cpu().numpy()[None], np.float32(sc))[0]
+        errs.append(float(np.abs(got[s] - want).max()))
+        rl2s.append(float(np.linalg.norm((got[s] - want).astype(np.float64)) / np.linalg.norm(want.astype(np.float64))))
     cache.close()
     return {"batch": B, "sum_len": sum(lens), "min_len": min(lens), "max_len": max(lens),
             "kv": "bf16" if bf16 else "f32", "ms": round(ms, 4), "bytes_per_call": total,
-            "gbs": round(total / (ms * 1e-3) / 1e9, 1), "hbm_frac": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            "gbs": round(total / (ms * 1e-3) / 1e9, 1), "hbm_frac": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "parity": {"sequences_checked": len(check), "max_abs_err": max(errs), "max_rel_l2_err": max(rl2s),
+                       "against": "oracle STANDARD decode on the cached bf16 K/V (fp32 bar 1e-4 / 1e-5)"}}
 
 
 def bench_model_decode(torch, sa, synth, steps: int = 128, warmup: int = 2, B: int = 64):

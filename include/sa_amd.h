@@ -90,6 +90,15 @@ sa_status sa_decode_dense_f32(const float* q, const float* k, const float* v,
  * appends write at positions seq_len[s] + i and become visible to later
  * steps only after sa_kvcache_commit (append-then-commit, as the reference's
  * update()/increment_seq_len()).
+ *
+ * Ordering: the page table and the lengths are decided on the host and
+ * published to the device by small kernels on the stream each call is given.
+ * Calls that change or read a cache (reset, reserve, set_pages, set_len,
+ * append, decode, commit, gather) are ordered when they are issued on one
+ * stream; a caller that spreads them over streams orders them itself.
+ * Every capacity, index and page check runs on the host before anything is
+ * enqueued: an append or decode that would overflow a sequence's pages
+ * returns SA_EFULL / SA_ERANGE and enqueues nothing.
  * ------------------------------------------------------------------------ */
 typedef struct sa_kv_desc {
     int num_layers;
@@ -109,10 +118,13 @@ sa_status sa_kvcache_destroy(sa_kvcache* cache);
 sa_status sa_kvcache_reset(sa_kvcache* cache, sa_stream_t stream);
 /* Make room for n_tokens tokens in total in sequence seq, taking pages from
  * the free list in order.  SA_EFULL if the pool or the table row is exhausted. */
-sa_status sa_kvcache_reserve(sa_kvcache* cache, int seq, int n_tokens);
-/* Give sequence seq an explicit page list (replaces its current pages). */
+sa_status sa_kvcache_reserve(sa_kvcache* cache, int seq, int n_tokens, sa_stream_t stream);
+/* Give sequence seq an explicit page list (host array; replaces its current
+ * pages).  Each page must be in the pool, listed once, and free or already
+ * seq's (SA_ERANGE / SA_EINVAL otherwise).  A committed length beyond the new
+ * capacity is cut to it. */
 sa_status sa_kvcache_set_pages(sa_kvcache* cache, int seq, const int32_t* pages,
-                               int n_pages);
+                               int n_pages, sa_stream_t stream);
 /* Set the committed length of seq (host and device), within its reserved pages. */
 sa_status sa_kvcache_set_len(sa_kvcache* cache, int seq, int len, sa_stream_t stream);
 /* Committed length of seq as tracked on the host, or -1. */
@@ -121,7 +133,8 @@ int sa_kvcache_len(const sa_kvcache* cache, int seq);
  * counterpart in the reference, whose dense cache has one fixed capacity
  * (tensor_cpp/include/tensor_cpp/kv_cache.h:47-86). */
 int sa_kvcache_capacity(const sa_kvcache* cache, int seq);
-/* Add n to the committed length of seqs[0..n_seqs) (host ids; NULL = 0..n_seqs-1). */
+/* Add n to the committed length of seqs[0..n_seqs) (host ids, each at most
+ * once; NULL = 0..n_seqs-1). */
 sa_status sa_kvcache_commit(sa_kvcache* cache, const int32_t* seqs, int n_seqs, int n,
                             sa_stream_t stream);
 /* Device pointers into the cache, for callers that drive kernels themselves. */
@@ -150,8 +163,10 @@ sa_status sa_rope_table_init(float* d_cos, float* d_sin, int max_pos, int head_d
  * concat and KVCache::update of the reference decoder layer (reference
  * tensor_cpp/src/qwen3_ops.cpp:697-861, kv_cache.h:94-130).
  * q [n_seq][S][n_q_heads][D], k and v [n_seq][S][n_kv_heads][D], fp32,
- * token-major.  seq_ids: device [n_seq] cache rows, or NULL for 0..n_seq-1.
- * Token s of sequence i is written at position seq_len[seq_ids[i]] + s.
+ * token-major.  seq_ids: host array [n_seq] of distinct cache rows, or NULL
+ * for 0..n_seq-1.  Token s of sequence i is written at position
+ * seq_len[seq_ids[i]] + s; every row must have pages for seq_len + S tokens
+ * (SA_EFULL otherwise) and, with RoPE, seq_len + S <= rope_max_pos.
  * q_norm_w / k_norm_w: [D] RMSNorm weights, or NULL to skip the norm
  * (y = x / sqrt(mean(x^2) + eps) * w).  rope_cos / rope_sin: tables from
  * sa_rope_table_init with rope_max_pos rows, or NULL to skip RoPE.
@@ -187,7 +202,10 @@ sa_status sa_qk_norm_rope(const float* x, int n_rows, int D, const int32_t* pos,
  * cache path (reference tensor_cpp/src/qwen3_ops.cpp:863-909).  Each sequence
  * i attends over its first seq_len[seq_ids[i]] + n_pending tokens, where
  * n_pending counts tokens appended but not yet committed (1 in a decode
- * step).  q [n_seq][n_q_heads][D] fp32, out likewise.
+ * step).  seq_ids: host array [n_seq] of cache rows, or NULL for
+ * 0..n_seq-1; every row must have pages for seq_len + n_pending tokens
+ * (SA_ERANGE otherwise).  A sequence of length 0 gets a zero output.
+ * q [n_seq][n_q_heads][D] fp32, out likewise.
  * ws must hold sa_paged_decode_ws_bytes(...) bytes.
  * ------------------------------------------------------------------------ */
 size_t sa_paged_decode_ws_bytes(const sa_kvcache* cache, int n_seq, int n_q_heads);

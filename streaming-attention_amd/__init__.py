@@ -69,8 +69,8 @@ SIGNATURES = {
     "sa_kvcache_create": (_I, [C.POINTER(KvDesc), C.POINTER(_P)]),
     "sa_kvcache_destroy": (_I, [_P]),
     "sa_kvcache_reset": (_I, [_P, _P]),
-    "sa_kvcache_reserve": (_I, [_P, _I, _I]),
-    "sa_kvcache_set_pages": (_I, [_P, _I, _P, _I]),
+    "sa_kvcache_reserve": (_I, [_P, _I, _I, _P]),
+    "sa_kvcache_set_pages": (_I, [_P, _I, _P, _I, _P]),
     "sa_kvcache_set_len": (_I, [_P, _I, _I, _P]),
     "sa_kvcache_len": (_I, [_P, _I]),
     "sa_kvcache_capacity": (_I, [_P, _I]),
@@ -128,6 +128,16 @@ def check(status: int) -> None:
 
 def _ptr(t) -> int | None:
     return None if t is None else t.data_ptr()
+
+
+def _rows(ids, n: int):
+    """Host int32 array of cache rows for the C ABI (None stays NULL)."""
+    if ids is None:
+        return None
+    ids = [int(i) for i in ids]
+    if len(ids) != n:
+        raise ValueError(f"seq_ids has {len(ids)} entries for {n} sequences")
+    return C.cast((C.c_int32 * n)(*ids), C.c_void_p)
 
 
 def _stream(stream) -> int | None:
@@ -204,12 +214,12 @@ class KVCache:
     def reset(self, stream=None) -> None:
         check(lib().sa_kvcache_reset(self.handle, _stream(stream)))
 
-    def reserve(self, seq: int, n_tokens: int) -> None:
-        check(lib().sa_kvcache_reserve(self.handle, seq, n_tokens))
+    def reserve(self, seq: int, n_tokens: int, stream=None) -> None:
+        check(lib().sa_kvcache_reserve(self.handle, seq, n_tokens, _stream(stream)))
 
-    def set_pages(self, seq: int, pages) -> None:
-        arr = (C.c_int32 * len(pages))(*[int(p) for p in pages])
-        check(lib().sa_kvcache_set_pages(self.handle, seq, arr, len(pages)))
+    def set_pages(self, seq: int, pages, stream=None) -> None:
+        arr = (C.c_int32 * max(len(pages), 1))(*[int(p) for p in pages])
+        check(lib().sa_kvcache_set_pages(self.handle, seq, arr, len(pages), _stream(stream)))
 
     def set_len(self, seq: int, n: int, stream=None) -> None:
         check(lib().sa_kvcache_set_len(self.handle, seq, n, _stream(stream)))
@@ -239,7 +249,8 @@ class KVCache:
 
     def append(self, layer: int, q, k, v, q_norm_w=None, k_norm_w=None, eps: float = 1e-6,
                rope=None, q_out=None, seq_ids=None, stream=None):
-        """q [n, S, Hq, D] (or None), k/v [n, S, Hkv, D]; rope = (cos, sin) tables."""
+        """q [n, S, Hq, D] (or None), k/v [n, S, Hkv, D]; rope = (cos, sin) tables;
+        seq_ids: cache rows of the n sequences (host ints), or None for 0..n-1."""
         n_seq, S = k.shape[0], k.shape[1]
         Hq = 0 if q is None else q.shape[2]
         cos, sin = (None, None) if rope is None else rope
@@ -249,7 +260,7 @@ class KVCache:
             q_out = torch.empty_like(q)
         check(lib().sa_qknorm_rope_append(
             self.handle, layer, _ptr(_f32(q, "q")), _ptr(_f32(k, "k")), _ptr(_f32(v, "v")), n_seq, S,
-            _ptr(seq_ids), Hq, _ptr(_f32(q_norm_w, "q_norm_w")), _ptr(_f32(k_norm_w, "k_norm_w")), eps,
+            _rows(seq_ids, n_seq), Hq, _ptr(_f32(q_norm_w, "q_norm_w")), _ptr(_f32(k_norm_w, "k_norm_w")), eps,
             _ptr(cos), _ptr(sin), max_pos, _ptr(q_out), _stream(stream)))
         return q_out
 
@@ -258,14 +269,15 @@ class KVCache:
 
     def decode(self, layer: int, q, scale: float, n_pending: int = 0, out=None, ws=None,
                seq_ids=None, stream=None):
-        """q [n_seq, Hq, D] -> out [n_seq, Hq, D]."""
+        """q [n_seq, Hq, D] -> out [n_seq, Hq, D]; seq_ids: cache rows (host
+        ints) or None for 0..n_seq-1."""
         import torch
         n_seq, Hq, _ = q.shape
         out = torch.empty_like(q) if out is None else out
         if ws is None:
             need = self.decode_ws_bytes(n_seq, Hq)
             ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=q.device)
-        check(lib().sa_paged_decode(self.handle, layer, _ptr(_f32(q, "q")), n_seq, _ptr(seq_ids), Hq,
+        check(lib().sa_paged_decode(self.handle, layer, _ptr(_f32(q, "q")), n_seq, _rows(seq_ids, n_seq), Hq,
                                     n_pending, scale, _ptr(out), _ptr(ws), ws.numel(), _stream(stream)))
         return out
 

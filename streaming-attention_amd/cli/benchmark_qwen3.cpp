@@ -206,7 +206,7 @@ struct Runner {
 
     void reset(int tokens) {
         check(sa_kvcache_reset(cache, nullptr), "sa_kvcache_reset");
-        for (int s = 0; s < cfg.batch_size; ++s) check(sa_kvcache_reserve(cache, s, tokens), "sa_kvcache_reserve");
+        for (int s = 0; s < cfg.batch_size; ++s) check(sa_kvcache_reserve(cache, s, tokens, nullptr), "sa_kvcache_reserve");
     }
     // Prefill prompt [L] replicated over the batch; returns the next token of sequence 0.
     int32_t prefill(const std::vector<int32_t>& prompt, float* logits = nullptr) {

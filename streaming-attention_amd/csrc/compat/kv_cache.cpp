@@ -35,7 +35,7 @@ KVCache::KVCache(size_t n_layers, size_t batch, size_t n_kv_heads, size_t dim, s
     d.kv_dtype = kv_dtype;
     check(sa_kvcache_create(&d, &cache_), "sa_kvcache_create");
     for (size_t b = 0; b < batch; ++b)
-        check(sa_kvcache_reserve(cache_, static_cast<int>(b), pages_per_seq * SA_PAGE_TOKENS),
+        check(sa_kvcache_reserve(cache_, static_cast<int>(b), pages_per_seq * SA_PAGE_TOKENS, nullptr),
               "sa_kvcache_reserve");
 }
 
@@ -107,7 +107,7 @@ void KVCache::reset() {
     check(sa_kvcache_reset(cache_, nullptr), "sa_kvcache_reset");
     const int pages_per_seq = static_cast<int>((max_seq_len + SA_PAGE_TOKENS - 1) / SA_PAGE_TOKENS);
     for (size_t b = 0; b < batch_size; ++b)
-        check(sa_kvcache_reserve(cache_, static_cast<int>(b), pages_per_seq * SA_PAGE_TOKENS),
+        check(sa_kvcache_reserve(cache_, static_cast<int>(b), pages_per_seq * SA_PAGE_TOKENS, nullptr),
               "sa_kvcache_reserve");
     sa_compat::hip_check(hipStreamSynchronize(nullptr), "hipStreamSynchronize");
     current_seq_len = 0;

@@ -65,7 +65,7 @@ struct DecodeArgs {
     float* part_o;           // [n_seq*n_q_heads][n_split][D]
     const int32_t* block_table;  // paged only: [max_seqs][max_pages]
     const int32_t* seq_lens;     // paged only: committed lengths
-    const int32_t* seq_ids;      // paged only: may be null
+    RowList rows;                // paged only: cache row of each sequence of the launch
     int n_kv;
     int n_q;
     int T;                   // dense length
@@ -231,9 +231,18 @@ split_kv_decode_kernel(DecodeArgs a) {
     int len;
     int cache_row = seq;
     if constexpr (PAGED) {
-        cache_row = a.seq_ids ? a.seq_ids[seq] : seq;
-        // Never walk past the block-table row, whatever the lengths say.
-        len = min(a.seq_lens[cache_row] + a.n_pending, a.max_pages * 64);
+        cache_row = a.rows.row[seq];
+        // Never walk past the block-table row or the chunks of the grid,
+        // whatever the device lengths say (the host has checked them).
+        len = min(min(a.seq_lens[cache_row] + a.n_pending, a.max_pages * 64), a.n_split * a.chunk);
+        if (len <= 0) {
+            // An empty sequence attends to nothing: its output is zero.
+            if (split == 0) {
+                for (int i = threadIdx.x; i < NREP * D; i += THREADS)
+                    a.out[((size_t)seq * a.n_q + g * NREP) * D + i] = 0.f;
+            }
+            return;
+        }
     } else {
         len = a.T;
     }
@@ -403,8 +412,8 @@ lse_merge_kernel(DecodeArgs a) {
     const int seq = bh / a.n_q;
     int len;
     if constexpr (PAGED) {
-        const int row = a.seq_ids ? a.seq_ids[seq] : seq;
-        len = min(a.seq_lens[row] + a.n_pending, a.max_pages * 64);
+        const int row = a.rows.row[seq];
+        len = min(min(a.seq_lens[row] + a.n_pending, a.max_pages * 64), a.n_split * a.chunk);
     } else {
         len = a.T;
     }
@@ -619,7 +628,8 @@ size_t decode_dense_ws(int batch, int n_q, int T, int d) {
 size_t paged_ws(int n_seq, int n_q, int n_kv, int d, int max_pages) {
     const long long max_tokens = (long long)max_pages * 64;
     (void)n_kv;
-    return ws_bytes_for((long long)n_seq * n_q, max_splits_for(max_tokens), d);
+    // Launches take up to kRowsPerLaunch sequences and reuse the workspace.
+    return ws_bytes_for((long long)std::min(n_seq, kRowsPerLaunch) * n_q, max_splits_for(max_tokens), d);
 }
 
 sa_status decode_paged(const PagedView& c, const float* q, int n_seq, const int32_t* seq_ids,
@@ -631,7 +641,7 @@ sa_status decode_paged(const PagedView& c, const float* q, int n_seq, const int3
     if (max_len <= 0) max_len = 1;
     DecodeArgs a{};
     a.q = q; a.k = c.k_pool; a.v = c.v_pool; a.out = out;
-    a.block_table = c.block_table; a.seq_lens = c.seq_lens; a.seq_ids = seq_ids;
+    a.block_table = c.block_table; a.seq_lens = c.seq_lens;
     a.n_kv = c.n_kv; a.n_q = n_q; a.max_pages = c.max_pages; a.n_pending = n_pending;
     a.num_pages = c.num_pages;
     a.scale = scale;
@@ -639,14 +649,26 @@ sa_status decode_paged(const PagedView& c, const float* q, int n_seq, const int3
     a.chunk = pick_chunk(total_len * c.n_kv, (long long)c.max_pages * 64, (long long)kMaxChunkPages * 64);
     if (a.chunk > kMaxChunkPages * 64) return fail(SA_EINVAL, "max_pages_per_seq too large for the split cap");
     a.n_split = (max_len + a.chunk - 1) / a.chunk;
-    const long long bh = (long long)n_seq * n_q;
+    const long long bh = (long long)std::min(n_seq, kRowsPerLaunch) * n_q;
     const size_t need = ws_bytes_for(bh, a.n_split, c.d);
     if (need > 0) {
         if (!ws || ws_bytes < need) return fail(SA_ENOMEM, "workspace too small for split-KV partials");
         carve_ws(a, ws, bh);
     }
-    if (c.bf16) return dispatch_decode<true, true>(a, n_seq, c.d, n_q / c.n_kv, st);
-    return dispatch_decode<false, true>(a, n_seq, c.d, n_q / c.n_kv, st);
+    // Up to kRowsPerLaunch sequences per launch, their cache rows by value;
+    // the workspace is reused launch after launch in stream order.
+    for (int i0 = 0; i0 < n_seq; i0 += kRowsPerLaunch) {
+        const int m = std::min(kRowsPerLaunch, n_seq - i0);
+        for (int i = 0; i < m; ++i) a.rows.row[i] = seq_ids ? seq_ids[i0 + i] : i0 + i;
+        a.q = q + (size_t)i0 * n_q * c.d;
+        a.out = out + (size_t)i0 * n_q * c.d;
+        if (c.bf16) {
+            SA_TRY((dispatch_decode<true, true>(a, m, c.d, n_q / c.n_kv, st)));
+        } else {
+            SA_TRY((dispatch_decode<false, true>(a, m, c.d, n_q / c.n_kv, st)));
+        }
+    }
+    return SA_OK;
 }
 
 }  // namespace sa

@@ -9,7 +9,13 @@
 // The reference keeps a dense [B, Hkv, max_seq, D] fp32 tensor per layer and
 // copies it out on every step (reference tensor_cpp/include/tensor_cpp/kv_cache.h:27-238);
 // here the cache stays resident and the decode kernel reads it in place.
+//
+// Ordering: the host decides (page_table.cpp) and publishes the table rows and
+// lengths with small kernels on the stream the caller passes, so a reset,
+// reserve, set_pages, append, decode and commit issued on one stream run in
+// the order they were called.
 #include "sa_internal.h"
+#include "page_table.h"
 
 #include <algorithm>
 #include <cmath>
@@ -25,10 +31,7 @@ struct sa_kvcache {
     size_t total_bytes = 0;
     int32_t* d_table = nullptr;    // [max_seqs][max_pages_per_seq]
     int32_t* d_lens = nullptr;     // [max_seqs]
-    std::vector<int32_t> h_table;
-    std::vector<int> h_lens;
-    std::vector<int> h_npages;     // pages assigned to each sequence
-    std::vector<int32_t> free_pages;
+    sa::PageTable pt;              // host decisions; the device arrays follow them
 };
 
 namespace sa {
@@ -54,14 +57,10 @@ __global__ void write_table_kernel(int32_t* dst, TableRow row, int n) {
     if ((int)threadIdx.x < n) dst[threadIdx.x] = row.v[threadIdx.x];
 }
 
-struct SeqList {
-    int32_t id[32];
-};
-
-// seq_lens[ids[i]] = add ? seq_lens[ids[i]] + val : val
-__global__ void update_lens_kernel(int32_t* lens, SeqList ids, int n, int val, int add) {
+// seq_lens[rows[i]] = add ? seq_lens[rows[i]] + val : val
+__global__ void update_lens_kernel(int32_t* lens, RowList rows, int n, int val, int add) {
     int i = threadIdx.x;
-    if (i < n) lens[ids.id[i]] = add ? lens[ids.id[i]] + val : val;
+    if (i < n) lens[rows.row[i]] = add ? lens[rows.row[i]] + val : val;
 }
 
 __global__ void add_lens_range_kernel(int32_t* lens, int n, int val) {
@@ -69,18 +68,36 @@ __global__ void add_lens_range_kernel(int32_t* lens, int n, int val) {
     if (i < n) lens[i] += val;
 }
 
-sa_status write_table_row(sa_kvcache* c, int seq, hipStream_t st) {
+// Publish entries [0, n) of seq's host table row (the rest of the device row
+// already holds -1 or is overwritten here).
+sa_status write_table_row(sa_kvcache* c, int seq, int n, hipStream_t st) {
     const int mp = c->desc.max_pages_per_seq;
-    for (int j0 = 0; j0 < mp; j0 += 64) {
+    const int32_t* src = c->pt.row(seq);
+    for (int j0 = 0; j0 < n; j0 += 64) {
         TableRow row;
-        const int n = std::min(64, mp - j0);
-        for (int j = 0; j < n; ++j) row.v[j] = c->h_table[(size_t)seq * mp + j0 + j];
+        const int m = std::min(64, n - j0);
+        for (int j = 0; j < m; ++j) row.v[j] = src[j0 + j];
         hipLaunchKernelGGL(write_table_kernel, dim3(1), dim3(64), 0, st,
-                           c->d_table + (size_t)seq * mp + j0, row, n);
+                           c->d_table + (size_t)seq * mp + j0, row, m);
         SA_CHECK_LAUNCH();
     }
     return SA_OK;
 }
+
+// Set (add = 0) or add to (add = 1) the device lengths of rows[0, n)
+// (rows == NULL: 0 .. n-1).
+sa_status publish_lens(sa_kvcache* c, const int32_t* rows, int n, int val, int add, hipStream_t st) {
+    for (int i0 = 0; i0 < n; i0 += kRowsPerLaunch) {
+        RowList rl;
+        const int m = std::min(kRowsPerLaunch, n - i0);
+        for (int i = 0; i < m; ++i) rl.row[i] = rows ? rows[i0 + i] : i0 + i;
+        hipLaunchKernelGGL(update_lens_kernel, dim3(1), dim3(kRowsPerLaunch), 0, st, c->d_lens, rl, m, val, add);
+        SA_CHECK_LAUNCH();
+    }
+    return SA_OK;
+}
+
+sa_status refused(const Verdict& v) { return fail(v.status, v.msg); }
 
 // ---------------------------------------------------------------------------
 // Fused QK-norm + RoPE + append.  One wave per (token, head row): waves
@@ -93,7 +110,7 @@ struct AppendArgs {
     float* q_out;
     const float* wq; const float* wk;
     const float* cos_t; const float* sin_t;
-    const int32_t* seq_ids;
+    RowList rows;              // cache row of each sequence of this launch
     const int32_t* seq_lens;
     const int32_t* table;
     char* k_pool; char* v_pool;
@@ -188,7 +205,7 @@ qknorm_rope_append_kernel(AppendArgs a) {
     const bool is_q = row_id < a.n_q;
     if (is_q && !a.q) return;
     const int head = is_q ? row_id : row_id - a.n_q;
-    const int cache_row = a.seq_ids ? a.seq_ids[i_seq] : i_seq;
+    const int cache_row = a.rows.row[i_seq];
     const int pos = a.seq_lens[cache_row] + s;
 
     const int nh = is_q ? a.n_q : a.n_kv;
@@ -206,7 +223,9 @@ qknorm_rope_append_kernel(AppendArgs a) {
     }
     const float* lo = r.lo;
     const float* hi = r.hi;
-    // Append K (normed, rotated) and V (as given) at pos.
+    // Append K (normed, rotated) and V (as given) at pos.  The host has
+    // checked that every row has a page there; these tests only keep a
+    // device length that disagrees with the host from writing out of bounds.
     if (pos >= a.max_pages * 64) return;
     const int page = a.table[(size_t)cache_row * a.max_pages + (pos >> 6)];
     if (page < 0) return;
@@ -303,9 +322,7 @@ extern "C" sa_status sa_kvcache_create(const sa_kv_desc* d, sa_kvcache** out) {
         delete c;
         return fail(SA_ENOMEM, "KV table allocation failed");
     }
-    c->h_table.assign(n_table, -1);
-    c->h_lens.assign(d->max_seqs, 0);
-    c->h_npages.assign(d->max_seqs, 0);
+    c->pt.init(d->max_seqs, d->max_pages_per_seq, d->num_pages);
     *out = c;
     sa_status st = sa_kvcache_reset(c, nullptr);
     if (st == SA_OK) {
@@ -334,13 +351,8 @@ extern "C" sa_status sa_kvcache_reset(sa_kvcache* c, sa_stream_t stream) {
     clear_error();
     if (!valid_cache(c)) return fail(SA_EINVAL, "invalid cache");
     hipStream_t st = as_stream(stream);
-    const size_t n_table = c->h_table.size();
-    std::fill(c->h_table.begin(), c->h_table.end(), -1);
-    std::fill(c->h_lens.begin(), c->h_lens.end(), 0);
-    std::fill(c->h_npages.begin(), c->h_npages.end(), 0);
-    c->free_pages.resize(c->desc.num_pages);
-    // Stack: page 0 is handed out first.
-    for (int i = 0; i < c->desc.num_pages; ++i) c->free_pages[i] = c->desc.num_pages - 1 - i;
+    const size_t n_table = (size_t)c->desc.max_seqs * c->desc.max_pages_per_seq;
+    c->pt.reset();
     hipLaunchKernelGGL(fill_i32_kernel, dim3((n_table + 255) / 256), dim3(256), 0, st, c->d_table,
                        n_table, -1);
     SA_CHECK_LAUNCH();
@@ -354,108 +366,67 @@ extern "C" sa_status sa_kvcache_reset(sa_kvcache* c, sa_stream_t stream) {
     return SA_OK;
 }
 
-extern "C" sa_status sa_kvcache_reserve(sa_kvcache* c, int seq, int n_tokens) {
+extern "C" sa_status sa_kvcache_reserve(sa_kvcache* c, int seq, int n_tokens, sa_stream_t stream) {
     clear_error();
     if (!valid_cache(c)) return fail(SA_EINVAL, "invalid cache");
-    if (seq < 0 || seq >= c->desc.max_seqs) return fail(SA_ERANGE, "sequence index out of range");
-    if (n_tokens < 0) return fail(SA_EINVAL, "n_tokens must be >= 0");
-    const int need = (n_tokens + 63) / 64;
-    if (need > c->desc.max_pages_per_seq)
-        return fail(SA_EFULL, "KV cache full, cannot append more tokens");
-    int have = c->h_npages[seq];
-    if (need <= have) return SA_OK;
-    if ((int)c->free_pages.size() < need - have)
-        return fail(SA_EFULL, "KV cache full, cannot append more tokens");
-    const int mp = c->desc.max_pages_per_seq;
-    for (; have < need; ++have) {
-        c->h_table[(size_t)seq * mp + have] = c->free_pages.back();
-        c->free_pages.pop_back();
-    }
-    c->h_npages[seq] = have;
-    return write_table_row(c, seq, nullptr);
+    const int before = c->pt.valid_seq(seq) ? c->pt.npages(seq) : 0;
+    const Verdict v = c->pt.reserve(seq, n_tokens);
+    if (!v.ok()) return refused(v);
+    if (c->pt.npages(seq) == before) return SA_OK;
+    return write_table_row(c, seq, c->pt.npages(seq), as_stream(stream));
 }
 
-extern "C" sa_status sa_kvcache_set_pages(sa_kvcache* c, int seq, const int32_t* pages, int n_pages) {
+extern "C" sa_status sa_kvcache_set_pages(sa_kvcache* c, int seq, const int32_t* pages, int n_pages,
+                                          sa_stream_t stream) {
     clear_error();
     if (!valid_cache(c)) return fail(SA_EINVAL, "invalid cache");
-    if (seq < 0 || seq >= c->desc.max_seqs) return fail(SA_ERANGE, "sequence index out of range");
-    if (n_pages < 0 || n_pages > c->desc.max_pages_per_seq || (n_pages > 0 && !pages))
-        return fail(SA_EINVAL, "bad page list");
-    for (int j = 0; j < n_pages; ++j)
-        if (pages[j] < 0 || pages[j] >= c->desc.num_pages)
-            return fail(SA_ERANGE, "page id out of range");
-    const int mp = c->desc.max_pages_per_seq;
-    // Pages the sequence held go back to the free list unless reused.
-    std::vector<char> used(c->desc.num_pages, 0);
-    for (int j = 0; j < n_pages; ++j) used[pages[j]] = 1;
-    for (int j = 0; j < c->h_npages[seq]; ++j) {
-        const int32_t p = c->h_table[(size_t)seq * mp + j];
-        if (p >= 0 && !used[p]) c->free_pages.push_back(p);
+    const int before = c->pt.valid_seq(seq) ? c->pt.npages(seq) : 0;
+    bool len_cut = false;
+    const Verdict v = c->pt.set_pages(seq, pages, n_pages, &len_cut);
+    if (!v.ok()) return refused(v);
+    hipStream_t st = as_stream(stream);
+    // Entries past the new list become -1 on the device too.
+    SA_TRY(write_table_row(c, seq, std::max(before, n_pages), st));
+    if (len_cut) {
+        const int32_t row = seq;
+        SA_TRY(publish_lens(c, &row, 1, c->pt.len(seq), 0, st));
     }
-    // Pages taken from the free list.
-    std::vector<int32_t> keep;
-    keep.reserve(c->free_pages.size());
-    for (int32_t p : c->free_pages)
-        if (!used[p]) keep.push_back(p);
-    c->free_pages.swap(keep);
-    for (int j = 0; j < mp; ++j) c->h_table[(size_t)seq * mp + j] = j < n_pages ? pages[j] : -1;
-    c->h_npages[seq] = n_pages;
-    if (c->h_lens[seq] > n_pages * 64) c->h_lens[seq] = n_pages * 64;
-    return write_table_row(c, seq, nullptr);
+    return SA_OK;
 }
 
 extern "C" sa_status sa_kvcache_set_len(sa_kvcache* c, int seq, int len, sa_stream_t stream) {
     clear_error();
     if (!valid_cache(c)) return fail(SA_EINVAL, "invalid cache");
-    if (seq < 0 || seq >= c->desc.max_seqs) return fail(SA_ERANGE, "sequence index out of range");
-    if (len < 0 || len > c->h_npages[seq] * 64) return fail(SA_EFULL, "length exceeds reserved pages");
-    c->h_lens[seq] = len;
-    SeqList ids;
-    ids.id[0] = seq;
-    hipLaunchKernelGGL(update_lens_kernel, dim3(1), dim3(32), 0, as_stream(stream), c->d_lens, ids, 1,
-                       len, 0);
-    SA_CHECK_LAUNCH();
-    return SA_OK;
+    const Verdict v = c->pt.set_len(seq, len);
+    if (!v.ok()) return refused(v);
+    const int32_t row = seq;
+    return publish_lens(c, &row, 1, len, 0, as_stream(stream));
 }
 
 extern "C" int sa_kvcache_len(const sa_kvcache* c, int seq) {
-    if (!valid_cache(c) || seq < 0 || seq >= c->desc.max_seqs) return -1;
-    return c->h_lens[seq];
+    if (!valid_cache(c) || !c->pt.valid_seq(seq)) return -1;
+    return c->pt.len(seq);
 }
 
 extern "C" int sa_kvcache_capacity(const sa_kvcache* c, int seq) {
-    if (!valid_cache(c) || seq < 0 || seq >= c->desc.max_seqs) return -1;
-    return c->h_npages[seq] * 64;
+    if (!valid_cache(c) || !c->pt.valid_seq(seq)) return -1;
+    return c->pt.capacity(seq);
 }
 
 extern "C" sa_status sa_kvcache_commit(sa_kvcache* c, const int32_t* seqs, int n_seqs, int n,
                                        sa_stream_t stream) {
     clear_error();
     if (!valid_cache(c)) return fail(SA_EINVAL, "invalid cache");
-    if (n_seqs < 0 || n_seqs > c->desc.max_seqs) return fail(SA_ERANGE, "bad sequence count");
-    if (n < 0) return fail(SA_EINVAL, "n must be >= 0");
-    for (int i = 0; i < n_seqs; ++i) {
-        const int s = seqs ? seqs[i] : i;
-        if (s < 0 || s >= c->desc.max_seqs) return fail(SA_ERANGE, "sequence index out of range");
-        if (c->h_lens[s] + n > c->h_npages[s] * 64)
-            return fail(SA_EFULL, "KV cache full, cannot append more tokens");
-    }
+    const Verdict v = c->pt.commit(seqs, n_seqs, n);
+    if (!v.ok()) return refused(v);
     hipStream_t st = as_stream(stream);
-    for (int i = 0; i < n_seqs; ++i) c->h_lens[seqs ? seqs[i] : i] += n;
     if (!seqs) {
         hipLaunchKernelGGL(add_lens_range_kernel, dim3((n_seqs + 255) / 256), dim3(256), 0, st,
                            c->d_lens, n_seqs, n);
         SA_CHECK_LAUNCH();
         return SA_OK;
     }
-    for (int i0 = 0; i0 < n_seqs; i0 += 32) {
-        SeqList ids;
-        const int m = std::min(32, n_seqs - i0);
-        for (int i = 0; i < m; ++i) ids.id[i] = seqs[i0 + i];
-        hipLaunchKernelGGL(update_lens_kernel, dim3(1), dim3(32), 0, st, c->d_lens, ids, m, n, 1);
-        SA_CHECK_LAUNCH();
-    }
-    return SA_OK;
+    return publish_lens(c, seqs, n_seqs, n, 1, st);
 }
 
 extern "C" sa_status sa_kvcache_get_desc(const sa_kvcache* c, sa_kv_desc* out) {
@@ -515,40 +486,43 @@ extern "C" sa_status sa_qknorm_rope_append(sa_kvcache* c, int layer, const float
     if (q && (!q_out || n_q_heads <= 0)) return fail(SA_EINVAL, "q needs q_out and n_q_heads > 0");
     if (n_seq <= 0 || S <= 0) return fail(SA_EINVAL, "n_seq and S must be positive");
     if ((rope_cos == nullptr) != (rope_sin == nullptr)) return fail(SA_EINVAL, "cos and sin go together");
-    if (!seq_ids) {
-        if (n_seq > c->desc.max_seqs) return fail(SA_ERANGE, "sequence index out of range");
-        for (int i = 0; i < n_seq; ++i)
-            if (c->h_lens[i] + S > c->h_npages[i] * 64)
-                return fail(SA_EFULL, "KV cache full, cannot append more tokens");
-    }
-    if (rope_cos && !seq_ids) {
-        for (int i = 0; i < n_seq; ++i)
-            if (c->h_lens[i] + S > rope_max_pos) return fail(SA_ERANGE, "position beyond RoPE table");
-    }
+    if (rope_cos && rope_max_pos <= 0) return fail(SA_EINVAL, "RoPE table needs rope_max_pos > 0");
+    const Verdict vd = c->pt.check_append(seq_ids, n_seq, S, rope_cos ? rope_max_pos : 0);
+    if (!vd.ok()) return refused(vd);
     AppendArgs a{};
-    a.q = q; a.k = k; a.v = v; a.q_out = q_out;
+    a.q_out = q_out;
     a.wq = q_norm_w; a.wk = k_norm_w; a.cos_t = rope_cos; a.sin_t = rope_sin;
-    a.seq_ids = seq_ids; a.seq_lens = c->d_lens; a.table = c->d_table;
+    a.seq_lens = c->d_lens; a.table = c->d_table;
     a.k_pool = k_pool_of(c, layer); a.v_pool = v_pool_of(c, layer);
     a.n_q = q ? n_q_heads : 0; a.n_kv = c->desc.num_kv_heads; a.S = S;
     a.max_pages = c->desc.max_pages_per_seq; a.rope_max_pos = rope_max_pos; a.eps = eps;
     const int rows = a.n_q + a.n_kv;
-    dim3 grid((rows + 3) / 4, S, n_seq);
+    const int D = c->desc.head_dim;
     hipStream_t st = as_stream(stream);
     const bool bf = c->desc.kv_dtype == SA_DTYPE_BF16;
-    switch (c->desc.head_dim) {
+    // Up to kRowsPerLaunch sequences per launch, their cache rows by value.
+    for (int i0 = 0; i0 < n_seq; i0 += kRowsPerLaunch) {
+        const int m = std::min(kRowsPerLaunch, n_seq - i0);
+        for (int i = 0; i < m; ++i) a.rows.row[i] = seq_ids ? seq_ids[i0 + i] : i0 + i;
+        a.q = q ? q + (size_t)i0 * S * n_q_heads * D : nullptr;
+        a.q_out = q ? q_out + (size_t)i0 * S * n_q_heads * D : nullptr;
+        a.k = k + (size_t)i0 * S * a.n_kv * D;
+        a.v = v + (size_t)i0 * S * a.n_kv * D;
+        dim3 grid((rows + 3) / 4, S, m);
+        switch (D) {
 #define SA_APPEND_CASE(DD)                                                                        \
     case DD:                                                                                      \
         if (bf) hipLaunchKernelGGL((qknorm_rope_append_kernel<DD, true>), grid, dim3(256), 0, st, a); \
         else hipLaunchKernelGGL((qknorm_rope_append_kernel<DD, false>), grid, dim3(256), 0, st, a); \
         break;
-        SA_APPEND_CASE(64)
-        SA_APPEND_CASE(128)
-        SA_APPEND_CASE(256)
+            SA_APPEND_CASE(64)
+            SA_APPEND_CASE(128)
+            SA_APPEND_CASE(256)
 #undef SA_APPEND_CASE
-        default: return fail(SA_EINVAL, "head_dim");
+            default: return fail(SA_EINVAL, "head_dim");
+        }
+        SA_CHECK_LAUNCH();
     }
-    SA_CHECK_LAUNCH();
     return SA_OK;
 }
 
@@ -563,21 +537,11 @@ extern "C" sa_status sa_paged_decode(const sa_kvcache* c, int layer, const float
     clear_error();
     if (!valid_cache(c)) return fail(SA_EINVAL, "invalid cache");
     if (layer < 0 || layer >= c->desc.num_layers) return fail(SA_ERANGE, "Layer index out of range");
-    if (n_pending < 0) return fail(SA_EINVAL, "n_pending must be >= 0");
-    if (n_seq > c->desc.max_seqs && !seq_ids) return fail(SA_ERANGE, "sequence index out of range");
-    // Grid sizing from the host-side lengths (all rows when ids live on the device).
-    const int rows = seq_ids ? c->desc.max_seqs : n_seq;
+    if (n_seq <= 0) return fail(SA_EINVAL, "n_seq must be positive");
     int max_len = 0;
     long long total = 0;
-    for (int i = 0; i < rows; ++i) {
-        const int L = c->h_lens[i] + n_pending;
-        if (!seq_ids && L > c->h_npages[i] * 64)
-            return fail(SA_ERANGE, "Requested seq_len exceeds cached length");
-        max_len = std::max(max_len, L);
-        total += L;
-    }
-    if (seq_ids) total = total * n_seq / std::max(1, rows);
-    max_len = std::min(max_len, c->desc.max_pages_per_seq * 64);
+    const Verdict vd = c->pt.check_decode(seq_ids, n_seq, n_pending, &max_len, &total);
+    if (!vd.ok()) return refused(vd);
     PagedView pv;
     pv.k_pool = k_pool_of(c, layer); pv.v_pool = v_pool_of(c, layer);
     pv.block_table = c->d_table; pv.seq_lens = c->d_lens;
@@ -594,7 +558,7 @@ extern "C" sa_status sa_kvcache_gather(const sa_kvcache* c, int layer, int seq, 
     if (!valid_cache(c)) return fail(SA_EINVAL, "invalid cache");
     if (layer < 0 || layer >= c->desc.num_layers) return fail(SA_ERANGE, "Layer index out of range");
     if (seq < 0 || seq >= c->desc.max_seqs) return fail(SA_ERANGE, "sequence index out of range");
-    if (len < 0 || len > c->h_lens[seq]) return fail(SA_ERANGE, "Requested seq_len exceeds cached length");
+    if (len < 0 || len > c->pt.len(seq)) return fail(SA_ERANGE, "Requested seq_len exceeds cached length");
     if (len == 0) return SA_OK;
     if (!k_out && !v_out) return fail(SA_EINVAL, "null outputs");
     dim3 grid(len, c->desc.num_kv_heads);

@@ -464,12 +464,6 @@ void release(sa_qwen3* m) {
 
 }  // namespace
 
-#define SA_TRY(expr)                      \
-    do {                                  \
-        sa_status _s = (expr);            \
-        if (_s != SA_OK) return _s;       \
-    } while (0)
-
 extern "C" sa_status sa_qwen3_create(const sa_qwen3_desc* desc, int max_batch, sa_qwen3** out) {
     clear_error();
     if (!desc || !out) return fail(SA_EINVAL, "null argument");

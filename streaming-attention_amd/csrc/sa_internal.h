@@ -24,6 +24,12 @@ int device_cu_count();
         if (_e != hipSuccess) return ::sa::hip_fail(_e, #expr); \
     } while (0)
 
+#define SA_TRY(expr)                                       \
+    do {                                                   \
+        sa_status _s = (expr);                             \
+        if (_s != SA_OK) return _s;                        \
+    } while (0)
+
 #define SA_CHECK_LAUNCH()                                  \
     do {                                                   \
         hipError_t _e = hipGetLastError();                 \
@@ -85,6 +91,13 @@ __device__ __forceinline__ float group_reduce(float v) {
     return v;
 }
 
+// Cache rows of the sequences of one launch, passed by value in the kernel
+// arguments (the host has checked every one of them against the page table).
+constexpr int kRowsPerLaunch = 64;
+struct RowList {
+    int32_t row[kRowsPerLaunch];
+};
+
 // ---------------------------------------------------------------------------
 // Entry points implemented in decode.hip, used by the cache glue.
 // ---------------------------------------------------------------------------
@@ -98,6 +111,7 @@ struct PagedView {
 };
 
 size_t paged_ws(int n_seq, int n_q, int n_kv, int d, int max_pages);
+// seq_ids: host array of cache rows (NULL: 0 .. n_seq-1), already checked.
 sa_status decode_paged(const PagedView& c, const float* q, int n_seq, const int32_t* seq_ids,
                        int n_q, int n_pending, int max_len, long long total_len, float scale,
                        float* out, void* ws, size_t ws_bytes, hipStream_t st);

@@ -88,3 +88,10 @@ def stream_inputs(T: int, d: int, seed: int, scale: float = 1.0, outlier_frac: f
         rows = permutation(seed, 4, T)[:n_out]
         K[rows] *= np.float32(outlier_mult)
     return Q, K, V
+
+
+def batch_lengths(B: int = 64, lo: int = 512, hi: int = 32768, seed: int = 70):
+    """Per-sequence context lengths ~ U[lo, hi] (seeded): the ragged batch of
+    the 64-sequence paged decode workload."""
+    u = uniform(seed, 1, B)
+    return [int(lo + min(int(x * (hi - lo + 1)), hi - lo)) for x in u]

@@ -56,7 +56,7 @@ def test_append_gather_roundtrip_shuffled_pages(sa, synth, bf16):
     for s, L in enumerate(lens):
         k = synth.normal(22, s, (1, L, HKV, D))
         v = synth.normal(23, s, (1, L, HKV, D))
-        ids = torch.tensor([s], dtype=torch.int32, device="cuda")
+        ids = [s]
         cache.append(1, None, dev(k), dev(v), seq_ids=ids)
         cache.commit(L, seqs=[s])
         gk, gv = cache.gather(1, s, L)
@@ -116,7 +116,7 @@ def test_paged_decode_matches_oracle(sa, oracle, synth, bf16):
         off += n
         k = synth.normal(27, s, (1, L, HKV, D))
         v = synth.normal(28, s, (1, L, HKV, D))
-        cache.append(0, None, dev(k), dev(v), seq_ids=torch.tensor([s], dtype=torch.int32, device="cuda"))
+        cache.append(0, None, dev(k), dev(v), seq_ids=[s])
         cache.commit(L, seqs=[s])
         ks.append(k[0].transpose(1, 0, 2))
         vs.append(v[0].transpose(1, 0, 2))
@@ -135,19 +135,19 @@ def test_paged_decode_matches_oracle(sa, oracle, synth, bf16):
 
 
 def test_paged_decode_seq_ids_subset(sa, oracle, synth):
-    """Decode a permuted subset of cache rows through device seq_ids."""
+    """Decode a permuted subset of cache rows through host seq_ids."""
     cache = sa.KVCache(1, HKV, D, 4, 20, 64, sa.SA_DTYPE_F32)
     data = {}
     for s, L in enumerate([100, 300, 7, 900]):
         cache.reserve(s, L)
         k = synth.normal(30, s, (1, L, HKV, D))
         v = synth.normal(31, s, (1, L, HKV, D))
-        cache.append(0, None, dev(k), dev(v), seq_ids=torch.tensor([s], dtype=torch.int32, device="cuda"))
+        cache.append(0, None, dev(k), dev(v), seq_ids=[s])
         cache.commit(L, seqs=[s])
         data[s] = (k[0].transpose(1, 0, 2)[None], v[0].transpose(1, 0, 2)[None])
     ids = [3, 0, 2]
     q = synth.normal(32, 1, (3, HQ, D))
-    out = host(cache.decode(0, dev(q), float(SCALE), seq_ids=torch.tensor(ids, dtype=torch.int32, device="cuda")))
+    out = host(cache.decode(0, dev(q), float(SCALE), seq_ids=ids))
     for i, s in enumerate(ids):
         assert_f32(out[i], oracle.decode_gqa(q[i][None], *data[s], SCALE)[0])
     cache.close()
@@ -334,3 +334,125 @@ def test_qk_norm_rope_rejects(sa):
         sa.qk_norm_rope(x, torch.zeros(3, dtype=torch.int32, device="cuda"))
     with pytest.raises(sa.SaError):
         sa.qk_norm_rope(torch.zeros(4, 96, device="cuda"), torch.zeros(4, dtype=torch.int32, device="cuda"))
+
+
+def test_set_pages_shrink_then_decode(sa, oracle, synth):
+    """A 1000-token sequence cut to 4 pages decodes over its first 256 tokens:
+    the device length follows the host's, so the decode sizes its grid and
+    workspace for 256 tokens and reads no partial it did not write."""
+    cache = sa.KVCache(1, HKV, D, 2, 20, 40, sa.SA_DTYPE_F32)
+    pages = [int(p) for p in synth.permutation(33, 1, 40)[:16]]
+    cache.set_pages(0, pages)
+    k = synth.normal(33, 2, (1, 1000, HKV, D))
+    v = synth.normal(33, 3, (1, 1000, HKV, D))
+    cache.append(0, None, dev(k), dev(v), seq_ids=[0])
+    cache.commit(1000, seqs=[0])
+    cache.set_pages(0, pages[:4])
+    assert cache.length(0) == 256 and cache.capacity(0) == 256
+    q = synth.normal(33, 4, (1, HQ, D))
+    out = host(cache.decode(0, dev(q), float(SCALE)))
+    K = k[0, :256].transpose(1, 0, 2)[None]
+    V = v[0, :256].transpose(1, 0, 2)[None]
+    assert_f32(out[0], oracle.decode_gqa(q, K, V, SCALE)[0])
+    # the released pages are free again: another sequence can take them
+    cache.set_pages(1, pages[4:16])
+    cache.close()
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_empty_sequence_decodes_to_zero(sa, oracle, synth, bf16):
+    """In a batch, a sequence with no tokens gets a zero output (as the dense
+    path writes for T = 0); its neighbours are unaffected."""
+    cache = sa.KVCache(1, HKV, D, 3, 40, 60, sa.SA_DTYPE_BF16 if bf16 else sa.SA_DTYPE_F32)
+    lens = [700, 0, 2000]
+    for s, L in enumerate(lens):
+        cache.reserve(s, max(L, 1))
+        if L:
+            k = synth.normal(34, 2 * s, (1, L, HKV, D))
+            v = synth.normal(34, 2 * s + 1, (1, L, HKV, D))
+            cache.append(0, None, dev(k), dev(v), seq_ids=[s])
+            cache.commit(L, seqs=[s])
+    q = synth.normal(34, 9, (3, HQ, D))
+    out = torch.full((3, HQ, D), 7.0, device="cuda")          # stale contents
+    got = host(cache.decode(0, dev(q), float(SCALE), out=out))
+    assert np.all(got[1] == 0.0)
+    for s in (0, 2):
+        gk, gv = cache.gather(0, s, lens[s])
+        assert_f32(got[s], oracle.decode_gqa(q[s][None], host(gk)[None], host(gv)[None], SCALE)[0])
+    cache.close()
+
+
+def test_set_pages_rejects_conflicts(sa):
+    cache = sa.KVCache(1, HKV, D, 3, 8, 10, sa.SA_DTYPE_F32)
+    cache.set_pages(0, [3, 4])
+    with pytest.raises(sa.SaError, match="another sequence") as e:
+        cache.set_pages(1, [5, 4])                 # page 4 is sequence 0's
+    assert e.value.status == sa.SA_EINVAL
+    with pytest.raises(sa.SaError, match="twice") as e:
+        cache.set_pages(1, [6, 6])
+    assert e.value.status == sa.SA_EINVAL
+    cache.set_pages(0, [4, 7])                     # keeps 4, drops 3, takes 7
+    cache.set_pages(1, [3])                        # 3 is free again
+    cache.reserve(2, 64 * 7)                       # the other 7 pages
+    with pytest.raises(sa.SaError) as e:
+        cache.reserve(2, 64 * 8)
+    assert e.value.status == sa.SA_EFULL
+    cache.close()
+
+
+def test_row_ids_checked_before_launch(sa, synth):
+    """With explicit cache rows, an append past a row's pages, a bad row, a
+    repeated row and a decode past a row's pages are refused on the host, and
+    nothing is written."""
+    cache = sa.KVCache(1, HKV, D, 4, 4, 8, sa.SA_DTYPE_F32)
+    cache.reserve(0, 64)
+    cache.reserve(2, 128)
+    k = torch.ones(2, 1, HKV, D, device="cuda")
+    cache.append(0, None, k, k, seq_ids=[2, 0])
+    cache.commit(1, seqs=[2, 0])
+    cache.set_len(0, 64)
+    with pytest.raises(sa.SaError) as e:
+        cache.append(0, None, k, k, seq_ids=[2, 0])   # row 0 is full
+    assert e.value.status == sa.SA_EFULL
+    with pytest.raises(sa.SaError) as e:
+        cache.append(0, None, k, k, seq_ids=[2, 9])   # no row 9
+    assert e.value.status == sa.SA_ERANGE
+    with pytest.raises(sa.SaError) as e:
+        cache.append(0, None, k, k, seq_ids=[2, 2])   # same row twice
+    assert e.value.status == sa.SA_EINVAL
+    q = torch.zeros(2, HQ, D, device="cuda")
+    with pytest.raises(sa.SaError) as e:
+        cache.decode(0, q, 1.0, n_pending=1, seq_ids=[2, 0])   # row 0 has no page for token 64
+    assert e.value.status == sa.SA_ERANGE
+    # the refused calls wrote nothing: row 2 holds one token of ones, row 1
+    # (no pages, no tokens) decodes to zeros
+    got = host(cache.decode(0, torch.ones(2, HQ, D, device="cuda"), 1.0, seq_ids=[2, 1]))
+    assert cache.length(2) == 1 and cache.length(0) == 64
+    np.testing.assert_array_equal(got[0], np.ones((HQ, D), np.float32))
+    np.testing.assert_array_equal(got[1], np.zeros((HQ, D), np.float32))
+    cache.close()
+
+
+def test_cache_on_nonblocking_stream(sa, oracle, synth):
+    """Reset, reserve, set_pages, append, commit and decode issued on one
+    non-blocking stream run in call order (the table and length updates go on
+    that stream)."""
+    side = torch.cuda.Stream()
+    cache = sa.KVCache(1, HKV, D, 2, 16, 32, sa.SA_DTYPE_F32)
+    k = synth.normal(35, 1, (1, 900, HKV, D))
+    v = synth.normal(35, 2, (1, 900, HKV, D))
+    q = synth.normal(35, 3, (1, HQ, D))
+    dk, dv, dq = dev(k), dev(v), dev(q)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(side):
+        for rep in range(3):
+            cache.reset(stream=side)
+            cache.set_pages(1, [int(p) for p in synth.permutation(35, 4 + rep, 32)[:15]], stream=side)
+            cache.append(0, None, dk, dv, seq_ids=[1], stream=side)
+            cache.commit(900, seqs=[1], stream=side)
+            out = cache.decode(0, dq, float(SCALE), seq_ids=[1], stream=side)
+    side.synchronize()
+    K = k[0].transpose(1, 0, 2)[None]
+    V = v[0].transpose(1, 0, 2)[None]
+    assert_f32(host(out)[0], oracle.decode_gqa(q, K, V, SCALE)[0])
+    cache.close()
