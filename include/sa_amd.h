@@ -61,6 +61,19 @@ sa_status sa_stream_attn_f32(const float* Q, const float* K, const float* V,
                              float* O, void* ws, size_t ws_bytes,
                              sa_stream_t stream);
 
+/* The same computation with no workspace argument and no allocation: the
+ * split-KV partials live in a 1 MiB device array of the library (one per GPU,
+ * held until the process ends), which covers every valid T for d <= 256.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The entry point calls no hipMalloc,
+ * hipFree or allocating library routine.  All calls on one GPU share that
+ * array, so calls that overlap on one GPU (concurrent streams or threads)
+ * race; serialise them.  Results equal sa_stream_attn_f32's bit for bit. */
+sa_status sa_stream_attn_f32_noalloc(const float* Q, const float* K, const float* V,
+                                     int T, int d, int block_size, float scale,
+                                     float* O, sa_stream_t stream);
+
 /* ------------------------------------------------------------------------
  * Dense multi-head single-query (decode) attention with grouped KV heads.
  *

@@ -64,6 +64,7 @@ SIGNATURES = {
     "sa_last_error": (C.c_char_p, []),
     "sa_stream_attn_ws_bytes": (_SZ, [_I, _I]),
     "sa_stream_attn_f32": (_I, [_P, _P, _P, _I, _I, _I, _F, _P, _P, _SZ, _P]),
+    "sa_stream_attn_f32_noalloc": (_I, [_P, _P, _P, _I, _I, _I, _F, _P, _P]),
     "sa_decode_dense_ws_bytes": (_SZ, [_I, _I, _I, _I]),
     "sa_decode_dense_f32": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _SZ, _P]),
     "sa_kvcache_create": (_I, [C.POINTER(KvDesc), C.POINTER(_P)]),

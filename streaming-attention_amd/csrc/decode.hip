@@ -25,6 +25,8 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
+#include <mutex>
+#include <vector>
 
 namespace sa {
 namespace {
@@ -671,6 +673,50 @@ sa_status decode_paged(const PagedView& c, const float* q, int n_seq, const int3
     return SA_OK;
 }
 
+// ----- allocation-free single-query entry --------------------------------------
+
+namespace {
+
+// Split-KV partials of sa_stream_attn_f32_noalloc: (m, l) and O per chunk,
+// for the most chunks any call can use (kSplitCap) at the widest head
+// (SA_MAX_HEAD_DIM): 1,056,768 bytes, held by each GPU the library runs on
+// until the process ends.  Nothing in it needs clearing: a call writes every
+// partial it reads.
+constexpr size_t kScratchBytes = (size_t)kSplitCap * (2 + SA_MAX_HEAD_DIM) * sizeof(float);
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+// The device address of this GPU's copy of `scratch`, looked up once per
+// device with that device current.  Host code never passes the array's name
+// itself to a kernel: on the host it is only a stand-in for the symbol.
+sa_status scratch_address(void** out) {
+    static std::mutex mu;
+    static std::vector<void*> per_device;
+    int dev = 0;
+    SA_HIP_TRY(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(mu);
+    if ((int)per_device.size() <= dev) per_device.resize(dev + 1, nullptr);
+    if (!per_device[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol,
+                                                   "hipGetSymbolAddress(scratch)");
+        per_device[dev] = p;
+    }
+    *out = per_device[dev];
+    return SA_OK;
+}
+
+}  // namespace
+
+sa_status stream_attn_noalloc(const float* Q, const float* K, const float* V, int T, int d, float scale,
+                              float* O, hipStream_t st) {
+    const size_t need = decode_dense_ws(1, 1, T, d);
+    if (need > kScratchBytes) return fail(SA_EINVAL, "T and d need more split-KV scratch than the 1 MiB maximum");
+    void* ws = nullptr;
+    SA_TRY(scratch_address(&ws));
+    return decode_dense(Q, K, V, 1, 1, 1, T, d, scale, O, ws, kScratchBytes, st);
+}
+
 }  // namespace sa
 
 // ----- C ABI -------------------------------------------------------------------
@@ -683,6 +729,14 @@ extern "C" sa_status sa_stream_attn_f32(const float* Q, const float* K, const fl
     sa::clear_error();
     if (block_size <= 0) return sa::fail(SA_EINVAL, "block_size must be positive");
     return sa::decode_dense(Q, K, V, 1, 1, 1, T, d, scale, O, ws, ws_bytes, sa::as_stream(stream));
+}
+
+extern "C" sa_status sa_stream_attn_f32_noalloc(const float* Q, const float* K, const float* V, int T,
+                                                int d, int block_size, float scale, float* O,
+                                                sa_stream_t stream) {
+    sa::clear_error();
+    if (block_size <= 0) return sa::fail(SA_EINVAL, "block_size must be positive");
+    return sa::stream_attn_noalloc(Q, K, V, T, d, scale, O, sa::as_stream(stream));
 }
 
 extern "C" size_t sa_decode_dense_ws_bytes(int batch, int n_q_heads, int T, int d) {
