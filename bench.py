@@ -6,8 +6,11 @@ Headline (`value`): single-query streaming attention over a long context,
 T = 262144 tokens, d = 128, fp32 (0.5 N(0,1) with 1% of K rows x8), as HBM
 GB/s of algorithmic traffic (K and V read once, Q read, O written).  Inputs
 are resident in HBM before the timed region; K/V are rotated over replicas
-whose footprint exceeds the 256 MB Infinity Cache, so every step streams from
-HBM.  A step is one call of the library (one kernel launch, merge included).
+whose footprint exceeds the 256 MB Infinity Cache, so every call streams from
+HBM.  A step is a batch of CALLS_PER_STEP back-to-back calls of the library
+(each a split-KV launch and its merge) over the replicas in turn, so even
+--steps 20 times a steady stream of calls rather than the first call's
+submission latency.
 
 `roofline` is computed for that kernel from its average duration measured
 with HIP events on the launch stream.  `cpu_baseline` times the reference's
@@ -36,6 +39,7 @@ sys.path.insert(0, str(ROOT))
 sys.path.insert(0, str(ROOT / "tests"))
 
 HBM_PEAK_GBS = 8000.0
+CALLS_PER_STEP = 25      # one headline step: 25 calls, 5 rounds over the 5 replicas
 BF16_PEAK_TFLOPS = 2500.0
 FP32_PEAK_TFLOPS = 157.3
 METRIC = "decode attn HBM GB/s (% of peak); prefill TFLOP/s; Qwen3-0.6B-shape tok/s"
@@ -113,7 +117,8 @@ def time_batch(torch, fn, steps: int, warmup: int, warm_s: float = 0.0):
 
 # ---------------------------------------------------------------- headline
 
-def bench_stream(torch, sa, synth, T: int, steps: int, warmup: int, min_footprint: float = 1.1e9):
+def bench_stream(torch, sa, synth, T: int, steps: int, warmup: int, min_footprint: float = 1.1e9,
+                 calls_per_step: int = 1):
     log(f"[bench] single-head streaming attention T={T} d=128 fp32: generating inputs")
     Q, K, V = synth.stream_inputs(T, 128, seed=2, scale=0.5, outlier_frac=0.01)
     per_rep = K.nbytes + V.nbytes
@@ -134,10 +139,11 @@ def bench_stream(torch, sa, synth, T: int, steps: int, warmup: int, min_footprin
     bound = [(dQ.data_ptr(), k.data_ptr(), v.data_ptr(), T, 128, 128, 1.0, out.data_ptr(), ws.data_ptr(),
               ws.numel(), stream) for k, v in reps]
 
-    def step(i):
+    def one_call(i):
         sa.check(call(*bound[i % n_rep]))
 
-    kern_ms, wall = time_batch(torch, step, steps, warmup, warm_s=0.5)
+    n_calls = steps * calls_per_step
+    kern_ms, wall = time_batch(torch, one_call, n_calls, warmup * calls_per_step, warm_s=0.5)
     bytes_per = (2 * T * 128 + 2 * 128) * 4
     got = out.cpu().numpy()
     from oracle import Oracle
@@ -146,9 +152,52 @@ def bench_stream(torch, sa, synth, T: int, steps: int, warmup: int, min_footprin
     rl2 = float(np.linalg.norm(got - want) / np.linalg.norm(want))
     del reps
     torch.cuda.empty_cache()
-    return {"T": T, "bytes_per_launch": bytes_per, "kernel_ms": kern_ms, "wall_ms_per_step": wall,
+    return {"T": T, "bytes_per_launch": bytes_per, "kernel_ms": kern_ms, "wall_ms_per_call": wall,
+            "wall_ms_per_step": wall * calls_per_step, "calls_per_step": calls_per_step,
             "gbs": bytes_per / (kern_ms * 1e-3) / 1e9, "wall_gbs": bytes_per / (wall * 1e-3) / 1e9,
-            "replicas": n_rep, "max_abs_err": err, "rel_l2_err": rl2}, (Q, K, V)
+            "replicas": n_rep, "max_abs_err": err, "rel_l2_err": rl2, "gpu_out": got}, (Q, K, V)
+
+
+def fp64_errors(Q, K, V, gpu_out):
+    """Config-2 errors against fp64 brute force: the GPU output, and the
+    reference's own streaming_attention_serial (block 128) when its build is
+    present (relative L2 and max-abs, as compute_l2_error / compute_max_error
+    define them)."""
+    from oracle import Oracle, Reference
+    exact = Oracle().sdpa_f64(Q[None], K, V, 1.0)[0]
+
+    def errs(x):
+        d = np.asarray(x, np.float64) - exact
+        return {"rel_l2_err": float(np.linalg.norm(d) / np.linalg.norm(exact)), "max_abs_err": float(np.abs(d).max())}
+
+    res = {"gpu_vs_fp64": errs(gpu_out)}
+    if Reference.available():
+        res["reference_vs_fp64"] = errs(Reference().streaming_serial(Q, K, V, 128))
+    return res
+
+
+def host_cpu() -> dict:
+    """The host the CPU baselines run on: model, sockets x cores x threads as
+    lscpu reports them, the CPUs this process may use, and the OpenMP thread
+    count the baselines run with."""
+    info = {}
+    try:
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        kv = dict(line.split(":", 1) for line in out.splitlines() if ":" in line)
+        kv = {k.strip(): v.strip() for k, v in kv.items()}
+        info = {"model": kv.get("Model name"), "sockets": int(kv.get("Socket(s)", 0) or 0),
+                "cores_per_socket": int(kv.get("Core(s) per socket", 0) or 0),
+                "threads_per_core": int(kv.get("Thread(s) per core", 0) or 0),
+                "logical_cpus": int(kv.get("CPU(s)", 0) or 0)}
+    except Exception as e:      # lscpu absent: report what Python knows
+        info = {"model": None, "error": str(e)}
+    try:
+        info["cpus_allowed"] = len(os.sched_getaffinity(0))
+    except AttributeError:
+        info["cpus_allowed"] = os.cpu_count()
+    info["omp_threads"] = _cpu_threads()
+    return info
 
 
 def cpu_baseline(Q, K, V, budget_s: float = 10.0):
@@ -172,14 +221,21 @@ def cpu_baseline(Q, K, V, budget_s: float = 10.0):
     gbs = (2 * T * 128 + 2 * 128) * 4 / med / 1e9
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": kind,
             "sample": f"streaming_attention_omp, T={T}, d=128, block 128, {len(times)} timed calls "
-                      f"(median {med * 1e3:.2f} ms) after 2 warmups, {threads} OpenMP threads"}
+                      f"(median {med * 1e3:.2f} ms) after 2 warmups, {threads} OpenMP threads",
+            "host": host_cpu()}
 
 
 def _cpu_threads() -> int:
+    """OpenMP threads for the CPU baselines: OMP_NUM_THREADS when set (the
+    process's CPU share on a shared host), else every CPU this process may
+    use."""
     omp = os.environ.get("OMP_NUM_THREADS")
     if omp and omp.isdigit():
         return int(omp)
-    return os.cpu_count() or 1
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
 
 
 def cpu_layer_decode(steps: int = 100, warm: int = 2):
@@ -192,7 +248,7 @@ def cpu_layer_decode(steps: int = 100, warm: int = 2):
     threads = _cpu_threads()
     secs = Reference().time_decode_layer(8, 8, 16, 8, 128, 1, 128 - warm, steps + warm, threads)[warm:]
     total = float(secs.sum())
-    return {"value": round(steps / total, 1), "unit": "steps/s", "cores": threads, "kind": "reference",
+    return {"value": round(steps / total, 1), "unit": "steps/s", "cores": threads, "kind": "reference", "host": host_cpu(),
             "sample": f"qwen3_decoder_layer_avx_with_cache STREAMING, hidden 8, {steps} steps over "
                       f"cached lengths 128..{127 + steps} after {warm} warmup steps; median "
                       f"{float(np.median(secs)) * 1e6:.0f} us/step"}
@@ -220,7 +276,7 @@ def cpu_prefill(L: int):
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
     tf = 2.0 * HQ * D * L * (L + 1) / med / 1e12
-    return {"value": round(tf, 4), "unit": "TFLOP/s", "cores": threads, "kind": "reference",
+    return {"value": round(tf, 4), "unit": "TFLOP/s", "cores": threads, "kind": "reference", "host": host_cpu(),
             "sample": f"self_attention_streaming_blockwise_avx2, L={L}, 16 heads, blocks 128/128, "
                       f"{reps} timed call(s), median {med:.3f} s"}
 
@@ -238,6 +294,7 @@ def cpu_model_decode(sum_len: int, B: int = 64, layers: int = 28, steps: int = 3
     secs = Reference().time_decode_layer(1024, 3072, 16, 8, 128, 1, L, steps + 1, threads)[1:]
     med = float(np.median(secs))
     return {"value": round(1.0 / (layers * med), 4), "unit": "tok/s", "cores": threads, "kind": "reference",
+            "host": host_cpu(),
             "sample": f"qwen3_decoder_layer_avx_with_cache STREAMING at hidden 1024, one sequence of "
                       f"{L} cached tokens (the mean of the batch), {steps} timed calls after 1 warmup, "
                       f"median {med * 1e3:.1f} ms per layer; tok/s = 1 / (28 x that), lm_head excluded"}
@@ -547,7 +604,9 @@ def main() -> int:
     if args.profile_copy:
         log("[bench] 1 GiB device copy (counter calibration)")
         calib = copy_calibration(torch)
-    head, (Q, K, V) = bench_stream(torch, sa, synth, args.T, args.steps, args.warmup)
+    head, (Q, K, V) = bench_stream(torch, sa, synth, args.T, args.steps, args.warmup,
+                                   calls_per_step=CALLS_PER_STEP)
+    head_fp64 = fp64_errors(Q, K, V, head["gpu_out"])
     log(f"[bench] headline: {head['gbs']:.1f} GB/s kernel, {head['wall_gbs']:.1f} GB/s wall, "
         f"err {head['max_abs_err']:.2e}")
     extra = {}
@@ -559,10 +618,11 @@ def main() -> int:
         extra["single_head_T1024"]["hbm_frac"] = round(c1["gbs"] / HBM_PEAK_GBS, 5)
         for T in (8192, 65536):
             log(f"[bench] single-head T={T}")
-            c2, _ = bench_stream(torch, sa, synth, T, 50, 5)
+            c2, (q2, k2, v2) = bench_stream(torch, sa, synth, T, 200, 5)
             extra[f"single_head_T{T}"] = {"kernel_ms": c2["kernel_ms"], "gbs": round(c2["gbs"], 1),
                                           "hbm_frac": round(c2["gbs"] / HBM_PEAK_GBS, 4),
-                                          "rel_l2_err": c2["rel_l2_err"]}
+                                          "rel_l2_err": c2["rel_l2_err"], "max_abs_err": c2["max_abs_err"],
+                                          **fp64_errors(q2, k2, v2, c2["gpu_out"])}
     from oracle import Reference
     cpu_extra = args.cpu_budget >= 1.0 and Reference.available()
     if run("layer"):
@@ -607,14 +667,16 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic (seeded splitmix64 + Box-Muller, 0.5 N(0,1), 1% K rows x8)",
         "config": {"workload": f"single-query streaming attention, T={args.T}, d=128, block 128, fp32",
-                   "T": args.T, "head_dim": 128, "block": 128, "replicas": head["replicas"]},
+                   "T": args.T, "head_dim": 128, "block": 128, "replicas": head["replicas"],
+                   "calls_per_step": CALLS_PER_STEP},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(args.T),
                      "kernel": "decode call = split_kv_decode_kernel<128,1,f32,dense> + lse_merge_kernel",
                      "kernel_ms": round(head["kernel_ms"], 5),
                      "algorithmic_bytes_per_launch": head["bytes_per_launch"]},
         "cpu_baseline": cpu,
-        "parity": {"max_abs_err": head["max_abs_err"], "rel_l2_err": head["rel_l2_err"]},
+        "parity": {"max_abs_err": head["max_abs_err"], "rel_l2_err": head["rel_l2_err"],
+                   "against": "oracle streaming_attention_serial, fp32, block 128", **head_fp64},
         "extra": extra,
     }
     if calib:

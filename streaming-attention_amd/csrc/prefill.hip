@@ -827,6 +827,334 @@ prefill_bf16_dma_kernel(PrefillArgs pa) {
 }
 
 // ===========================================================================
+// bf16 kernel, head_dim 128, load-unit tiles, folded softmax
+// ===========================================================================
+// The load-to-LDS kernel's data movement and schedules with less softmax
+// work per score:
+//   * q is pre-scaled once, q' = bf16(q * scale * log2 e), and the score MFMA
+//     chain starts from -m (a register block holding the running max of each
+//     query column), so the MFMA delivers s' = q'.k - m and p = 2^s' needs no
+//     multiply or subtract;
+//   * no per-tile row max: a lane's 16 p values are summed (bf16 dot products
+//     of the packed P that the PV product uses), and only when a sum exceeds
+//     2^16, which bounds every p by 2^16, does a slow path compute the row max,
+//     raise m (rescaling O and the row sum), and recompute P; the first tile
+//     of a wave always takes it (m starts at -inf, the bias at 0);
+//   * the row sums use the bf16 P of the PV product, so the normalised
+//     weights are the ones applied.
+constexpr float kSumCap = 65536.f;
+
+// acc + the sum of the 8 bf16 values of v (v_dot2c_f32_bf16 against 1.0).
+// The pairs are taken with shufflevector: bit-casting the 32-bit elements of
+// the vector to bf16 pairs made hipcc (ROCm 7.2) feed the first pair to all
+// four dot products.
+__device__ __forceinline__ float sum_bf16x8(const bf16x8_t& v, float acc) {
+    const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 0, 1), one, acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 2, 3), one, acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 4, 5), one, acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 6, 7), one, acc, false);
+    return acc;
+}
+
+__device__ __forceinline__ bf16x8_t pack_bf16x8(const float* p) {
+    const bf16x2_t p01 = __builtin_convertvector(f32x2_t{p[0], p[1]}, bf16x2_t);
+    const bf16x2_t p23 = __builtin_convertvector(f32x2_t{p[2], p[3]}, bf16x2_t);
+    const bf16x2_t p45 = __builtin_convertvector(f32x2_t{p[4], p[5]}, bf16x2_t);
+    const bf16x2_t p67 = __builtin_convertvector(f32x2_t{p[6], p[7]}, bf16x2_t);
+    return __builtin_bit_cast(bf16x8_t, make_uint4(__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23),
+                                                   __builtin_bit_cast(uint32_t, p45), __builtin_bit_cast(uint32_t, p67)));
+}
+
+template <int W, int NS>
+__global__ void __launch_bounds__(W * 64)
+prefill_bf16_fold_kernel(PrefillArgs pa) {
+    constexpr int NKS = 8;          // k-steps of the score product
+    constexpr int NDB = 4;          // 32-row d blocks of O^T
+    constexpr int NI = 16 / W;      // loads per wave, tensor and tile (64 lanes x 16 bytes each)
+    extern __shared__ __align__(16) unsigned char smem[];
+    lds_u8_t* const lsm = (lds_u8_t*)smem;
+
+    const int L = pa.L;
+    const Work wk = map_work(pa, blockIdx.x);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = lane & 31;
+    const int hh = lane >> 5;
+
+    const int wph = W / pa.gh;
+    const int qtile = wph * 32;
+    const int h = wk.h0 + wave / wph;
+    const uint16_t* Q = static_cast<const uint16_t*>(pa.q) + wk.b * pa.qs[0] + h * pa.qs[1];
+    const uint16_t* K = static_cast<const uint16_t*>(pa.k) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
+    const uint16_t* V = static_cast<const uint16_t*>(pa.v) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
+    const int kv_row = static_cast<int>(pa.kvs[2]);
+
+    const int q_wave0 = wk.qt * qtile + (wave % wph) * 32;
+    const int n_kt = (min(L, (wk.qt + 1) * qtile) - 1) / kKTile + 1;
+    const int wave_kt = q_wave0 < L ? (q_wave0 + 31) / kKTile + 1 : 0;
+
+    int d_row[NI], d_col[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int r = 4 * (wave * NI + i) + lane / 16;
+        d_row[i] = r;
+        d_col[i] = 8 * ((lane % 16) ^ dma_swz(r & 15));
+    }
+    auto dma_tile = [&](int kt, int stage) {
+        const int key0 = kt * kKTile;
+        lds_u8_t* sb = lsm + stage * kDmaStageBytes;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const long long e = (long long)min(key0 + d_row[i], L - 1) * kv_row + d_col[i];
+            lds_u8_t* dst = sb + (wave * NI + i) * 1024;
+            dma16(K + e, dst);
+            dma16(V + e, dst + kDmaTileBytes);
+        }
+    };
+#pragma unroll
+    for (int s = 0; s < (W == 8 ? NS : NS - 1); ++s) dma_tile(s, s);
+
+    // q' = bf16(q * scale * log2 e): the scores come out in the log2 domain.
+    bf16x8_t qf[NKS];
+    {
+        const float sq = pa.scale * kLog2eP;
+        const int qi = min(q_wave0 + n, L - 1);
+        const uint16_t* qrow = Q + qi * pa.qs[2] + 8 * hh;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+            const u32x4_t raw = *reinterpret_cast<const u32x4_t*>(qrow + ks * 16);
+            float x[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                x[2 * i] = bf16_lo(raw[i]) * sq;
+                x[2 * i + 1] = bf16_hi(raw[i]) * sq;
+            }
+            qf[ks] = pack_bf16x8(x);
+        }
+    }
+    f32x16_t acc[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) acc[db] = f32x16_t{};
+    float ms = -INFINITY;      // running max of this query (log2 domain) at the last raise
+    float lp = 0.f;            // this lane's part of the row sum
+    float cap = -1.f;          // kSumCap once ms is finite: the first tile always raises
+    f32x16_t negm = {};        // -ms in every element (0 while ms = -inf): the score chain's start
+
+    int k_off[NKS];
+    {
+        const int r = swap_bits23(n);
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) k_off[ks] = r * kDmaRowBytes + (((2 * ks + hh) ^ dma_swz(r & 15)) << 4);
+    }
+    int v_off[2][NDB];
+    {
+        const int g = lane >> 4, j = lane & 15;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int r = 8 * hh + 4 * u + j / 4;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) {
+                const int col = 32 * db + 16 * (g & 1) + 4 * (j & 3);
+                v_off[u][db] = kDmaTileBytes + r * kDmaRowBytes + (((col >> 3) ^ dma_swz(r & 15)) << 4) + (col & 7) * 2;
+            }
+        }
+    }
+    auto lds_k = [&](const lds_u8_t* sb, int kb, int ks) {
+        return *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(sb + kb * 32 * kDmaRowBytes +
+                                                                                     k_off[ks]);
+    };
+    auto lds_vt = [&](const lds_u8_t* sb, int kb, int t, int db) {
+        const lds_u8_t* p = sb + (kb * 32 + t * 16) * kDmaRowBytes;
+        const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(p + v_off[0][db]));
+        const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(p + v_off[1][db]));
+        return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    };
+
+    constexpr int VM = (NS - 2) * 2 * NI;
+    static_assert(VM == 0 || VM == 4 || VM == 8, "vmcnt literal");
+    auto next_tile_ready = [&]() {
+        if constexpr (VM == 0) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        else if constexpr (VM == 4) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+    if constexpr (W == 8) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else next_tile_ready();   // tile 0
+
+    // Scores of one 32-key half, biased by -m: element j is key 16 (j/8) +
+    // 8 hh + j%8 of the half for query q_wave0 + n.
+    auto scores = [&](const bf16x8_t (&kf)[NKS]) {
+        f32x16_t s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0], qf[0], negm, 0, 0, 0);
+#pragma unroll
+        for (int ks = 1; ks < NKS; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qf[ks], s, 0, 0, 0);
+        return s;
+    };
+    // P = 2^s as the PV product's B operand, and this lane's sum of it.
+    auto softmax = [&](const f32x16_t& s, bf16x8_t (&pb)[2]) {
+        float p[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) p[j] = __builtin_amdgcn_exp2f(s[j]);
+        pb[0] = pack_bf16x8(p);
+        pb[1] = pack_bf16x8(p + 8);
+        return sum_bf16x8(pb[1], sum_bf16x8(pb[0], 0.f));
+    };
+    // Raise m to the row max of this half when the sum left the cap (or m is
+    // still -inf): O and the row sum are rescaled and P recomputed.
+    auto settle = [&](const f32x16_t& s, bf16x8_t (&pb)[2], float& rs) {
+        if (!__any(!(rs <= cap))) return;
+        float mt = s[0];
+#pragma unroll
+        for (int j = 1; j < 16; ++j) mt = fmaxf(mt, s[j]);
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+        const float b = negm[0];
+        const float mq = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) - b;   // unbiased row max
+        const float m_new = fmaxf(ms, mq);
+        const float alpha = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - m_new);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) acc[db] *= alpha;
+        lp *= alpha;
+        const float b_new = m_new == -INFINITY ? 0.f : -m_new;
+        const float delta = b_new - b;
+        float p[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) p[j] = __builtin_amdgcn_exp2f(s[j] + delta);
+        pb[0] = pack_bf16x8(p);
+        pb[1] = pack_bf16x8(p + 8);
+        rs = sum_bf16x8(pb[1], sum_bf16x8(pb[0], 0.f));
+        ms = m_new;
+        cap = m_new == -INFINITY ? -1.f : kSumCap;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) negm[j] = b_new;
+    };
+
+    // One tile from stage sb (W = 4, leftover tiles and the diagonal): per
+    // 32-key half, scores, mask, P, settle, PV.
+    auto tile = [&](int kt, const lds_u8_t* sb, auto diag_tag) {
+        constexpr bool DIAG = decltype(diag_tag)::value;
+        bf16x8_t kf[NKS];
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) kf[ks] = lds_k(sb, 0, ks);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            f32x16_t s = scores(kf);
+            if constexpr (DIAG) {
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    if (kt * kKTile + 32 * kb + 16 * (j / 8) + 8 * hh + (j % 8) > q_wave0 + n) s[j] = -INFINITY;
+            }
+            bf16x8_t vf[NDB][2];
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int t = 0; t < 2; ++t) vf[db][t] = lds_vt(sb, kb, t, db);
+            bf16x8_t pb[2];
+            float rs = softmax(s, pb);
+            settle(s, pb, rs);
+            lp += rs;
+            if (kb == 0) {
+#pragma unroll
+                for (int ks = 0; ks < NKS; ++ks) kf[ks] = lds_k(sb, 1, ks);
+            }
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+                    acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][t], pb[t], acc[db], 0, 0, 0);
+        }
+    };
+
+    if constexpr (W == 8) {
+        // Ping-pong schedule of the load-to-LDS kernel: waves w and w + 4
+        // share a SIMD; per 32-key half an MFMA block (the previous half's PV,
+        // then this half's scores) and a softmax block, with waves 4-7 taking
+        // the half's barrier between them and waves 0-3 after both.
+        static_assert(NS == 2 && NI == 2, "ping-pong schedule: two stages, two loads per tensor tile");
+        const bool late = wave >= W / 2;
+        bf16x8_t pv_v[NDB][2];
+        bf16x8_t pv_p[2];
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) pv_v[db][0] = pv_v[db][1] = bf16x8_t{};
+        pv_p[0] = pv_p[1] = bf16x8_t{};
+        auto flush = [&]() {
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+                    acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pv_v[db][t], pv_p[t], acc[db], 0, 0, 0);
+        };
+        auto end_tile = [&](int kt, int stage) {
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            if (kt + NS < n_kt) dma_tile(kt + NS, stage);
+        };
+        auto half = [&](int kt, int stage, int kb) {
+            const lds_u8_t* sb = lsm + stage * kDmaStageBytes;
+            bf16x8_t kf[NKS];
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) kf[ks] = lds_k(sb, kb, ks);
+            flush();
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int t = 0; t < 2; ++t) pv_v[db][t] = lds_vt(sb, kb, t, db);
+            const f32x16_t s = scores(kf);
+            auto sync = [&]() {
+                __builtin_amdgcn_sched_barrier(0);
+                if (kb == 0) asm volatile("s_barrier" ::: "memory");
+                else end_tile(kt, stage);
+                __builtin_amdgcn_sched_barrier(0);
+            };
+            if (late) sync();
+            float rs = softmax(s, pv_p);
+            settle(s, pv_p, rs);
+            lp += rs;
+            if (!late) sync();
+        };
+        const int kt_pp = (wk.qt * qtile + 31) / kKTile / NS * NS;
+        for (int kt = 0; kt < kt_pp; kt += NS) {
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                half(kt + s, s, 0);
+                half(kt + s, s, 1);
+            }
+        }
+        flush();
+        for (int kt = kt_pp; kt < n_kt; ++kt) {
+            const int stage = kt % NS;
+            if (kt + 1 < wave_kt) tile(kt, lsm + stage * kDmaStageBytes, std::false_type{});
+            end_tile(kt, stage);
+        }
+    } else {
+        auto step = [&](int kt, int stage) {
+            const bool more = kt + NS - 1 < n_kt;
+            if (more) dma_tile(kt + NS - 1, (stage + NS - 1) % NS);
+            if (kt + 1 < wave_kt) tile(kt, lsm + stage * kDmaStageBytes, std::false_type{});
+            if (more) next_tile_ready();
+            else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        };
+        const int n_steps = (n_kt + NS - 1) / NS * NS;
+        for (int kt = 0; kt < n_steps; kt += NS) {
+#pragma unroll
+            for (int s = 0; s < NS; ++s) step(kt + s, s);
+        }
+    }
+    if (wave_kt > 0) tile(wave_kt - 1, lsm + ((wave_kt - 1) % NS) * kDmaStageBytes, std::true_type{});
+
+    const float l = lp + __shfl_xor(lp, 32, 64);
+    const int qi = q_wave0 + n;
+    if (qi < L) {
+        const float inv = 1.0f / l;
+        float* orow = pa.out + wk.b * pa.os[0] + h * pa.os[1] + qi * pa.os[2] + 4 * hh;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+                *reinterpret_cast<float4*>(orow + 32 * db + 8 * jj) =
+                    make_float4(acc[db][4 * jj] * inv, acc[db][4 * jj + 1] * inv, acc[db][4 * jj + 2] * inv,
+                                acc[db][4 * jj + 3] * inv);
+    }
+}
+
+// ===========================================================================
 // fp32 kernel
 // ===========================================================================
 constexpr int kFQTile = 128;    // queries per workgroup
@@ -1079,6 +1407,16 @@ template <int W>
 sa_status launch_bf16_dma(const PrefillArgs& pa, dim3 grid, hipStream_t st) {
     constexpr int NS = dma_stages<W>();
     constexpr int bytes = NS * kDmaStageBytes;
+    static const bool fold = [] {
+        const char* e = std::getenv("SA_PREFILL_FOLD");
+        return !e || std::atoi(e) != 0;
+    }();
+    if (fold) {
+        sa_status s = opt_in_lds<&prefill_bf16_fold_kernel<W, NS>>(bytes);
+        if (s != SA_OK) return s;
+        hipLaunchKernelGGL((prefill_bf16_fold_kernel<W, NS>), grid, dim3(W * 64), bytes, st, pa);
+        return SA_OK;
+    }
     sa_status s = opt_in_lds<&prefill_bf16_dma_kernel<W, NS>>(bytes);
     if (s != SA_OK) return s;
     hipLaunchKernelGGL((prefill_bf16_dma_kernel<W, NS>), grid, dim3(W * 64), bytes, st, pa);
