@@ -29,63 +29,12 @@
 #include <numeric>
 #include <type_traits>
 
-#include "sa_internal.h"
+#include "prefill_shared.h"
 
 namespace sa {
 namespace {
+using namespace pf;
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-// Staging registers use the native vector type: HIP's uint4 is a struct whose
-// copies lower to memcpy and end up in scratch memory.
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-
-constexpr int kKTile = 64;    // keys per LDS tile (both kernels)
-constexpr float kLog2eP = 1.4426950408889634f;
-
-struct PrefillArgs {
-    const void* q;
-    const void* k;
-    const void* v;
-    float* out;
-    long long qs[3];    // element strides {batch, head, row} of q
-    long long kvs[3];   // of k and v
-    long long os[3];    // of out
-    int Hq, Hkv, L;
-    int n_qt;           // query tiles per head
-    int xcd_groups;     // KV groups per XCD when the grid maps groups to XCDs, else 0
-    int gh;             // query heads per workgroup (divides Hq / Hkv)
-    float sl2;          // |scale| * log2(e)
-    uint32_t q_sign;    // 0x80008000 to negate bf16 q pairs (negative scale), else 0
-    float scale;        // signed scale (fp32 kernel)
-};
-
-// Work mapping shared by both kernels.  A KV group is one (batch, kv head);
-// its G = Hq/Hkv query heads read the same K/V, and a workgroup serves gh of
-// them (so G/gh workgroups share each query tile).  When the number of groups
-// is a multiple of 8, hardware workgroup i (dispatched to XCD i % 8) takes
-// work slot i / 8 of the groups owned by that XCD, so each XCD's L2 holds the
-// K/V of its own groups only.  Inside an XCD (or the whole grid otherwise)
-// slots run heaviest query tile first, which balances the causal triangle.
-struct Work { int b, h0, kvh, qt; };
-__device__ __forceinline__ Work map_work(const PrefillArgs& pa, int i) {
-    const int G = pa.Hq / pa.Hkv;
-    const int HS = G / pa.gh;                         // head sets per group
-    int x = 0, j = i, span = gridDim.x / (HS * pa.n_qt);   // groups in this slot range
-    if (pa.xcd_groups) { x = i & 7; j = i >> 3; span = pa.xcd_groups; }
-    const int per_qt = span * HS;
-    Work w;
-    w.qt = pa.n_qt - 1 - j / per_qt;
-    const int rem = j % per_qt;
-    const int group = x * span + rem / HS;
-    w.b = group / pa.Hkv;
-    w.kvh = group % pa.Hkv;
-    w.h0 = w.kvh * G + (rem % HS) * pa.gh;
-    return w;
-}
 
 // ===========================================================================
 // bf16 kernel
@@ -112,13 +61,6 @@ struct BfLds {
     static_assert(V_ITEMS % THREADS == 0 || THREADS % V_ITEMS == 0, "V items must tile the workgroup");
 };
 
-// The K rows a lane feeds to the score MFMA are permuted within each 32-key
-// block (bits 2 and 3 of the row swapped).  With the 32x32 output layout
-// (lane l: column l%32, rows 8*(j/4) + 4*(l/32) + j%4 for element j) this
-// makes element j of lane l the score of key 16*(j/8) + 8*(l/32) + j%8: each
-// lane's 8-element groups are 8 consecutive keys, exactly what the B operand
-// of the 32x32x16 PV step needs, and what one 16-byte read of V^T supplies.
-__device__ __forceinline__ int swap_bits23(int m) { return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1); }
 
 template <int D, int W>
 struct BfStage {
@@ -451,386 +393,22 @@ prefill_bf16_kernel(PrefillArgs pa) {
 }
 
 // ===========================================================================
-// bf16 kernel, head_dim 128, tiles moved by the load unit
+// bf16 kernel, head_dim 128, tiles moved by the load unit, folded softmax
 // ===========================================================================
-// Same per-wave work as prefill_bf16_kernel (one 32-query block per wave, a
-// lazily raised running max), but tiles go from global memory straight into
-// LDS with global_load_lds_dwordx4: no staging registers, no LDS stores, no
-// V transposition on the way in.  K and V sit row-major in LDS (256-byte
-// rows) with the 16-byte chunks of row r permuted by dma_swz(r); the V^T
-// fragments of the PV product come from ds_read_b64_tr_b16.  NS stages: tile
-// kt + NS - 1 is loaded while tile kt is computed.  Tiles past the last one
-// are never loaded, so the stages of the last NS - 1 tiles are intact after
-// the loop; every wave's diagonal tile is among them (the launch checks that
-// a workgroup's queries span at most NS - 1 tiles) and is processed there,
+// One 32-query block per wave, like prefill_bf16_kernel, with two changes.
+//
+// Data movement: tiles go from global memory straight into LDS with
+// global_load_lds_dwordx4: no staging registers, no LDS stores, no V
+// transposition on the way in.  K and V sit row-major in LDS (256-byte rows)
+// with the 16-byte chunks of row r permuted by dma_swz(r); the V^T fragments
+// of the PV product come from ds_read_b64_tr_b16.  NS stages: tile kt + NS - 1
+// is loaded while tile kt is computed.  Tiles past the last one are never
+// loaded, so the stages of the last NS - 1 tiles are intact after the loop;
+// every wave's diagonal tile is among them (the launch checks that a
+// workgroup's queries span at most NS - 1 tiles) and is processed there,
 // which keeps the mask out of the main loop.
-constexpr int kDmaRowBytes = 256;                     // one row of 128 bf16
-constexpr int kDmaTileBytes = kKTile * kDmaRowBytes;  // one tensor's tile
-constexpr int kDmaStageBytes = 2 * kDmaTileBytes;     // K, then V
-
-// Chunk c (16 bytes) of tile row r sits at chunk position c ^ dma_swz(r) of
-// the row.  Exhaustive check over the lane patterns: the K fragment reads (16
-// lanes, 16 rows, one chunk) and the V transpose reads (32 lanes, 2 x 4 rows,
-// 4 chunks) touch 64 distinct banks per cycle.
-__device__ __forceinline__ int dma_swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
-
-typedef short s16x4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) unsigned char lds_u8_t;
-typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
-
-// One global_load_lds_dwordx4: lane l copies 16 bytes from g into LDS at dst
-// + 16 l.  Issued as inline assembly so that the compiler does not track it:
-// its wait-count pass makes every LDS read after a load-to-LDS wait for all
-// of them (vmcnt(0)), which would drain the tile prefetched NS - 1 tiles ahead
-// in the middle of each tile.  The kernel waits for these loads itself
-// (s_waitcnt vmcnt before each tile barrier).  m0 holds the LDS address; the
-// s_nop covers the m0-write-to-load-to-LDS hazard.
-__device__ __forceinline__ void dma16(const uint16_t* g, lds_u8_t* dst) {
-    const uint32_t m = static_cast<uint32_t>(reinterpret_cast<size_t>(dst));
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m) : "memory", "m0");
-}
-
-template <int W, int NS>
-__global__ void __launch_bounds__(W * 64)
-prefill_bf16_dma_kernel(PrefillArgs pa) {
-    constexpr int NKS = 8;          // k-steps of the score product
-    constexpr int NDB = 4;          // 32-row d blocks of O^T
-    constexpr int NI = 16 / W;      // loads per wave, tensor and tile (64 lanes x 16 bytes each)
-    extern __shared__ __align__(16) unsigned char smem[];
-    lds_u8_t* const lsm = (lds_u8_t*)smem;
-
-    const int L = pa.L;
-    const Work wk = map_work(pa, blockIdx.x);
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int n = lane & 31;
-    const int hh = lane >> 5;
-    const float sl2 = pa.sl2;
-
-    const int wph = W / pa.gh;
-    const int qtile = wph * 32;
-    const int h = wk.h0 + wave / wph;
-    const uint16_t* Q = static_cast<const uint16_t*>(pa.q) + wk.b * pa.qs[0] + h * pa.qs[1];
-    const uint16_t* K = static_cast<const uint16_t*>(pa.k) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
-    const uint16_t* V = static_cast<const uint16_t*>(pa.v) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
-    const int kv_row = static_cast<int>(pa.kvs[2]);
-
-    const int q_wave0 = wk.qt * qtile + (wave % wph) * 32;
-    const int n_kt = (min(L, (wk.qt + 1) * qtile) - 1) / kKTile + 1;
-    const int wave_kt = q_wave0 < L ? (q_wave0 + 31) / kKTile + 1 : 0;
-
-    // Load i of this wave fills chunk positions 64 (wave NI + i) + lane of a
-    // tensor tile: row r = 4 (wave NI + i) + lane / 16, position lane % 16,
-    // which holds global chunk (lane % 16) ^ dma_swz(r).
-    int d_row[NI], d_col[NI];
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-        const int r = 4 * (wave * NI + i) + lane / 16;
-        d_row[i] = r;
-        d_col[i] = 8 * ((lane % 16) ^ dma_swz(r & 15));
-    }
-    // Rows past the end of the sequence are clamped to the last row: they
-    // only feed keys that the causal mask removes.
-    auto dma_tile = [&](int kt, int stage) {
-        const int key0 = kt * kKTile;
-        lds_u8_t* sb = lsm + stage * kDmaStageBytes;
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const long long e = (long long)min(key0 + d_row[i], L - 1) * kv_row + d_col[i];
-            lds_u8_t* dst = sb + (wave * NI + i) * 1024;
-            dma16(K + e, dst);
-            dma16(V + e, dst + kDmaTileBytes);
-        }
-    };
-#pragma unroll
-    for (int s = 0; s < (W == 8 ? NS : NS - 1); ++s) dma_tile(s, s);
-
-    bf16x8_t qf[NKS];
-    {
-        const int qi = min(q_wave0 + n, L - 1);
-        const uint16_t* qrow = Q + qi * pa.qs[2] + 8 * hh;
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-            // Q stays in arch VGPRs: any AGPR use caps arch VGPRs at 128 and
-            // the LDS addresses would then be kept in AGPRs.
-            const u32x4_t raw = *reinterpret_cast<const u32x4_t*>(qrow + ks * 16) ^ pa.q_sign;
-            qf[ks] = __builtin_bit_cast(bf16x8_t, raw);
-        }
-    }
-    f32x16_t acc[NDB];
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) acc[db] = f32x16_t{};
-    float ms = -INFINITY, lp = 0.f;
-
-    // Fragment offsets (bytes within a stage).  K (score A operand): lane
-    // (n, hh) reads row swap_bits23(n) (+ 32 kb), chunk 2 ks + hh.  V^T (PV A
-    // operand): transpose read u of d block db; lane j of 16-lane group g
-    // addresses 4 bf16 of row 8 hh + 4 u + j / 4 (+ 16 t + 32 kb), columns
-    // 32 db + 16 (g % 2) + 4 (j % 4) .. + 3, and receives 4 consecutive keys
-    // of column 32 db + 16 (g % 2) + j.
-    int k_off[NKS];
-    {
-        const int r = swap_bits23(n);
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) k_off[ks] = r * kDmaRowBytes + (((2 * ks + hh) ^ dma_swz(r & 15)) << 4);
-    }
-    int v_off[2][NDB];
-    {
-        const int g = lane >> 4, j = lane & 15;
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int r = 8 * hh + 4 * u + j / 4;
-#pragma unroll
-            for (int db = 0; db < NDB; ++db) {
-                const int col = 32 * db + 16 * (g & 1) + 4 * (j & 3);
-                v_off[u][db] = kDmaTileBytes + r * kDmaRowBytes + (((col >> 3) ^ dma_swz(r & 15)) << 4) + (col & 7) * 2;
-            }
-        }
-    }
-    auto lds_k = [&](const lds_u8_t* sb, int kb, int ks) {
-        return *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(sb + kb * 32 * kDmaRowBytes +
-                                                                                     k_off[ks]);
-    };
-    auto lds_vt = [&](const lds_u8_t* sb, int kb, int t, int db) {
-        const lds_u8_t* p = sb + (kb * 32 + t * 16) * kDmaRowBytes;
-        const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(p + v_off[0][db]));
-        const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(p + v_off[1][db]));
-        return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-    };
-
-    // After this every wave has finished reading tile kt and tile kt + 1 is in
-    // LDS for all of them; tiles kt + 2 .. kt + NS - 1 (NS - 2 tiles of 2 NI
-    // loads per wave, issued later) may still be in flight.  The memory
-    // clobber keeps LDS accesses on their side of the barrier.
-    constexpr int VM = (NS - 2) * 2 * NI;
-    static_assert(VM == 0 || VM == 4 || VM == 8, "vmcnt literal");
-    auto next_tile_ready = [&]() {
-        if constexpr (VM == 0) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        else if constexpr (VM == 4) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        else asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    };
-    if constexpr (W == 8) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else next_tile_ready();   // tile 0
-
-    // One tile from stage sb, as two 32-key halves: scores, raise of the
-    // running max when it grew by more than 2^kHugeExcess, softmax, PV, lazy
-    // raise after the PV (exact, as in prefill_bf16_kernel).
-    auto tile = [&](int kt, const lds_u8_t* sb, auto diag_tag) {
-        constexpr bool DIAG = decltype(diag_tag)::value;
-        bf16x8_t kf[NKS];
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) kf[ks] = lds_k(sb, 0, ks);
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            // element j of the score block: key kt*64 + 32 kb + 16 (j/8) + 8 hh + j%8, query q_wave0 + n
-            auto masked = [&](int j) {
-                return DIAG && kt * kKTile + 32 * kb + 16 * (j / 8) + 8 * hh + (j % 8) > q_wave0 + n;
-            };
-            f32x16_t s = {};
-#pragma unroll
-            for (int ks = 0; ks < NKS; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qf[ks], s, 0, 0, 0);
-            if constexpr (DIAG) {
-#pragma unroll
-                for (int j = 0; j < 16; ++j)
-                    if (masked(j)) s[j] = -INFINITY;
-            }
-            bf16x8_t vf[NDB][2];
-#pragma unroll
-            for (int db = 0; db < NDB; ++db)
-#pragma unroll
-                for (int t = 0; t < 2; ++t) vf[db][t] = lds_vt(sb, kb, t, db);
-            float mt = s[0];
-#pragma unroll
-            for (int j = 1; j < 16; ++j) mt = fmaxf(mt, s[j]);
-            auto raise = [&]() {
-                // the other lane half holds the same query's other 16 keys
-                const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
-                const float mq = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-                const float m_new = fmaxf(ms, mq * sl2);
-                const float alpha = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - m_new);
-#pragma unroll
-                for (int db = 0; db < NDB; ++db) acc[db] *= alpha;
-                lp *= alpha;
-                ms = m_new;
-            };
-            if (__any(mt * sl2 > ms + kHugeExcess)) raise();
-            const float nm = -ms;
-            float p[16];
-            float rs = 0.f;
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j], sl2, nm));
-                if (masked(j)) p[j] = 0.f;   // exact zero also for a zero scale
-                rs += p[j];
-            }
-            lp += rs;
-            bf16x8_t pb[2];
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const bf16x2_t p01 = __builtin_convertvector(f32x2_t{p[8 * t + 0], p[8 * t + 1]}, bf16x2_t);
-                const bf16x2_t p23 = __builtin_convertvector(f32x2_t{p[8 * t + 2], p[8 * t + 3]}, bf16x2_t);
-                const bf16x2_t p45 = __builtin_convertvector(f32x2_t{p[8 * t + 4], p[8 * t + 5]}, bf16x2_t);
-                const bf16x2_t p67 = __builtin_convertvector(f32x2_t{p[8 * t + 6], p[8 * t + 7]}, bf16x2_t);
-                pb[t] = __builtin_bit_cast(
-                    bf16x8_t, make_uint4(__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23),
-                                         __builtin_bit_cast(uint32_t, p45), __builtin_bit_cast(uint32_t, p67)));
-            }
-            if (kb == 0) {
-#pragma unroll
-                for (int ks = 0; ks < NKS; ++ks) kf[ks] = lds_k(sb, 1, ks);
-            }
-#pragma unroll
-            for (int db = 0; db < NDB; ++db)
-#pragma unroll
-                for (int t = 0; t < 2; ++t)
-                    acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][t], pb[t], acc[db], 0, 0, 0);
-            if (__any(mt * sl2 > ms + kLazyRescale)) raise();
-        }
-    };
-
-    if constexpr (W == 8) {
-        // Ping-pong: waves w and w + 4 share a SIMD.  Each 32-key half is an
-        // MFMA block (the previous half's PV, then this half's scores) and a
-        // softmax block.  Waves 4-7 take the half's barrier between their two
-        // blocks, waves 0-3 after both, so on every SIMD one wave's softmax
-        // runs while the other issues MFMAs.  The previous half's P and V^T
-        // fragments stay in registers across the barrier.  The loop covers
-        // the tiles [0, kt_pp) that every wave computes off its diagonal,
-        // without per-wave branches (with them the compiler spilled); the
-        // remaining tiles and each wave's diagonal run one tile per barrier.
-        // Tile kt + 2 loads once every wave is done with tile kt.
-        static_assert(NS == 2 && NI == 2, "ping-pong schedule: two stages, two loads per tensor tile");
-        const bool late = wave >= W / 2;
-        auto raise_to = [&](float mt) {
-            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
-            const float mq = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-            const float m_new = fmaxf(ms, mq * sl2);
-            const float alpha = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - m_new);
-#pragma unroll
-            for (int db = 0; db < NDB; ++db) acc[db] *= alpha;
-            lp *= alpha;
-            ms = m_new;
-        };
-        // The pending half starts as zeros: its PV adds exact zeros, and its
-        // lazy-raise test is false (sl2 >= 0: -inf * sl2 is -inf or NaN).
-        bf16x8_t pv_v[NDB][2];
-        bf16x8_t pv_p[2];
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) pv_v[db][0] = pv_v[db][1] = bf16x8_t{};
-        pv_p[0] = pv_p[1] = bf16x8_t{};
-        float pv_mt = -INFINITY;
-        auto flush = [&]() {
-#pragma unroll
-            for (int db = 0; db < NDB; ++db)
-#pragma unroll
-                for (int t = 0; t < 2; ++t)
-                    acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pv_v[db][t], pv_p[t], acc[db], 0, 0, 0);
-            if (__any(pv_mt * sl2 > ms + kLazyRescale)) raise_to(pv_mt);
-        };
-        // End of tile kt: tile kt + 1 resident for all waves, then tile kt + 2
-        // loads into the stage tile kt used.
-        auto end_tile = [&](int kt, int stage) {
-            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-            if (kt + NS < n_kt) dma_tile(kt + NS, stage);
-        };
-        auto half = [&](int kt, int stage, int kb) {
-            const lds_u8_t* sb = lsm + stage * kDmaStageBytes;
-            bf16x8_t kf[NKS];
-#pragma unroll
-            for (int ks = 0; ks < NKS; ++ks) kf[ks] = lds_k(sb, kb, ks);
-            flush();
-#pragma unroll
-            for (int db = 0; db < NDB; ++db)
-#pragma unroll
-                for (int t = 0; t < 2; ++t) pv_v[db][t] = lds_vt(sb, kb, t, db);
-            f32x16_t s = {};
-#pragma unroll
-            for (int ks = 0; ks < NKS; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qf[ks], s, 0, 0, 0);
-            auto sync = [&]() {
-                __builtin_amdgcn_sched_barrier(0);
-                if (kb == 0) asm volatile("s_barrier" ::: "memory");
-                else end_tile(kt, stage);
-                __builtin_amdgcn_sched_barrier(0);
-            };
-            if (late) sync();
-            float mt = s[0];
-#pragma unroll
-            for (int j = 1; j < 16; ++j) mt = fmaxf(mt, s[j]);
-            if (__any(mt * sl2 > ms + kHugeExcess)) raise_to(mt);
-            const float nm = -ms;
-            float p[16];
-#pragma unroll
-            for (int j = 0; j < 16; ++j) p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j], sl2, nm));
-            float rs = p[0];
-#pragma unroll
-            for (int j = 1; j < 16; ++j) rs += p[j];
-            lp += rs;
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const bf16x2_t p01 = __builtin_convertvector(f32x2_t{p[8 * t + 0], p[8 * t + 1]}, bf16x2_t);
-                const bf16x2_t p23 = __builtin_convertvector(f32x2_t{p[8 * t + 2], p[8 * t + 3]}, bf16x2_t);
-                const bf16x2_t p45 = __builtin_convertvector(f32x2_t{p[8 * t + 4], p[8 * t + 5]}, bf16x2_t);
-                const bf16x2_t p67 = __builtin_convertvector(f32x2_t{p[8 * t + 6], p[8 * t + 7]}, bf16x2_t);
-                pv_p[t] = __builtin_bit_cast(
-                    bf16x8_t, make_uint4(__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23),
-                                         __builtin_bit_cast(uint32_t, p45), __builtin_bit_cast(uint32_t, p67)));
-            }
-            pv_mt = mt;
-            if (!late) sync();
-        };
-        // Tiles every wave computes off its diagonal, in whole rounds of NS.
-        const int kt_pp = (wk.qt * qtile + 31) / kKTile / NS * NS;
-        for (int kt = 0; kt < kt_pp; kt += NS) {
-#pragma unroll
-            for (int s = 0; s < NS; ++s) {
-                half(kt + s, s, 0);
-                half(kt + s, s, 1);
-            }
-        }
-        flush();
-        for (int kt = kt_pp; kt < n_kt; ++kt) {
-            const int stage = kt % NS;
-            if (kt + 1 < wave_kt) tile(kt, lsm + stage * kDmaStageBytes, std::false_type{});
-            end_tile(kt, stage);
-        }
-    } else {
-        auto step = [&](int kt, int stage) {
-            const bool more = kt + NS - 1 < n_kt;
-            if (more) dma_tile(kt + NS - 1, (stage + NS - 1) % NS);   // into the stage tile kt - 1 used
-            if (kt + 1 < wave_kt) tile(kt, lsm + stage * kDmaStageBytes, std::false_type{});
-            if (more) next_tile_ready();
-            else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        };
-        // Whole rounds of NS steps keep every stage index a constant; the extra
-        // steps past n_kt only synchronise.
-        const int n_steps = (n_kt + NS - 1) / NS * NS;
-        for (int kt = 0; kt < n_steps; kt += NS) {
-    #pragma unroll
-            for (int s = 0; s < NS; ++s) step(kt + s, s);
-        }
-    }
-    if (wave_kt > 0) tile(wave_kt - 1, lsm + ((wave_kt - 1) % NS) * kDmaStageBytes, std::true_type{});
-
-    const float l = lp + __shfl_xor(lp, 32, 64);
-    const int qi = q_wave0 + n;
-    if (qi < L) {
-        const float inv = 1.0f / l;
-        float* orow = pa.out + wk.b * pa.os[0] + h * pa.os[1] + qi * pa.os[2] + 4 * hh;
-#pragma unroll
-        for (int db = 0; db < NDB; ++db)
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj)
-                *reinterpret_cast<float4*>(orow + 32 * db + 8 * jj) =
-                    make_float4(acc[db][4 * jj] * inv, acc[db][4 * jj + 1] * inv, acc[db][4 * jj + 2] * inv,
-                                acc[db][4 * jj + 3] * inv);
-    }
-}
-
-// ===========================================================================
-// bf16 kernel, head_dim 128, load-unit tiles, folded softmax
-// ===========================================================================
-// The load-to-LDS kernel's data movement and schedules with less softmax
-// work per score:
+//
+// Softmax, with less work per score:
 //   * q is pre-scaled once, q' = bf16(q * scale * log2 e), and the score MFMA
 //     chain starts from -m (a register block holding the running max of each
 //     query column), so the MFMA delivers s' = q'.k - m and p = 2^s' needs no
@@ -842,30 +420,9 @@ prefill_bf16_dma_kernel(PrefillArgs pa) {
 //     of a wave always takes it (m starts at -inf, the bias at 0);
 //   * the row sums use the bf16 P of the PV product, so the normalised
 //     weights are the ones applied.
-constexpr float kSumCap = 65536.f;
-
-// acc + the sum of the 8 bf16 values of v (v_dot2c_f32_bf16 against 1.0).
-// The pairs are taken with shufflevector: bit-casting the 32-bit elements of
-// the vector to bf16 pairs made hipcc (ROCm 7.2) feed the first pair to all
-// four dot products.
-__device__ __forceinline__ float sum_bf16x8(const bf16x8_t& v, float acc) {
-    const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
-    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 0, 1), one, acc, false);
-    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 2, 3), one, acc, false);
-    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 4, 5), one, acc, false);
-    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 6, 7), one, acc, false);
-    return acc;
-}
-
-__device__ __forceinline__ bf16x8_t pack_bf16x8(const float* p) {
-    const bf16x2_t p01 = __builtin_convertvector(f32x2_t{p[0], p[1]}, bf16x2_t);
-    const bf16x2_t p23 = __builtin_convertvector(f32x2_t{p[2], p[3]}, bf16x2_t);
-    const bf16x2_t p45 = __builtin_convertvector(f32x2_t{p[4], p[5]}, bf16x2_t);
-    const bf16x2_t p67 = __builtin_convertvector(f32x2_t{p[6], p[7]}, bf16x2_t);
-    return __builtin_bit_cast(bf16x8_t, make_uint4(__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23),
-                                                   __builtin_bit_cast(uint32_t, p45), __builtin_bit_cast(uint32_t, p67)));
-}
-
+// Measured at L = 8192 (16/8 heads, same box, interleaved): 251 us against
+// 258-264 us for the same schedule with a per-tile row max, a scaled fma per
+// score and fp32 row sums (34 VALU per half-tile instead of about 75).
 template <int W, int NS>
 __global__ void __launch_bounds__(W * 64)
 prefill_bf16_fold_kernel(PrefillArgs pa) {
@@ -1064,10 +621,16 @@ prefill_bf16_fold_kernel(PrefillArgs pa) {
     };
 
     if constexpr (W == 8) {
-        // Ping-pong schedule of the load-to-LDS kernel: waves w and w + 4
-        // share a SIMD; per 32-key half an MFMA block (the previous half's PV,
-        // then this half's scores) and a softmax block, with waves 4-7 taking
-        // the half's barrier between them and waves 0-3 after both.
+        // Ping-pong schedule: waves w and w + 4 share a SIMD (read from
+        // HW_ID).  Each 32-key half is an MFMA block (the previous half's PV,
+        // then this half's scores) and a softmax block.  Waves 4-7 take the
+        // half's barrier between their two blocks, waves 0-3 after both, so
+        // on every SIMD one wave's softmax runs while the other issues MFMAs.
+        // The previous half's P and V^T fragments stay in registers across
+        // the barrier.  The loop covers the tiles every wave computes off its
+        // diagonal, without per-wave branches; the remaining tiles and each
+        // wave's diagonal run one tile per barrier.  Tile kt + 2 loads once
+        // every wave is done with tile kt.
         static_assert(NS == 2 && NI == 2, "ping-pong schedule: two stages, two loads per tensor tile");
         const bool late = wave >= W / 2;
         bf16x8_t pv_v[NDB][2];
@@ -1359,20 +922,6 @@ prefill_f32_kernel(PrefillArgs pa) {
 // ===========================================================================
 // Launch
 // ===========================================================================
-// Dynamic LDS above 64 KiB needs a per-kernel, per-device opt-in.
-template <auto KERNEL>
-sa_status opt_in_lds(int bytes) {
-    if (bytes <= 65536) return SA_OK;
-    static thread_local int opted_device = -1;
-    int dev = 0;
-    SA_HIP_TRY(hipGetDevice(&dev));
-    if (opted_device != dev) {
-        SA_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(KERNEL),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
-        opted_device = dev;
-    }
-    return SA_OK;
-}
 
 // bf16 shape: W waves of QB 32-query blocks each.  Measured at L = 8192
 // (16/8 heads) on MI355X, steady-state clocks, with the register-staged
@@ -1383,7 +932,13 @@ sa_status opt_in_lds(int bytes) {
 // barriers (the load-to-LDS kernel's ping-pong schedule is that idea without
 // the register spills); the next half's score MFMAs software-pipelined under
 // the current half's softmax (sched_group_barrier interleaving, three LDS
-// stages); the score product split into two independent MFMA chains.
+// stages); the score product split into two independent MFMA chains.  With
+// the load-to-LDS tiles and the folded softmax, 4 waves x 64 queries (one
+// wave per SIMD, O and q in AGPRs, four stages, each K and V^T fragment
+// feeding two MFMAs) measured 272-275 us at L = 8192 against 261-273 us for
+// the 8-wave ping-pong kernel on the same box: its dependency stalls fell
+// (28 % of wave cycles waiting against 43 %) but the single wave spent 45 %
+// of its cycles issuing VALU, AGPR reads of the scores included.
 constexpr int kBfQB = 1;
 constexpr int kBfW = 8;
 constexpr int kBfWSmall = 4;
@@ -1407,19 +962,9 @@ template <int W>
 sa_status launch_bf16_dma(const PrefillArgs& pa, dim3 grid, hipStream_t st) {
     constexpr int NS = dma_stages<W>();
     constexpr int bytes = NS * kDmaStageBytes;
-    static const bool fold = [] {
-        const char* e = std::getenv("SA_PREFILL_FOLD");
-        return !e || std::atoi(e) != 0;
-    }();
-    if (fold) {
-        sa_status s = opt_in_lds<&prefill_bf16_fold_kernel<W, NS>>(bytes);
-        if (s != SA_OK) return s;
-        hipLaunchKernelGGL((prefill_bf16_fold_kernel<W, NS>), grid, dim3(W * 64), bytes, st, pa);
-        return SA_OK;
-    }
-    sa_status s = opt_in_lds<&prefill_bf16_dma_kernel<W, NS>>(bytes);
+    sa_status s = opt_in_lds<&prefill_bf16_fold_kernel<W, NS>>(bytes);
     if (s != SA_OK) return s;
-    hipLaunchKernelGGL((prefill_bf16_dma_kernel<W, NS>), grid, dim3(W * 64), bytes, st, pa);
+    hipLaunchKernelGGL((prefill_bf16_fold_kernel<W, NS>), grid, dim3(W * 64), bytes, st, pa);
     return SA_OK;
 }
 
