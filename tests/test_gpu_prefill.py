@@ -68,9 +68,21 @@ def test_prefill_fp32_8192_rows(sa, oracle, synth):
     assert rel_l2(got, want) <= 1e-5
 
 
-@pytest.mark.parametrize("L", [128, 1000, 8192])
-def test_prefill_bf16(sa, oracle, synth, L):
+def roped(oracle, x):
+    """x [B, H, L, D] rotated at positions 0 .. L-1 (theta 1e6), as the
+    prompt's q and k are after the decoder layer's RoPE."""
+    B, H, L, D = x.shape
+    cos, sin = oracle.rope_tables(L, D, 1e6)
+    pos = np.tile(np.arange(L), B * H)
+    return oracle.apply_rope(x.reshape(-1, D), pos, cos, sin).reshape(x.shape)
+
+
+@pytest.mark.parametrize("L,rope", [(128, False), (1000, False), (1024, False), (1024, True), (8192, False),
+                                    (8192, True)])
+def test_prefill_bf16(sa, oracle, synth, L, rope):
     q, k, v = inputs(synth, L, seed=51)
+    if rope:
+        q, k = roped(oracle, q), roped(oracle, k)
     qb, kb, vb = synth.bf16_round(q), synth.bf16_round(k), synth.bf16_round(v)
     sc = np.float32(1 / np.sqrt(128))
     t = lambda a: dev(a).to(torch.bfloat16)  # exact: values are already bf16
@@ -171,3 +183,4 @@ def test_prefill_scale_sign(sa, oracle, synth, monkeypatch, scale, bf16, waves):
     if scale == 0.0:
         cum = np.cumsum(v.astype(np.float64), axis=2) / np.arange(1, L + 1)[:, None]
         assert np.abs(out[:, ::2] - cum).max() <= (2e-2 if bf16 else 1e-5)
+
