@@ -208,6 +208,18 @@ sa_status sa_qk_norm_rope(const float* x, int n_rows, int D, const int32_t* pos,
                           const float* rope_sin, int rope_max_pos, float* y,
                           sa_stream_t stream);
 
+/* Where eps enters the per-row RMSNorm: inside the sqrt,
+ * x / sqrt(mean(x^2) + eps) (reference tensor_cpp/src/qwen3_ops.cpp:716-717),
+ * or added to it, x / (sqrt(mean(x^2)) + eps), as the reference's AVX2 layer
+ * normalises q and k (tensor_cpp/src/qwen3_ops_avx.cpp:537, :566). */
+typedef enum { SA_NORM_EPS_INSIDE = 0, SA_NORM_EPS_OUTSIDE = 1 } sa_norm_mode;
+
+/* sa_qk_norm_rope with the placement of eps chosen by mode. */
+sa_status sa_qk_norm_rope_ex(const float* x, int n_rows, int D, const int32_t* pos,
+                             const float* norm_w, float eps, sa_norm_mode mode,
+                             const float* rope_cos, const float* rope_sin, int rope_max_pos,
+                             float* y, sa_stream_t stream);
+
 /* ------------------------------------------------------------------------
  * Paged GQA decode attention (split-KV online softmax + LSE merge).
  *
@@ -253,6 +265,36 @@ sa_status sa_prefill_causal_strided(const void* q, const void* k, const void* v,
                                     const int64_t q_strides[3], const int64_t kv_strides[3],
                                     const int64_t out_strides[3], float scale, float* out,
                                     sa_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Dense fp32 operators of the decoder layer (projections, norms, MLP,
+ * residuals), for callers whose weights are fp32.  All pointers are device
+ * pointers; rows are contiguous.
+ * ------------------------------------------------------------------------ */
+
+/* y[M][N] = x[M][K] . w[N][K]^T (+ bias[N] when bias is not NULL), fp32 MFMA
+ * with fp32 accumulation: ops::linear with nn.Linear's weight layout
+ * (reference tensor_cpp/src/ops.cpp:315-369).  y must not overlap x or w; x
+ * and w may be NULL when K = 0 (then y = bias, or 0). */
+sa_status sa_linear_f32(const float* x, int M, int K, const float* w, int N, const float* bias,
+                        float* y, sa_stream_t stream);
+
+/* y[r] = (x[r] / sqrt(sum(x[r]^2) / n + eps)) * w over rows of n floats; w may
+ * be NULL (no gain); y may alias x (ops::rms_norm, reference
+ * tensor_cpp/src/ops.cpp:375-418). */
+sa_status sa_rms_norm_f32(const float* x, int rows, int n, const float* w, float eps, float* y,
+                          sa_stream_t stream);
+
+/* out[i] = up[i] * gate[i] * sigmoid(gate[i]): the SwiGLU of qwen3_mlp and
+ * ops::swiglu(up, gate) (reference tensor_cpp/src/qwen3_ops.cpp:282-290,
+ * tensor_cpp/src/ops.cpp:493-509).  out may alias either input. */
+sa_status sa_swiglu_f32(const float* gate, const float* up, size_t n, float* out, sa_stream_t stream);
+
+/* out[i] = a x[i] + b y[i], or a x[i] when y is NULL; out may alias x or y.
+ * With a = 1 it is ops::add(x, y, b) (reference tensor_cpp/src/ops.cpp:194-207)
+ * and, with b = 1, the residual add of the decoder layer. */
+sa_status sa_axpby_f32(const float* x, float a, const float* y, float b, size_t n, float* out,
+                       sa_stream_t stream);
 
 #ifdef __cplusplus
 }

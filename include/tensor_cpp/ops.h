@@ -1,11 +1,12 @@
 /*
- * tensor_cpp/ops.h - the attention operators of the reference's ops namespace,
+ * tensor_cpp/ops.h - the operators of the reference's ops namespace that the
+ * Qwen3 layer uses (attention, linear, RMSNorm, SwiGLU, add, embedding),
  * served by the MI355X library.
  *
- * Same signatures as the reference (reference tensor_cpp/include/tensor_cpp/ops.h:133-329);
- * tensors are host [batch, heads, seq, head_dim] fp32 as there, and each call
- * runs the gfx950 kernels (split-KV decode, MFMA causal prefill) and returns
- * a host tensor.  Beyond the reference, key/value may carry fewer heads than
+ * Same signatures as the reference (reference tensor_cpp/include/tensor_cpp/ops.h:35-329);
+ * tensors are host fp32 as there (attention: [batch, heads, seq, head_dim]),
+ * and each call runs the gfx950 kernels (split-KV decode, MFMA causal
+ * prefill, fp32 MFMA linear) and returns a host tensor.  Beyond the reference, key/value may carry fewer heads than
  * the query (grouped KV heads: query head h reads KV head h / (H_q / H_kv)),
  * so repeat_kv is not needed.
  *
@@ -17,12 +18,57 @@
 #ifndef SA_AMD_TENSOR_CPP_OPS_H
 #define SA_AMD_TENSOR_CPP_OPS_H
 
+#include <stdexcept>
 #include <vector>
 
 #include "tensor_cpp/tensor.h"
 
+/* The reference's ops.h brings in OpenMP's API (ops.h:20); its benchmarks and
+ * tests call omp_set_num_threads and the like through this header. */
+#if __has_include(<omp.h>)
+#include <omp.h>
+#endif
+
+/* Integer tensor of token ids (reference tensor_cpp/include/tensor_cpp/ops.h:35-52). */
+class TensorL {
+public:
+    TensorL() = default;
+    TensorL(const std::vector<long>& data, const tensor_cpp::Shape& shape) : data_(data), shape_(shape) {
+        if (data.size() != shape.total()) throw std::invalid_argument("Data size does not match shape");
+    }
+    const tensor_cpp::Shape& shape() const { return shape_; }
+    size_t size() const { return data_.size(); }
+    const long* data() const { return data_.data(); }
+    long operator[](size_t i) const { return data_[i]; }
+
+private:
+    std::vector<long> data_;
+    tensor_cpp::Shape shape_;
+};
+
 namespace tensor_cpp {
 namespace ops {
+
+/* input + alpha * other, same shapes (reference tensor_cpp/src/ops.cpp:194-207).
+ * On the GPU. */
+Tensor add(const Tensor& input, const Tensor& other, float alpha = 1.0f);
+
+/* Rows of weight [num_embeddings, dim] picked by indices -> [indices..., dim];
+ * an index outside the table throws std::out_of_range unless it equals
+ * padding_idx (a zero row) (reference tensor_cpp/src/ops.cpp:278-309).  A copy
+ * of host rows: only the picked rows cross to the GPU in the layer path. */
+Tensor embedding(const TensorL& indices, const Tensor& weight, long padding_idx = -1);
+
+/* input [..., in] . weight[out, in]^T (+ bias [out]) -> [..., out], fp32 MFMA
+ * on the GPU (reference tensor_cpp/src/ops.cpp:315-369). */
+Tensor linear(const Tensor& input, const Tensor& weight, const Tensor* bias = nullptr);
+
+/* x / sqrt(mean(x^2) + eps) * weight over the last axis, on the GPU
+ * (reference tensor_cpp/src/ops.cpp:375-418).  Only dim = -1 (the last). */
+Tensor rms_norm(const Tensor& input, const Tensor* weight = nullptr, float eps = 1e-8f, int dim = -1);
+
+/* x * silu(gate), elementwise on the GPU (reference tensor_cpp/src/ops.cpp:493-509). */
+Tensor swiglu(const Tensor& x, const Tensor& gate);
 
 /* softmax(scale * Q K^T + mask) V (reference tensor_cpp/src/ops.cpp:514-641). */
 Tensor self_attention(const Tensor& query, const Tensor& key, const Tensor& value,

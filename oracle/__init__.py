@@ -50,7 +50,7 @@ _REF_SIGS = {
     "ref_self_attention_streaming": (None, [_P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _P]),
     "ref_blockwise": (None, [_P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _I, _P]),
     "ref_layer_attention": (_I, [_I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _F, _I, _I, _I, _P, _P]),
-    "ref_qwen3_forward": (_I, [_I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _I] + [_P] * 13),
+    "ref_qwen3_forward": (_I, [_I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _I] + [_P] * 12 + [_I, _P]),
     "ref_set_threads": (None, [_I]),
     "ref_qwen3_forward_file": (_I, [C.c_char_p, _F, _I, _I, _I, _P, _P]),
     "ref_time_decode_layer": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
@@ -310,11 +310,11 @@ class Reference:
             raise RuntimeError("reference layer raised")
         return secs
 
-    def qwen3_forward(self, weights, cfg, tokens, prompt_len):
-        """qwen3_forward_with_cache over tokens [B][P + n] (teacher forcing):
-        a P-token prompt, then n one-token forwards.  weights as in
-        oracle.qwen3_model.  Returns logits [n + 1][B][V] at the last position
-        of each forward."""
+    def qwen3_forward(self, weights, cfg, tokens, prompt_len, avx2=False):
+        """qwen3_forward_with_cache (avx2: qwen3_forward_avx_with_cache) over
+        tokens [B][P + n] (teacher forcing): a P-token prompt, then n one-token
+        forwards.  weights as in oracle.qwen3_model.  Returns logits
+        [n + 1][B][V] at the last position of each forward."""
         tokens = np.ascontiguousarray(tokens, dtype=np.int32)
         B, N = tokens.shape
         n_steps = N - prompt_len
@@ -328,7 +328,7 @@ class Reference:
             c["head_dim"], c["rms_eps"], B, prompt_len, n_steps, _p(tokens), _p(glob["embed"]),
             _p(stack["in_norm"]), _p(stack["qkv"]), _p(stack["q_norm"]), _p(stack["k_norm"]), _p(stack["o"]),
             _p(stack["post_norm"]), _p(stack["gate_up"]), _p(stack["down"]), _p(glob["final_norm"]),
-            _p(glob["lm_head"]), _p(logits))
+            _p(glob["lm_head"]), int(avx2), _p(logits))
         if rc != 0:
             raise RuntimeError("reference forward raised")
         return logits

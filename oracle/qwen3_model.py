@@ -70,10 +70,13 @@ class Qwen3Decoder:
     step() appends one token per sequence to a KvStore and returns the logits.
     """
 
-    def __init__(self, weights: dict, cfg: dict, oracle):
+    def __init__(self, weights: dict, cfg: dict, oracle, qk_eps_outside: bool = False):
         self.w = weights
         self.cfg = cfg
         self.or_ = oracle
+        # q/k RMSNorm as the AVX2 layer: x / (sqrt(mean(x^2)) + eps)
+        # (reference tensor_cpp/src/qwen3_ops_avx.cpp:537, :566)
+        self.qk_eps_outside = qk_eps_outside
         self.cos, self.sin = oracle.rope_tables(cfg["max_pos"], cfg["head_dim"], cfg["rope_theta"])
 
     def step(self, tokens, kv: KvStore):
@@ -87,8 +90,9 @@ class Qwen3Decoder:
         for l, L in enumerate(w["layers"]):
             h = rms_norm(x, L["in_norm"], eps)
             qkv = h @ L["qkv"].T
-            q = o.rms_norm_rows(qkv[:, :nq].reshape(B, Hq, D), L["q_norm"], eps)
-            k = o.rms_norm_rows(qkv[:, nq:nq + nk].reshape(B, Hkv, D), L["k_norm"], eps)
+            # the q/k RMSNorm's eps is 1e-6 whatever rms_eps is (qwen3_ops.cpp:716)
+            q = o.rms_norm_rows(qkv[:, :nq].reshape(B, Hq, D), L["q_norm"], 1e-6, self.qk_eps_outside)
+            k = o.rms_norm_rows(qkv[:, nq:nq + nk].reshape(B, Hkv, D), L["k_norm"], 1e-6, self.qk_eps_outside)
             v = qkv[:, nq + nk:].reshape(B, Hkv, D)
             q = o.apply_rope(q, np.repeat(pos, Hq), self.cos, self.sin)
             k = o.apply_rope(k, np.repeat(pos, Hkv), self.cos, self.sin)

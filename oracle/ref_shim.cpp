@@ -47,12 +47,13 @@ Tensor filled(std::vector<size_t> dims, float amp, uint64_t& state) {
     return Tensor(std::move(v), Shape(dims));
 }
 
-// Teacher-forced forwards through qwen3_forward_with_cache (STANDARD
-// attention, dense KVCache): a P-token prompt, then n_steps one-token
-// forwards; logits [n_steps + 1][B][V] at the last position of each.
+// Teacher-forced forwards through qwen3_forward_with_cache, or with avx2
+// qwen3_forward_avx_with_cache (STANDARD attention, dense KVCache): a P-token
+// prompt, then n_steps one-token forwards; logits [n_steps + 1][B][V] at the
+// last position of each.
 void run_forward(const std::vector<q3::Qwen3LayerWeights>& layers, const Tensor& embed, const Tensor& norm,
                  const Tensor& head, int nl, int Hq, int Hkv, int D, float eps, int B, int P, int n_steps,
-                 const int* tokens, int V, float* logits) {
+                 const int* tokens, int V, int avx2, float* logits) {
     q3::KVCache cache(nl, B, Hkv, D, P + n_steps + 1);
     const int N = P + n_steps;
     int t0 = 0;
@@ -62,8 +63,11 @@ void run_forward(const std::vector<q3::Qwen3LayerWeights>& layers, const Tensor&
         for (int b = 0; b < B; ++b)
             for (int s = 0; s < S; ++s) ids[(size_t)b * S + s] = tokens[(size_t)b * N + t0 + s];
         TensorL input(ids, Shape({(size_t)B, (size_t)S}));
-        Tensor out = q3::qwen3_forward_with_cache(input, &cache, embed, layers, norm, head, nl, Hq, Hkv, D, eps,
-                                                  q3::AttentionType::STANDARD);
+        Tensor out = avx2 ? tensor_cpp::qwen3::avx2::qwen3_forward_avx_with_cache(
+                                input, &cache, embed, layers, norm, head, nl, Hq, Hkv, D, eps,
+                                q3::AttentionType::STANDARD)
+                          : q3::qwen3_forward_with_cache(input, &cache, embed, layers, norm, head, nl, Hq, Hkv, D,
+                                                         eps, q3::AttentionType::STANDARD);
         for (int b = 0; b < B; ++b)
             std::memcpy(logits + ((size_t)call * B + b) * V, out.data() + ((size_t)b * S + S - 1) * V,
                         (size_t)V * sizeof(float));
@@ -301,7 +305,9 @@ int ref_time_decode_layer(int H, int I, int Hq, int Hkv, int D, int B, int L0, i
 // tensor_cpp/src/qwen3_ops.cpp:936-1014) with its dense KVCache and STANDARD
 // attention: a prompt of P tokens per sequence, then n_steps one-token
 // forwards fed the given tokens (teacher forcing).  tokens [B][P + n_steps];
-// logits [n_steps + 1][B][V]: the last position of each forward.
+// logits [n_steps + 1][B][V]: the last position of each forward.  avx2
+// selects qwen3_forward_avx_with_cache (tensor_cpp/src/qwen3_ops_avx.cpp:760-843),
+// which reads the layers' q_proj/k_proj/v_proj (filled here from qkv).
 // Weights, all row-major fp32: embed [V][H], in_norm [nl][H],
 // qkv [nl][(Hq+2Hkv)D][H], q_norm/k_norm [nl][D], o [nl][H][Hq D],
 // post_norm [nl][H], gate_up [nl][2I][H] (gate rows then up rows),
@@ -310,14 +316,18 @@ int ref_qwen3_forward(int nl, int H, int I, int V, int Hq, int Hkv, int D, float
                       int n_steps, const int* tokens, const float* embed, const float* in_norm,
                       const float* qkv, const float* q_norm, const float* k_norm, const float* o,
                       const float* post_norm, const float* gate_up, const float* down,
-                      const float* final_norm, const float* lm_head, float* logits) {
+                      const float* final_norm, const float* lm_head, int avx2, float* logits) {
     try {
         const size_t qd = (size_t)Hq * D, kd = (size_t)Hkv * D, proj = qd + 2 * kd;
         std::vector<q3::Qwen3LayerWeights> layers(nl);
         for (int l = 0; l < nl; ++l) {
             auto& w = layers[l];
             w.input_layernorm_weight = make(in_norm + (size_t)l * H, {(size_t)H});
-            w.qkv_projs = make(qkv + (size_t)l * proj * H, {proj, (size_t)H});
+            const float* wqkv = qkv + (size_t)l * proj * H;
+            w.qkv_projs = make(wqkv, {proj, (size_t)H});
+            w.q_proj = make(wqkv, {qd, (size_t)H});
+            w.k_proj = make(wqkv + qd * H, {kd, (size_t)H});
+            w.v_proj = make(wqkv + (qd + kd) * H, {kd, (size_t)H});
             w.q_norm_weight = make(q_norm + (size_t)l * D, {(size_t)D});
             w.k_norm_weight = make(k_norm + (size_t)l * D, {(size_t)D});
             w.o_proj = make(o + (size_t)l * H * qd, {(size_t)H, qd});
@@ -330,7 +340,7 @@ int ref_qwen3_forward(int nl, int H, int I, int V, int Hq, int Hkv, int D, float
         Tensor t_embed = make(embed, {(size_t)V, (size_t)H});
         Tensor t_norm = make(final_norm, {(size_t)H});
         Tensor t_head = make(lm_head, {(size_t)V, (size_t)H});
-        run_forward(layers, t_embed, t_norm, t_head, nl, Hq, Hkv, D, eps, B, P, n_steps, tokens, V, logits);
+        run_forward(layers, t_embed, t_norm, t_head, nl, Hq, Hkv, D, eps, B, P, n_steps, tokens, V, avx2, logits);
         return 0;
     } catch (const std::exception&) {
         return -1;
@@ -348,7 +358,7 @@ int ref_qwen3_forward_file(const char* path, float eps, int B, int P, int n_step
         q3::Qwen3Weights w = q3::load_qwen3_weights(path);
         run_forward(w.layers, w.embed_tokens, w.norm_weight, w.lm_head, (int)w.num_layers,
                     (int)w.num_attention_heads, (int)w.num_key_value_heads, (int)w.head_dim, eps, B, P, n_steps,
-                    tokens, (int)w.vocab_size, logits);
+                    tokens, (int)w.vocab_size, 0, logits);
         return 0;
     } catch (const std::exception&) {
         return -1;

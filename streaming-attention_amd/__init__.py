@@ -86,6 +86,11 @@ SIGNATURES = {
     "sa_qknorm_rope_append": (_I, [_P, _I, _P, _P, _P, _I, _I, _P, _I, _P, _P, _F, _P, _P, _I,
                                    _P, _P]),
     "sa_qk_norm_rope": (_I, [_P, _I, _I, _P, _P, _F, _P, _P, _I, _P, _P]),
+    "sa_qk_norm_rope_ex": (_I, [_P, _I, _I, _P, _P, _F, _I, _P, _P, _I, _P, _P]),
+    "sa_linear_f32": (_I, [_P, _I, _I, _P, _I, _P, _P, _P]),
+    "sa_rms_norm_f32": (_I, [_P, _I, _I, _P, _F, _P, _P]),
+    "sa_swiglu_f32": (_I, [_P, _P, _SZ, _P, _P]),
+    "sa_axpby_f32": (_I, [_P, _F, _P, _F, _SZ, _P, _P]),
     "sa_paged_decode_ws_bytes": (_SZ, [_P, _I, _I]),
     "sa_paged_decode": (_I, [_P, _I, _P, _I, _P, _I, _I, _F, _P, _P, _SZ, _P]),
     "sa_kvcache_gather": (_I, [_P, _I, _I, _I, _P, _P, _P]),
@@ -300,10 +305,14 @@ def rope_tables(max_pos: int, head_dim: int, theta: float = 1e6, device="cuda"):
     return cos, sin
 
 
-def qk_norm_rope(x, pos, norm_w=None, eps: float = 1e-6, rope=None, out=None, stream=None):
+SA_NORM_EPS_INSIDE, SA_NORM_EPS_OUTSIDE = 0, 1
+
+
+def qk_norm_rope(x, pos, norm_w=None, eps: float = 1e-6, rope=None, out=None, stream=None,
+                 eps_outside: bool = False):
     """Per-row RMSNorm (weights norm_w [D], or none) and rotate-half RoPE (rope =
     (cos, sin) tables, or none) of x [..., D] fp32 at positions pos (int32
-    [rows]); out may alias x."""
+    [rows]); out may alias x.  eps_outside: x / (sqrt(mean(x^2)) + eps)."""
     import torch
     D = x.shape[-1]
     rows = x.numel() // D
@@ -311,8 +320,61 @@ def qk_norm_rope(x, pos, norm_w=None, eps: float = 1e-6, rope=None, out=None, st
         raise ValueError("pos must be int32 with one entry per row")
     out = torch.empty_like(x) if out is None else out
     cos, sin = rope if rope is not None else (None, None)
-    check(lib().sa_qk_norm_rope(_ptr(_f32(x, "x")), rows, D, _ptr(pos), _ptr(norm_w), eps, _ptr(cos), _ptr(sin),
-                                cos.shape[0] if cos is not None else 0, _ptr(out), _stream(stream)))
+    mode = SA_NORM_EPS_OUTSIDE if eps_outside else SA_NORM_EPS_INSIDE
+    check(lib().sa_qk_norm_rope_ex(_ptr(_f32(x, "x")), rows, D, _ptr(pos), _ptr(norm_w), eps, mode, _ptr(cos),
+                                   _ptr(sin), cos.shape[0] if cos is not None else 0, _ptr(out),
+                                   _stream(stream)))
+    return out
+
+
+# ---------------------------------------------------------------- dense fp32 operators
+
+def linear(x, w, bias=None, out=None, stream=None):
+    """x [..., K] . w[N][K]^T (+ bias [N]) -> [..., N], fp32 (ops::linear)."""
+    import torch
+    K = x.shape[-1]
+    if w.dim() != 2 or w.shape[1] != K:
+        raise ValueError("w must be [N, K] with K = x.shape[-1]")
+    N = w.shape[0]
+    M = 1
+    for n in x.shape[:-1]:
+        M *= n
+    out = torch.empty(*x.shape[:-1], N, dtype=torch.float32, device=x.device) if out is None else out
+    check(lib().sa_linear_f32(_ptr(_f32(x, "x")), M, K, _ptr(_f32(w, "w")), N,
+                              _ptr(_f32(bias, "bias")) if bias is not None else None, _ptr(out),
+                              _stream(stream)))
+    return out
+
+
+def rms_norm(x, w=None, eps: float = 1e-6, out=None, stream=None):
+    """x / sqrt(mean(x^2) + eps) * w over the last axis (ops::rms_norm)."""
+    import torch
+    n = x.shape[-1]
+    out = torch.empty_like(x) if out is None else out
+    check(lib().sa_rms_norm_f32(_ptr(_f32(x, "x")), x.numel() // n, n,
+                                _ptr(_f32(w, "w")) if w is not None else None, eps, _ptr(out), _stream(stream)))
+    return out
+
+
+def swiglu(gate, up, out=None, stream=None):
+    """up * silu(gate), elementwise (qwen3_mlp's activation)."""
+    import torch
+    if gate.shape != up.shape:
+        raise ValueError("gate and up must have one shape")
+    out = torch.empty_like(gate) if out is None else out
+    check(lib().sa_swiglu_f32(_ptr(_f32(gate, "gate")), _ptr(_f32(up, "up")), gate.numel(), _ptr(out),
+                              _stream(stream)))
+    return out
+
+
+def axpby(x, a: float, y=None, b: float = 0.0, out=None, stream=None):
+    """a x + b y (or a x without y), elementwise."""
+    import torch
+    if y is not None and y.shape != x.shape:
+        raise ValueError("x and y must have one shape")
+    out = torch.empty_like(x) if out is None else out
+    check(lib().sa_axpby_f32(_ptr(_f32(x, "x")), a, _ptr(_f32(y, "y")) if y is not None else None, b,
+                             x.numel(), _ptr(out), _stream(stream)))
     return out
 
 

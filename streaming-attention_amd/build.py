@@ -87,18 +87,22 @@ def build_library(jobs: int = 8, verbose: bool = True) -> Path:
 
 
 def build_cpp_tests(verbose: bool = True) -> list[Path]:
-    """C++ drivers under tests/cpp that exercise the reference-shaped API."""
+    """C++ drivers under tests/cpp that exercise the reference-shaped API:
+    lib*.cpp become shared libraries (bin/lib*.so, loaded by pytest), the
+    others executables."""
     tdir = ROOT / "tests" / "cpp"
     out_dir = tdir / "bin"
     out_dir.mkdir(parents=True, exist_ok=True)
     oracle_lib = ROOT / "oracle" / "liboracle.so"
     outs = []
     for src in sorted(tdir.glob("*.cpp")):
-        exe = out_dir / src.stem
+        shared = src.stem.startswith("lib")
+        exe = out_dir / (src.stem + (".so" if shared else ""))
         cmd = [HIPCC, "-O2", "-std=c++17", f"-I{ROOT / 'include'}", f"-I{ROOT / 'oracle'}",
+               *(["-shared", "-fPIC"] if shared else []),
                str(src), "-o", str(exe), f"-L{LIB_DIR}", "-lsa_amd",
                f"-Wl,-rpath,{LIB_DIR}", f"-Wl,-rpath,$ORIGIN/../../../streaming-attention_amd/lib"]
-        if oracle_lib.exists():
+        if oracle_lib.exists() and not shared:
             cmd += [f"-L{oracle_lib.parent}", "-loracle",
                     "-Wl,-rpath,$ORIGIN/../../../oracle", "-fopenmp"]
         res = subprocess.run(cmd, capture_output=True, text=True)

@@ -134,14 +134,16 @@ struct RowPairs {
             hi[c] = (i < H) ? x[i + H] : 0.f;
         }
     }
-    // y = (x / sqrt(mean(x^2) + eps)) * w, eps inside the sqrt
-    // (reference tensor_cpp/src/qwen3_ops.cpp:716-717).
-    __device__ __forceinline__ void rms_norm(const float* w, float eps, int lane) {
+    // y = (x / sqrt(mean(x^2) + eps)) * w, eps inside the sqrt (reference
+    // tensor_cpp/src/qwen3_ops.cpp:716-717), or with eps_outside
+    // y = (x / (sqrt(mean(x^2)) + eps)) * w, as the reference's AVX2 layer
+    // (tensor_cpp/src/qwen3_ops_avx.cpp:537, :566).
+    __device__ __forceinline__ void rms_norm(const float* w, float eps, int lane, bool eps_outside = false) {
         float ss = 0.f;
 #pragma unroll
         for (int c = 0; c < NP; ++c) ss = fmaf(lo[c], lo[c], fmaf(hi[c], hi[c], ss));
         ss = group_reduce<OpSum, 1, kWave>(ss);
-        const float rms = sqrtf(ss / (float)D + eps);
+        const float rms = eps_outside ? sqrtf(ss / (float)D) + eps : sqrtf(ss / (float)D + eps);
 #pragma unroll
         for (int c = 0; c < NP; ++c) {
             const int i = lane + c * kWave;
@@ -179,13 +181,13 @@ struct RowPairs {
 template <int D>
 __global__ void __launch_bounds__(256)
 qk_norm_rope_kernel(const float* x, int n_rows, const int32_t* pos, const float* w, float eps,
-                    const float* cos_t, const float* sin_t, int max_pos, float* y) {
+                    bool eps_outside, const float* cos_t, const float* sin_t, int max_pos, float* y) {
     const int lane = threadIdx.x & (kWave - 1);
     const int row = blockIdx.x * 4 + threadIdx.x / kWave;
     if (row >= n_rows) return;
     RowPairs<D> r;
     r.load(x + (size_t)row * D, lane);
-    if (w) r.rms_norm(w, eps, lane);
+    if (w) r.rms_norm(w, eps, lane, eps_outside);
     const int p = pos ? pos[row] : 0;
     if (cos_t && p >= 0 && p < max_pos) r.rope(cos_t, sin_t, p, lane);
     r.store(y + (size_t)row * D, lane);
@@ -576,34 +578,44 @@ extern "C" sa_status sa_kvcache_gather(const sa_kvcache* c, int layer, int seq, 
     return SA_OK;
 }
 
-extern "C" sa_status sa_qk_norm_rope(const float* x, int n_rows, int D, const int32_t* pos,
-                                     const float* norm_w, float eps, const float* rope_cos,
-                                     const float* rope_sin, int rope_max_pos, float* y,
-                                     sa_stream_t stream) {
+extern "C" sa_status sa_qk_norm_rope_ex(const float* x, int n_rows, int D, const int32_t* pos,
+                                        const float* norm_w, float eps, sa_norm_mode mode,
+                                        const float* rope_cos, const float* rope_sin, int rope_max_pos,
+                                        float* y, sa_stream_t stream) {
     clear_error();
     if (!x || !y) return fail(SA_EINVAL, "null pointer");
     if (n_rows < 0) return fail(SA_EINVAL, "n_rows must be >= 0");
+    if (mode != SA_NORM_EPS_INSIDE && mode != SA_NORM_EPS_OUTSIDE) return fail(SA_EINVAL, "unknown norm mode");
     if ((rope_cos == nullptr) != (rope_sin == nullptr)) return fail(SA_EINVAL, "cos and sin go together");
     if (rope_cos && !pos) return fail(SA_EINVAL, "RoPE needs positions");
     if (n_rows == 0) return SA_OK;
     hipStream_t st = as_stream(stream);
     const dim3 grid((n_rows + 3) / 4);
+    const bool outside = mode == SA_NORM_EPS_OUTSIDE;
     switch (D) {
         case 64:
             hipLaunchKernelGGL(qk_norm_rope_kernel<64>, grid, dim3(256), 0, st, x, n_rows, pos, norm_w, eps,
-                               rope_cos, rope_sin, rope_max_pos, y);
+                               outside, rope_cos, rope_sin, rope_max_pos, y);
             break;
         case 128:
             hipLaunchKernelGGL(qk_norm_rope_kernel<128>, grid, dim3(256), 0, st, x, n_rows, pos, norm_w, eps,
-                               rope_cos, rope_sin, rope_max_pos, y);
+                               outside, rope_cos, rope_sin, rope_max_pos, y);
             break;
         case 256:
             hipLaunchKernelGGL(qk_norm_rope_kernel<256>, grid, dim3(256), 0, st, x, n_rows, pos, norm_w, eps,
-                               rope_cos, rope_sin, rope_max_pos, y);
+                               outside, rope_cos, rope_sin, rope_max_pos, y);
             break;
         default:
             return fail(SA_EINVAL, "head_dim must be 64, 128 or 256");
     }
     SA_CHECK_LAUNCH();
     return SA_OK;
+}
+
+extern "C" sa_status sa_qk_norm_rope(const float* x, int n_rows, int D, const int32_t* pos,
+                                     const float* norm_w, float eps, const float* rope_cos,
+                                     const float* rope_sin, int rope_max_pos, float* y,
+                                     sa_stream_t stream) {
+    return sa_qk_norm_rope_ex(x, n_rows, D, pos, norm_w, eps, SA_NORM_EPS_INSIDE, rope_cos, rope_sin,
+                              rope_max_pos, y, stream);
 }

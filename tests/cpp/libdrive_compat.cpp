@@ -1,0 +1,211 @@
+// Test driver: the library's reference-shaped C++ API (tensor_cpp/qwen3_ops.h,
+// tensor_cpp/qwen3_ops_avx.h, tensor_cpp/kv_cache.h, tensor_cpp/ops.h) driven
+// exactly as oracle/ref_shim.cpp drives the reference, behind the same plain
+// array arguments, so tests can put the GPU results beside the reference's
+// golden vectors.  Built as tests/cpp/bin/libdrive_compat.so.
+#include <cstring>
+#include <exception>
+#include <string>
+#include <vector>
+
+#include "tensor_cpp/kv_cache.h"
+#include "tensor_cpp/ops.h"
+#include "tensor_cpp/qwen3_ops.h"
+#include "tensor_cpp/qwen3_ops_avx.h"
+
+using tensor_cpp::Shape;
+using tensor_cpp::Tensor;
+namespace q3 = tensor_cpp::qwen3;
+
+namespace {
+
+std::string g_error;
+
+Tensor make(const float* p, std::vector<size_t> dims) {
+    size_t n = 1;
+    for (size_t d : dims) n *= d;
+    return Tensor(std::vector<float>(p, p + n), Shape(dims));
+}
+
+int failed(const std::exception& e) {
+    g_error = e.what();
+    return -1;
+}
+
+// Layer weights from the flat arrays of drv_qwen3_forward (layout below).
+std::vector<q3::Qwen3LayerWeights> layer_weights(int nl, int H, int I, int Hq, int Hkv, int D, const float* in_norm,
+                                                 const float* qkv, const float* q_norm, const float* k_norm,
+                                                 const float* o, const float* post_norm, const float* gate_up,
+                                                 const float* down) {
+    const size_t qd = (size_t)Hq * D, kd = (size_t)Hkv * D, proj = qd + 2 * kd;
+    std::vector<q3::Qwen3LayerWeights> layers(nl);
+    for (int l = 0; l < nl; ++l) {
+        auto& w = layers[l];
+        w.input_layernorm_weight = make(in_norm + (size_t)l * H, {(size_t)H});
+        const float* wqkv = qkv + (size_t)l * proj * H;
+        w.qkv_projs = make(wqkv, {proj, (size_t)H});
+        w.q_proj = make(wqkv, {qd, (size_t)H});
+        w.k_proj = make(wqkv + qd * H, {kd, (size_t)H});
+        w.v_proj = make(wqkv + (qd + kd) * H, {kd, (size_t)H});
+        w.q_norm_weight = make(q_norm + (size_t)l * D, {(size_t)D});
+        w.k_norm_weight = make(k_norm + (size_t)l * D, {(size_t)D});
+        w.o_proj = make(o + (size_t)l * H * qd, {(size_t)H, qd});
+        w.post_attention_layernorm_weight = make(post_norm + (size_t)l * H, {(size_t)H});
+        const float* gu = gate_up + (size_t)l * 2 * I * H;
+        w.gate_proj = make(gu, {(size_t)I, (size_t)H});
+        w.up_proj = make(gu + (size_t)I * H, {(size_t)I, (size_t)H});
+        w.down_proj = make(down + (size_t)l * H * I, {(size_t)H, (size_t)I});
+    }
+    return layers;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* drv_last_error() { return g_error.c_str(); }
+
+// One decoder layer with a KVCache through a prompt of prompt_len tokens and
+// then n_steps single-token steps, wired so that its attention output appears
+// verbatim in its output (the arguments and wiring of ref_layer_attention in
+// oracle/ref_shim.cpp): hidden rows [q | k | v | 0], combined projection
+// [I | 0], o_proj into the zero block, zero MLP, RMSNorm weights 1.
+// streaming selects AttentionType::STREAMING with the reference's
+// scale-on-output single-query kernel.  Returns 0, or -1 on an exception.
+int drv_layer_attention(int Hq, int Hkv, int D, int prompt_len, int n_steps, const float* q_in, const float* k_in,
+                        const float* v_in, const float* wq, const float* wk, float eps, int max_seq, int avx2,
+                        int streaming, float* attn_out, float* qkv_eff) {
+    const bool saved = tensor_cpp::ops::g_streaming_scale_on_output;
+    try {
+        tensor_cpp::ops::g_streaming_scale_on_output = streaming != 0;
+        const size_t qd = (size_t)Hq * D, kd = (size_t)Hkv * D;
+        const size_t proj = qd + 2 * kd;
+        const size_t W = proj + qd;
+        std::vector<float> qkv(proj * W, 0.0f), qp(qd * W, 0.0f), kp(kd * W, 0.0f), vp(kd * W, 0.0f);
+        for (size_t r = 0; r < proj; ++r) qkv[r * W + r] = 1.0f;
+        for (size_t r = 0; r < qd; ++r) qp[r * W + r] = 1.0f;
+        for (size_t r = 0; r < kd; ++r) kp[r * W + qd + r] = 1.0f;
+        for (size_t r = 0; r < kd; ++r) vp[r * W + qd + kd + r] = 1.0f;
+        std::vector<float> op(W * qd, 0.0f);
+        for (size_t c = 0; c < qd; ++c) op[(proj + c) * qd + c] = 1.0f;
+        Tensor t_qkv(qkv, Shape({proj, W}));
+        Tensor t_qp(qp, Shape({qd, W})), t_kp(kp, Shape({kd, W})), t_vp(vp, Shape({kd, W}));
+        Tensor t_op(op, Shape({W, qd}));
+        Tensor ones(std::vector<float>(W, 1.0f), Shape({W}));
+        Tensor t_wq = make(wq, {(size_t)D});
+        Tensor t_wk = make(wk, {(size_t)D});
+        const size_t I = 8;
+        Tensor gate(std::vector<float>(I * W, 0.0f), Shape({I, W}));
+        Tensor up(std::vector<float>(I * W, 0.0f), Shape({I, W}));
+        Tensor down(std::vector<float>(W * I, 0.0f), Shape({W, I}));
+
+        q3::KVCache cache(1, 1, Hkv, D, max_seq);
+        auto cs = q3::compute_rope_freqs(cache.max_seq_len, D, 1000000.0f);
+        const auto type = streaming ? q3::AttentionType::STREAMING : q3::AttentionType::STANDARD;
+
+        int t0 = 0;
+        for (int call = 0; call <= n_steps; ++call) {
+            const int S = call == 0 ? prompt_len : 1;
+            std::vector<float> h((size_t)S * W, 0.0f);
+            for (int s = 0; s < S; ++s) {
+                const int t = t0 + s;
+                std::memcpy(&h[s * W], q_in + (size_t)t * qd, qd * sizeof(float));
+                std::memcpy(&h[s * W + qd], k_in + (size_t)t * kd, kd * sizeof(float));
+                std::memcpy(&h[s * W + qd + kd], v_in + (size_t)t * kd, kd * sizeof(float));
+            }
+            Tensor hidden(h, Shape({1, (size_t)S, W}));
+            Tensor normed = tensor_cpp::ops::rms_norm(hidden, &ones, eps);
+            for (int s = 0; s < S; ++s)
+                std::memcpy(qkv_eff + (size_t)(t0 + s) * proj, normed.data() + (size_t)s * W, proj * sizeof(float));
+            Tensor out;
+            if (avx2)
+                out = q3::avx2::qwen3_decoder_layer_avx_with_cache(hidden, &cache, 0, Hq, Hkv, D, eps, ones, t_qp,
+                                                                   t_kp, t_vp, t_op, t_wq, t_wk, ones, gate, up, down,
+                                                                   cs.first, cs.second, type);
+            else
+                out = q3::qwen3_decoder_layer_with_cache(hidden, &cache, 0, Hq, Hkv, D, eps, ones, t_qkv, t_op, t_wq,
+                                                         t_wk, ones, gate, up, down, cs.first, cs.second, type);
+            for (int s = 0; s < S; ++s)
+                std::memcpy(attn_out + (size_t)(t0 + s) * qd, out.data() + (size_t)s * W + proj, qd * sizeof(float));
+            cache.increment_seq_len(S);
+            t0 += S;
+        }
+        tensor_cpp::ops::g_streaming_scale_on_output = saved;
+        return 0;
+    } catch (const std::exception& e) {
+        tensor_cpp::ops::g_streaming_scale_on_output = saved;
+        return failed(e);
+    }
+}
+
+// Teacher-forced forwards through qwen3_forward_with_cache (avx2:
+// qwen3_forward_avx_with_cache), STANDARD attention: a P-token prompt, then
+// n_steps one-token forwards; logits [n_steps + 1][B][V] at the last position
+// of each (the arguments of ref_qwen3_forward in oracle/ref_shim.cpp).
+// Weights, row-major fp32: embed [V][H], in_norm [nl][H],
+// qkv [nl][(Hq+2Hkv)D][H], q_norm/k_norm [nl][D], o [nl][H][Hq D],
+// post_norm [nl][H], gate_up [nl][2I][H], down [nl][H][I], final_norm [H],
+// lm_head [V][H].
+int drv_qwen3_forward(int nl, int H, int I, int V, int Hq, int Hkv, int D, float eps, int B, int P, int n_steps,
+                      const int* tokens, const float* embed, const float* in_norm, const float* qkv,
+                      const float* q_norm, const float* k_norm, const float* o, const float* post_norm,
+                      const float* gate_up, const float* down, const float* final_norm, const float* lm_head,
+                      int avx2, float* logits) {
+    try {
+        const auto layers = layer_weights(nl, H, I, Hq, Hkv, D, in_norm, qkv, q_norm, k_norm, o, post_norm, gate_up,
+                                          down);
+        Tensor t_embed = make(embed, {(size_t)V, (size_t)H});
+        Tensor t_norm = make(final_norm, {(size_t)H});
+        Tensor t_head = make(lm_head, {(size_t)V, (size_t)H});
+        q3::KVCache cache(nl, B, Hkv, D, P + n_steps + 1);
+        const int N = P + n_steps;
+        int t0 = 0;
+        for (int call = 0; call <= n_steps; ++call) {
+            const int S = call == 0 ? P : 1;
+            std::vector<long> ids((size_t)B * S);
+            for (int b = 0; b < B; ++b)
+                for (int s = 0; s < S; ++s) ids[(size_t)b * S + s] = tokens[(size_t)b * N + t0 + s];
+            TensorL input(ids, Shape({(size_t)B, (size_t)S}));
+            Tensor out = avx2 ? q3::avx2::qwen3_forward_avx_with_cache(input, &cache, t_embed, layers, t_norm, t_head,
+                                                                        nl, Hq, Hkv, D, eps,
+                                                                        q3::AttentionType::STANDARD)
+                              : q3::qwen3_forward_with_cache(input, &cache, t_embed, layers, t_norm, t_head, nl, Hq,
+                                                             Hkv, D, eps, q3::AttentionType::STANDARD);
+            for (int b = 0; b < B; ++b)
+                std::memcpy(logits + ((size_t)call * B + b) * V, out.data() + ((size_t)b * S + S - 1) * V,
+                            (size_t)V * sizeof(float));
+            t0 += S;
+        }
+        return 0;
+    } catch (const std::exception& e) {
+        return failed(e);
+    }
+}
+
+// One forward without a cache (qwen3_forward, avx2: qwen3_forward_avx) over
+// all N tokens of tokens [B][N]: logits [B][N][V] at every position.  Same
+// weight layout as drv_qwen3_forward.
+int drv_qwen3_forward_nocache(int nl, int H, int I, int V, int Hq, int Hkv, int D, float eps, int B, int N,
+                              const int* tokens, const float* embed, const float* in_norm, const float* qkv,
+                              const float* q_norm, const float* k_norm, const float* o, const float* post_norm,
+                              const float* gate_up, const float* down, const float* final_norm, const float* lm_head,
+                              int avx2, float* logits) {
+    try {
+        const auto layers = layer_weights(nl, H, I, Hq, Hkv, D, in_norm, qkv, q_norm, k_norm, o, post_norm, gate_up,
+                                          down);
+        Tensor t_embed = make(embed, {(size_t)V, (size_t)H});
+        Tensor t_norm = make(final_norm, {(size_t)H});
+        Tensor t_head = make(lm_head, {(size_t)V, (size_t)H});
+        std::vector<long> ids((size_t)B * N);
+        for (size_t i = 0; i < ids.size(); ++i) ids[i] = tokens[i];
+        TensorL input(ids, Shape({(size_t)B, (size_t)N}));
+        Tensor out = avx2 ? q3::avx2::qwen3_forward_avx(input, t_embed, layers, t_norm, t_head, nl, Hq, Hkv, D, eps)
+                          : q3::qwen3_forward(input, t_embed, layers, t_norm, t_head, nl, Hq, Hkv, D, eps);
+        std::memcpy(logits, out.data(), out.size() * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) {
+        return failed(e);
+    }
+}
+
+}  // extern "C"

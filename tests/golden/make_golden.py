@@ -5,7 +5,9 @@ oracle/_ref/libsa_ref.so (only possible where the reference is mounted).
 Inputs are rebuilt from (seed, stream) with the package's generator, so only
 the reference outputs and a SHA-256 of the inputs are stored.
 
-    make -C oracle ref && python tests/golden/make_golden.py
+    make -C oracle ref && python tests/golden/make_golden.py [name ...]
+
+With names (e.g. qwen3_forward), only those files are rewritten.
 """
 from __future__ import annotations
 
@@ -26,6 +28,7 @@ from util import load_synth  # noqa: E402
 import golden_inputs as gi  # noqa: E402
 
 synth = load_synth()
+ONLY = set(sys.argv[1:])
 
 
 def digest(*arrays) -> str:
@@ -36,6 +39,8 @@ def digest(*arrays) -> str:
 
 
 def save(name: str, meta: dict, **arrays) -> None:
+    if ONLY and name not in ONLY:
+        return
     path = HERE / f"{name}.npz"
     np.savez(path, meta=np.array(json.dumps(meta)), **arrays)
     print(f"wrote {path.name}: {sorted(arrays)} ({path.stat().st_size} B)")
@@ -116,11 +121,13 @@ def main() -> None:
             out["qkv_eff"] = eff
     save("layer", {"prompt": gi.LAYER_PROMPT, "inputs_sha256": digest(ql, kl, vl, wq, wk)}, **out)
 
-    # Whole-model forwards (qwen3_forward_with_cache, STANDARD attention).
+    # Whole-model forwards (STANDARD attention): qwen3_forward_with_cache and
+    # qwen3_forward_avx_with_cache.
     out, shas = {}, []
     for i, case in enumerate(gi.MODEL_CASES):
         w, tokens = gi.model_inputs(case)
         out[f"logits{i}"] = ref.qwen3_forward(w, case["cfg"], tokens, case["prompt"])
+        out[f"logits_avx{i}"] = ref.qwen3_forward(w, case["cfg"], tokens, case["prompt"], avx2=True)
         shas.append(digest(tokens, w["embed"], w["lm_head"], *[v for L in w["layers"] for v in L.values()]))
     save("qwen3_forward", {"inputs_sha256": shas}, **out)
 

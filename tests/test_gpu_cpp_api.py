@@ -1,6 +1,9 @@
 """GPU: the C++ mirror of the reference API (attention.h, KVCache, ops,
 qwen3 attention path), exercised by tests/cpp/test_compat.cpp against the
-oracle.  The driver prints one PASS/FAIL line per check."""
+oracle (one PASS/FAIL line per check), and the reference's own attention
+unit test (tensor_cpp/tests/unit/test_streaming_attention.cpp), compiled
+unchanged against include/ and linked to the library by oracle/Makefile
+(ref-on-lib), run on the GPU kernels."""
 from __future__ import annotations
 
 import subprocess
@@ -11,6 +14,7 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 EXE = Path(__file__).resolve().parent / "cpp" / "bin" / "test_compat"
+REF_TEST = Path(__file__).resolve().parents[1] / "oracle" / "_ref" / "test_streaming_attention_on_sa_amd"
 
 
 def test_cpp_api_mirror():
@@ -20,3 +24,15 @@ def test_cpp_api_mirror():
     failed = [line for line in r.stdout.splitlines() if line.startswith("FAIL")]
     assert r.returncode == 0 and not failed, "\n".join(failed) + r.stderr
     assert r.stdout.count("PASS") >= 40
+
+
+def test_reference_unit_test_on_the_gpu():
+    """The reference's correctness grid (T 512..4096 x d 64/128/256 at a 1e-5
+    max-abs bar against naive attention), its OpenMP-vs-serial check (1e-4)
+    and its block-size sweep, all through the library."""
+    if not REF_TEST.exists():
+        pytest.skip("built only where the reference sources are mounted (make -C oracle ref-on-lib)")
+    r = subprocess.run([str(REF_TEST)], capture_output=True, text=True, timeout=600)
+    print(r.stdout[-4000:])
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    assert r.stdout.count("Status: OK") == 4

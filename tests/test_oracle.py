@@ -342,12 +342,12 @@ def test_mistake_gqa_head_map_is_caught(oracle):
 
 # ---------------------------------------------------------------- Qwen3 decoder
 
-def _decode_teacher_forced(oracle, case, w, tokens, mutate=None):
+def _decode_teacher_forced(oracle, case, w, tokens, mutate=None, qk_eps_outside=False):
     """The oracle decoder fed the case's tokens one at a time; logits at the
     positions the reference golden stores (last prompt token, then each step)."""
     from oracle.qwen3_model import KvStore, Qwen3Decoder
     c = case["cfg"]
-    dec = Qwen3Decoder(w, c, oracle)
+    dec = Qwen3Decoder(w, c, oracle, qk_eps_outside=qk_eps_outside)
     if mutate:
         mutate(dec)
     B = tokens.shape[0]
@@ -360,15 +360,18 @@ def _decode_teacher_forced(oracle, case, w, tokens, mutate=None):
     return np.stack(out)
 
 
+@pytest.mark.parametrize("avx2", [False, True])
 @pytest.mark.parametrize("i", range(len(gi.MODEL_CASES)))
-def test_oracle_qwen3_decoder_golden(oracle, i):
+def test_oracle_qwen3_decoder_golden(oracle, i, avx2):
     """The oracle's decode step, token by token, equals the reference's
-    qwen3_forward_with_cache (prompt, then single-token steps) golden logits."""
+    qwen3_forward_with_cache (avx2: qwen3_forward_avx_with_cache, whose q/k
+    RMSNorm adds eps to the root) golden logits: prompt, then single-token
+    steps."""
     case = gi.MODEL_CASES[i]
     _, g = gi.load("qwen3_forward")
     w, tokens = gi.model_inputs(case)
-    got = _decode_teacher_forced(oracle, case, w, tokens)
-    want = g[f"logits{i}"]
+    got = _decode_teacher_forced(oracle, case, w, tokens, qk_eps_outside=avx2)
+    want = g[f"logits_avx{i}" if avx2 else f"logits{i}"]
     assert np.abs(got - want).max() <= 1e-4
     assert np.linalg.norm(got - want) / np.linalg.norm(want) <= 1e-5
     assert (got.argmax(-1) == want.argmax(-1)).all()
