@@ -14,7 +14,10 @@
 // the same kernels (the online-softmax kernels are exact attention), --threads
 // sets nothing, and the kernels' tile sizes are fixed (--q-block-size and
 // --kv-block-size are printed, not applied).  --synthetic replaces --model
-// with seeded random weights of the Qwen3-0.6B shape.
+// with seeded random weights of the Qwen3-0.6B shape; --synthetic-shape,
+// --seed and --std (not in the reference) pick another shape and draw, and
+// --logits-out writes --verify's logits, so the command line can be checked
+// against a host forward of the same weights.
 //
 // Phases, as the reference times them:
 //  prefill: iters forwards of batch x prompt-len tokens (after warmup ones),
@@ -57,6 +60,10 @@ struct Config {
     int q_block_size = 128, kv_block_size = 128;
     bool verbose = false, use_kv_cache = true, compare_kv_cache = false, verify_mode = false;
     bool kv_bf16 = false;
+    std::vector<int> shape;                 // layers, hidden, intermediate, vocab, q heads, kv heads, head_dim
+    unsigned long long seed = 42;
+    float init_std = 0.02f;
+    std::string logits_out;
     std::vector<int32_t> verify_tokens = {151644, 872, 198, 35127, 752, 264, 2805, 16800, 311,
                                           3460, 4128, 1614, 13, 151645, 198, 151644, 77091, 198};
 };
@@ -75,6 +82,9 @@ void usage(const char* prog) {
               << "  --compare-kv-cache        decode both ways and print the speedup\n"
               << "  --verify [T1,T2,...]      prefill vs token-by-token decode on these tokens\n"
               << "  --kv-bf16                 bf16 KV cache (default fp32, as the reference)\n"
+              << "  --synthetic-shape L,H,I,V,Hq,Hkv,D   shape of the synthetic model [28,1024,3072,151936,16,8,128]\n"
+              << "  --seed N, --std X         synthetic draw: seed [42], N(0, X) matrices, 1 + N(0, X) norms [0.02]\n"
+              << "  --logits-out PATH         --verify writes both paths' last logits there (fp32 [2][batch][vocab])\n"
               << "  --mode, --method, --parallel-strategy, --attention-algo, --attention,\n"
               << "  --threads, --q-block-size, --kv-block-size: accepted for compatibility\n"
               << "  --verbose, --help\n";
@@ -121,6 +131,24 @@ Config parse(int argc, char** argv) {
         else if (a == "--no-kv-cache") c.use_kv_cache = false;
         else if (a == "--compare-kv-cache") c.compare_kv_cache = true;
         else if (a == "--kv-bf16") c.kv_bf16 = true;
+        else if (a == "--synthetic-shape") {
+            std::stringstream ss(val("--synthetic-shape"));
+            std::string t;
+            while (std::getline(ss, t, ',')) c.shape.push_back(to_int(t.c_str(), "--synthetic-shape"));
+            if (c.shape.size() != 7) {
+                std::cerr << "error: --synthetic-shape takes 7 integers L,H,I,V,Hq,Hkv,D\n";
+                std::exit(1);
+            }
+        } else if (a == "--seed") c.seed = (unsigned long long)to_int(val("--seed"), "--seed");
+        else if (a == "--std") {
+            const char* v = val("--std");
+            char* end = nullptr;
+            c.init_std = std::strtof(v, &end);
+            if (!end || *end || !(c.init_std > 0.0f)) {
+                std::cerr << "error: bad value for --std: " << v << "\n";
+                std::exit(1);
+            }
+        } else if (a == "--logits-out") c.logits_out = val("--logits-out");
         else if (a == "--verify") {
             c.verify_mode = true;
             if (i + 1 < argc && argv[i + 1][0] != '-') {
@@ -180,7 +208,10 @@ struct Runner {
     int max_tokens = 0;
 
     Runner(const Config& c, int max_tokens_) : cfg(c), max_tokens(max_tokens_) {
-        if (c.synthetic) {
+        if (c.synthetic && !c.shape.empty()) {
+            const auto& s = c.shape;
+            desc = sa_qwen3_desc{s[0], s[1], s[2], s[3], s[4], s[5], s[6], 0, 1e-6f, 1e6f};
+        } else if (c.synthetic) {
             desc = sa_qwen3_desc{28, 1024, 3072, 151936, 16, 8, 128, 0, 1e-6f, 1e6f};
         } else {
             if (c.model_path.empty()) throw std::runtime_error("--model PATH or --synthetic is required");
@@ -189,7 +220,7 @@ struct Runner {
         desc.max_pos = max_tokens + 1;
         check(sa_qwen3_create(&desc, c.batch_size, &model), "sa_qwen3_create");
         if (c.synthetic) {
-            check(sa_qwen3_init_random(model, 42, 0.02f, nullptr), "sa_qwen3_init_random");
+            check(sa_qwen3_init_random(model, c.seed, c.init_std, nullptr), "sa_qwen3_init_random");
         } else {
             check(sa_qwen3_load_safetensors(model, c.model_path.c_str()), "loading the checkpoint");
         }
@@ -292,7 +323,10 @@ void print_header(const Config& c, const Runner& r) {
     std::cout << "\n==================================================\n"
               << "         Qwen3 Performance Benchmark (MI355X)\n"
               << "==================================================\n"
-              << "model:           " << (c.synthetic ? "synthetic (seed 42, N(0, 0.02))" : c.model_path) << "\n"
+              << "model:           "
+              << (c.synthetic ? "synthetic (seed " + std::to_string(c.seed) + ", N(0, " + std::to_string(c.init_std) + "))"
+                              : c.model_path)
+              << "\n"
               << "phase:           " << c.phase << "\n"
               << "method:          " << c.method << " / " << c.attention_algo << " (one GPU path for all)\n";
     if (c.phase == "prefill")
@@ -352,6 +386,13 @@ int verify(Runner& r) {
               << "  prefill of 1 + " << n - 1 << " decode steps   -> next token " << next_b << "\n"
               << "  last-position logits: max abs diff " << max_diff << ", max rel diff " << max_rel * 100.f
               << "%\n";
+    if (!r.cfg.logits_out.empty()) {
+        FILE* f = std::fopen(r.cfg.logits_out.c_str(), "wb");
+        if (!f) throw std::runtime_error("cannot write " + r.cfg.logits_out);
+        const bool wrote = std::fwrite(a.data(), sizeof(float), a.size(), f) == a.size() &&
+                           std::fwrite(b.data(), sizeof(float), b.size(), f) == b.size();
+        if (std::fclose(f) != 0 || !wrote) throw std::runtime_error("cannot write " + r.cfg.logits_out);
+    }
     const bool ok = next_a == next_b && max_diff <= 1e-3f;
     std::cout << "  result: " << (ok ? "MATCH" : "MISMATCH") << "\n";
     return ok ? 0 : 2;

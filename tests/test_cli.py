@@ -71,3 +71,50 @@ def test_verify_matches():
     assert "MATCH" in r.stdout
     toks = re.findall(r"next token (\d+)", r.stdout)
     assert len(toks) == 2 and toks[0] == toks[1]
+
+
+VERIFY_CFG = dict(num_layers=2, hidden=128, intermediate=192, vocab=320, n_q_heads=4, n_kv_heads=2, head_dim=64,
+                  rms_eps=1e-6, rope_theta=1e6, max_pos=64)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("batch", [1, 3])
+def test_verify_against_host_forward(tmp_path, oracle, synth, batch):
+    """--verify on a small synthetic model (seed 9, std 0.1): the next token and
+    the last-position logits of both GPU paths (one prefill; a one-token
+    prefill then decode steps) against the oracle decoder on the same weights
+    (oracle.qwen3_model.synth_weights draws what sa_qwen3_init_random draws)
+    and, where it is built, the reference's qwen3_forward_with_cache.  fp32
+    bar: max-abs <= 1e-4, relative L2 <= 1e-5, same argmax."""
+    import numpy as np
+    from oracle import Reference
+    from oracle.qwen3_model import KvStore, Qwen3Decoder, synth_weights
+
+    c = VERIFY_CFG
+    tokens = [3, 17, 99, 250, 7, 120, 64]
+    out = tmp_path / "logits.bin"
+    shape = ",".join(str(c[k]) for k in ("num_layers", "hidden", "intermediate", "vocab", "n_q_heads",
+                                         "n_kv_heads", "head_dim"))
+    r = run("--synthetic", "--synthetic-shape", shape, "--seed", "9", "--std", "0.1", "--batch-size", str(batch),
+            "--verify", ",".join(map(str, tokens)), "--logits-out", str(out))
+    assert r.returncode == 0, r.stdout + r.stderr
+    got = np.fromfile(out, np.float32).reshape(2, batch, c["vocab"])
+    next_tok = [int(t) for t in re.findall(r"next token (\d+)", r.stdout)]
+
+    w = synth_weights(synth, c, 9, 0.1)
+    dec = Qwen3Decoder(w, c, oracle)
+    kv = KvStore(c["num_layers"], batch, c["n_kv_heads"], c["head_dim"], len(tokens))
+    for t in tokens:
+        want = dec.step([t] * batch, kv)
+    wants = [("oracle", want)]
+    if Reference.available():
+        seq = np.array([tokens] * batch, np.int32)
+        wants.append(("reference", Reference().qwen3_forward(w, c, seq, len(tokens))[0]))
+    for name, wt in wants:
+        for path in range(2):
+            g = got[path]
+            err = float(np.abs(g - wt).max())
+            rel = float(np.linalg.norm(g - wt) / np.linalg.norm(wt))
+            assert err <= 1e-4 and rel <= 1e-5, (name, path, err, rel)
+            assert (g.argmax(-1) == wt.argmax(-1)).all(), (name, path)
+        assert next_tok == [int(wt[0].argmax())] * 2, (name, next_tok)
