@@ -303,79 +303,91 @@ def cpu_model_decode(sum_len: int, B: int = 64, layers: int = 28, steps: int = 3
 # ---------------------------------------------------------------- extra configs
 
 def bench_layer_decode_loop(torch, sa, synth, steps_timed: int = 3):
-    """One layer, B=1, 16 q / 8 KV heads, D=128: 128-token prompt, 100 steps of
-    fused norm + RoPE + append, paged decode, commit.  Eager: every step's
-    launches issued from the host.  Graph: the 100 steps captured once into a
-    HIP graph (each step's launch parameters are the ones the eager loop
-    uses) and replayed from the 128-token cache; every replay's per-step
-    outputs must equal the eager ones bit for bit."""
-    HQ, HKV, D, P, N = 16, 8, 128, 128, 100
+    """One layer, B=1, 16 q / 8 KV heads, D=128: 128-token prompt, 100 decode
+    steps, each q/k norm + RoPE + append, paged decode and commit: one
+    sa_append_decode call (a single kernel launch while the sequence fits one
+    chunk), and, under "three_calls", as sa_qknorm_rope_append +
+    sa_paged_decode + sa_kvcache_commit.  Eager: every step's launches issued
+    from the host.  Graph: the 100 steps captured once into a HIP graph (each
+    step's launch parameters are the ones the eager loop uses) and replayed
+    from the 128-token cache; every replay's per-step outputs must equal the
+    eager ones bit for bit."""
     res = {}
     for name, dt in (("fp32", sa.SA_DTYPE_F32), ("bf16", sa.SA_DTYPE_BF16)):
-        cache = sa.KVCache(1, HKV, D, 1, 4, 4, dt)
-        cos, sin = sa.rope_tables(P + N, D, 1e6)
-        wq = torch.from_numpy(1 + synth.normal(40, 1, D, 0.02)).cuda()
-        wk = torch.from_numpy(1 + synth.normal(40, 2, D, 0.02)).cuda()
-        q = torch.from_numpy(synth.normal(40, 5, (N, 1, 1, HQ, D))).cuda()
-        k = torch.from_numpy(synth.normal(40, 6, (N, 1, 1, HKV, D))).cuda()
-        v = torch.from_numpy(synth.normal(40, 7, (N, 1, 1, HKV, D))).cuda()
-        kp = torch.from_numpy(synth.normal(40, 3, (1, P, HKV, D))).cuda()
-        vp = torch.from_numpy(synth.normal(40, 4, (1, P, HKV, D))).cuda()
-        ws = torch.zeros(max(cache.decode_ws_bytes(1, HQ), 1), dtype=torch.uint8, device="cuda")
-        outs_e = torch.empty(N, 1, HQ, D, device="cuda")
-        outs_g = torch.empty(N, 1, HQ, D, device="cuda")
-        qo = torch.empty(1, 1, HQ, D, device="cuda")
-        sc = float(1 / np.sqrt(D))
+        res[name] = _layer_decode_loop(torch, sa, synth, dt, True, steps_timed)
+        res[name]["three_calls"] = _layer_decode_loop(torch, sa, synth, dt, False, steps_timed)
+    return res
 
-        def prompt():
-            cache.reset()
-            cache.reserve(0, P + N)
-            cache.append(0, None, kp, vp, None, wk, 1e-6, rope=(cos, sin))
-            cache.commit(P, n_seqs=1)
 
-        def steps(outs):
-            for t in range(N):
+def _layer_decode_loop(torch, sa, synth, dt, fused: bool, steps_timed: int):
+    HQ, HKV, D, P, N = 16, 8, 128, 128, 100
+    cache = sa.KVCache(1, HKV, D, 1, 4, 4, dt)
+    cos, sin = sa.rope_tables(P + N, D, 1e6)
+    wq = torch.from_numpy(1 + synth.normal(40, 1, D, 0.02)).cuda()
+    wk = torch.from_numpy(1 + synth.normal(40, 2, D, 0.02)).cuda()
+    q = torch.from_numpy(synth.normal(40, 5, (N, 1, 1, HQ, D))).cuda()
+    k = torch.from_numpy(synth.normal(40, 6, (N, 1, 1, HKV, D))).cuda()
+    v = torch.from_numpy(synth.normal(40, 7, (N, 1, 1, HKV, D))).cuda()
+    kp = torch.from_numpy(synth.normal(40, 3, (1, P, HKV, D))).cuda()
+    vp = torch.from_numpy(synth.normal(40, 4, (1, P, HKV, D))).cuda()
+    ws = torch.zeros(max(cache.decode_ws_bytes(1, HQ), 1), dtype=torch.uint8, device="cuda")
+    outs_e = torch.empty(N, 1, HQ, D, device="cuda")
+    outs_g = torch.empty(N, 1, HQ, D, device="cuda")
+    qo = torch.empty(1, 1, HQ, D, device="cuda")
+    sc = float(1 / np.sqrt(D))
+
+    def prompt():
+        cache.reset()
+        cache.reserve(0, P + N)
+        cache.append(0, None, kp, vp, None, wk, 1e-6, rope=(cos, sin))
+        cache.commit(P, n_seqs=1)
+
+    def steps(outs):
+        for t in range(N):
+            if fused:
+                cache.append_decode(0, q[t].view(1, HQ, D), k[t].view(1, HKV, D), v[t].view(1, HKV, D), sc,
+                                    wq, wk, 1e-6, rope=(cos, sin), out=outs[t], ws=ws, commit=True)
+            else:
                 cache.append(0, q[t], k[t], v[t], wq, wk, 1e-6, rope=(cos, sin), q_out=qo)
                 cache.decode(0, qo.view(1, HQ, D), sc, n_pending=1, out=outs[t], ws=ws)
                 cache.commit(1, n_seqs=1)
 
-        walls = []
-        for rep in range(steps_timed + 1):
-            prompt()
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            steps(outs_e)
-            torch.cuda.synchronize()
-            if rep:
-                walls.append(time.perf_counter() - t0)
-        wall = statistics.median(walls)
-
+    walls = []
+    for rep in range(steps_timed + 1):
         prompt()
         torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            steps(outs_g)
-        g_walls, exact = [], True
-        for rep in range(steps_timed + 1):
-            outs_g.zero_()
-            cache.set_len(0, P)          # the captured steps start from the prompt
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            graph.replay()
-            torch.cuda.synchronize()
-            if rep:
-                g_walls.append(time.perf_counter() - t0)
-            exact = exact and bool(torch.equal(outs_g, outs_e))
-        del graph
-        cache.close()
-        g_wall = statistics.median(g_walls)
-        kv_bytes = sum(HKV * (P + t + 1) * D * 2 * (4 if name == "fp32" else 2) for t in range(N))
-        res[name] = {"steps_per_s": round(N / wall, 1), "us_per_step": round(wall / N * 1e6, 2),
-                     "graph_steps_per_s": round(N / g_wall, 1), "graph_us_per_step": round(g_wall / N * 1e6, 2),
-                     "graph_equals_eager": exact,
-                     "kv_read_bytes_100_steps": kv_bytes,
-                     "hbm_frac": round(kv_bytes / g_wall / 1e9 / HBM_PEAK_GBS, 5)}
-    return res
+        t0 = time.perf_counter()
+        steps(outs_e)
+        torch.cuda.synchronize()
+        if rep:
+            walls.append(time.perf_counter() - t0)
+    wall = statistics.median(walls)
+
+    prompt()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        steps(outs_g)
+    g_walls, exact = [], True
+    for rep in range(steps_timed + 1):
+        outs_g.zero_()
+        cache.set_len(0, P)          # the captured steps start from the prompt
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        graph.replay()
+        torch.cuda.synchronize()
+        if rep:
+            g_walls.append(time.perf_counter() - t0)
+        exact = exact and bool(torch.equal(outs_g, outs_e))
+    del graph
+    cache.close()
+    g_wall = statistics.median(g_walls)
+    kv_bytes = sum(HKV * (P + t + 1) * D * 2 * (4 if dt == sa.SA_DTYPE_F32 else 2) for t in range(N))
+    return {"steps_per_s": round(N / wall, 1), "us_per_step": round(wall / N * 1e6, 2),
+            "graph_steps_per_s": round(N / g_wall, 1), "graph_us_per_step": round(g_wall / N * 1e6, 2),
+            "graph_equals_eager": exact,
+            "kv_read_bytes_100_steps": kv_bytes,
+            "hbm_frac": round(kv_bytes / g_wall / 1e9 / HBM_PEAK_GBS, 5)}
 
 
 def batch_lengths(synth, B: int = 64, lo: int = 512, hi: int = 32768, seed: int = 70):

@@ -239,6 +239,30 @@ sa_status sa_paged_decode(const sa_kvcache* cache, int layer, const float* q,
                           float scale, float* out, void* ws, size_t ws_bytes,
                           sa_stream_t stream);
 
+/* ------------------------------------------------------------------------
+ * One decode step of a layer in one call: sa_qknorm_rope_append with S = 1,
+ * sa_paged_decode with n_pending = 1 and, when commit != 0,
+ * sa_kvcache_commit(cache, seq_ids, n_seq, 1).
+ *
+ * Replaces the per-token body of the reference decoder layer's attention
+ * block: QK-norm, RoPE at current_seq_len, KVCache::update, attention over
+ * the cache plus the new token (reference tensor_cpp/src/qwen3_ops.cpp:697-909),
+ * and, for the last layer, increment_seq_len(1) (qwen3_ops.cpp:986-991).
+ * q [n_seq][n_q_heads][D] (before norm and RoPE), k and v [n_seq][n_kv_heads][D];
+ * out [n_seq][n_q_heads][D]; q_out, when not NULL, receives the normed and
+ * rotated q.  Other arguments as in sa_qknorm_rope_append and
+ * sa_paged_decode (ws: sa_paged_decode_ws_bytes bytes).  Sequences whose
+ * cache plus the new token fit one chunk take a single kernel launch per 64
+ * sequences; longer ones add the LSE merge launch.  Rows are checked as for
+ * an append of one token; a refused call enqueues nothing.
+ * ------------------------------------------------------------------------ */
+sa_status sa_append_decode(sa_kvcache* cache, int layer, const float* q, const float* k,
+                           const float* v, int n_seq, const int32_t* seq_ids, int n_q_heads,
+                           const float* q_norm_w, const float* k_norm_w, float eps,
+                           const float* rope_cos, const float* rope_sin, int rope_max_pos,
+                           float scale, float* out, float* q_out, void* ws, size_t ws_bytes,
+                           int commit, sa_stream_t stream);
+
 /* Dense copy of a sequence's first len tokens: k_out, v_out [n_kv_heads][len][D]
  * fp32 (serves KVCache::get_cached_keys / get_cached_values, kv_cache.h:161-237). */
 sa_status sa_kvcache_gather(const sa_kvcache* cache, int layer, int seq, int len,

@@ -94,6 +94,8 @@ SIGNATURES = {
     "sa_paged_decode_ws_bytes": (_SZ, [_P, _I, _I]),
     "sa_paged_decode": (_I, [_P, _I, _P, _I, _P, _I, _I, _F, _P, _P, _SZ, _P]),
     "sa_kvcache_gather": (_I, [_P, _I, _I, _I, _P, _P, _P]),
+    "sa_append_decode": (_I, [_P, _I, _P, _P, _P, _I, _P, _I, _P, _P, _F, _P, _P, _I, _F, _P, _P, _P, _SZ,
+                              _I, _P]),
     "sa_prefill_causal": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _P]),
     "sa_prefill_causal_strided": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _F, _P, _P]),
     "sa_qwen3_create": (_I, [C.POINTER(Qwen3Desc), _I, C.POINTER(_P)]),
@@ -285,6 +287,27 @@ class KVCache:
             ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=q.device)
         check(lib().sa_paged_decode(self.handle, layer, _ptr(_f32(q, "q")), n_seq, _rows(seq_ids, n_seq), Hq,
                                     n_pending, scale, _ptr(out), _ptr(ws), ws.numel(), _stream(stream)))
+        return out
+
+    def append_decode(self, layer: int, q, k, v, scale: float, q_norm_w=None, k_norm_w=None, eps: float = 1e-6,
+                      rope=None, out=None, q_out=None, ws=None, commit: bool = False, seq_ids=None, stream=None):
+        """One decode step in one call: q [n_seq, Hq, D] and k/v [n_seq, Hkv, D]
+        of the new token (before norm and RoPE) -> out [n_seq, Hq, D], the
+        attention over the cache plus the token; commit=True also commits it.
+        q_out, if given, receives the normed, rotated q."""
+        import torch
+        n_seq, Hq, _ = q.shape
+        out = torch.empty_like(q) if out is None else out
+        if ws is None:
+            need = self.decode_ws_bytes(n_seq, Hq)
+            ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=q.device)
+        cos, sin = (None, None) if rope is None else rope
+        max_pos = 0 if rope is None else cos.shape[0]
+        check(lib().sa_append_decode(
+            self.handle, layer, _ptr(_f32(q, "q")), _ptr(_f32(k, "k")), _ptr(_f32(v, "v")), n_seq,
+            _rows(seq_ids, n_seq), Hq, _ptr(_f32(q_norm_w, "q_norm_w")), _ptr(_f32(k_norm_w, "k_norm_w")), eps,
+            _ptr(cos), _ptr(sin), max_pos, scale, _ptr(out), _ptr(q_out), _ptr(ws), ws.numel(), int(bool(commit)),
+            _stream(stream)))
         return out
 
     def gather(self, layer: int, seq: int, length: int, stream=None):

@@ -77,6 +77,21 @@ struct DecodeArgs {
     int chunk;               // tokens per workgroup, multiple of 64
     int n_split;             // chunks per (sequence, kv head) in the grid
     float scale;
+    // Fused append step (FUSED kernels only): q above is the raw q; the new
+    // token's K/V, norm weights, RoPE tables, optional q output, and its
+    // position in each sequence (the committed length, from the host).
+    const float* k_new;      // [n_seq][n_kv][D]
+    const float* v_new;
+    const float* wq;
+    const float* wk;
+    const float* cos_t;
+    const float* sin_t;
+    float* q_out;            // [n_seq][n_q_heads][D] or NULL
+    int32_t* lens_out;       // the cache's device lengths, written on commit
+    RowList pos;
+    float eps;
+    int rope_max_pos;
+    int commit;
 };
 
 // Widen one 16-byte slice of a K/V row to fp32.
@@ -214,9 +229,17 @@ __device__ __forceinline__ void consume(const TileRegs<Geo<D, BF16>::R>& regs, i
     }
 }
 
-template <int D, int NREP, bool BF16, bool PAGED, int W>
+// FUSED (paged only): the decode step's append runs in the same launch.  Each
+// workgroup normalises and rotates the q heads of its group into LDS; the
+// workgroup whose chunk holds the new token's position also normalises and
+// rotates its K, writes K and V into the cache there (and q to q_out), and,
+// on commit, sets the sequence's device length to pos + 1.  Lengths come
+// from the launch arguments, so no workgroup reads the device length another
+// one writes.
+template <int D, int NREP, bool BF16, bool PAGED, int W, bool FUSED = false>
 __global__ void __launch_bounds__(W * kWave)
 split_kv_decode_kernel(DecodeArgs a) {
+    static_assert(!FUSED || PAGED, "the fused step appends to a paged cache");
     using G = Geo<D, BF16>;
     constexpr int E = G::E, LPR = G::LPR, TILE = G::TILE;
     constexpr int THREADS = W * kWave;
@@ -232,11 +255,17 @@ split_kv_decode_kernel(DecodeArgs a) {
 
     int len;
     int cache_row = seq;
+    int pos = 0;                   // FUSED: position of the new token
     if constexpr (PAGED) {
         cache_row = a.rows.row[seq];
         // Never walk past the block-table row or the chunks of the grid,
         // whatever the device lengths say (the host has checked them).
-        len = min(min(a.seq_lens[cache_row] + a.n_pending, a.max_pages * 64), a.n_split * a.chunk);
+        if constexpr (FUSED) {
+            pos = a.pos.row[seq];
+            len = min(min(pos + 1, a.max_pages * 64), a.n_split * a.chunk);
+        } else {
+            len = min(min(a.seq_lens[cache_row] + a.n_pending, a.max_pages * 64), a.n_split * a.chunk);
+        }
         if (len <= 0) {
             // An empty sequence attends to nothing: its output is zero.
             if (split == 0) {
@@ -253,11 +282,150 @@ split_kv_decode_kernel(DecodeArgs a) {
     const int t_end = min(len, t_begin + a.chunk);
     const int n_active = (len - 1) / a.chunk + 1;   // chunks holding tokens
 
+    TileWalker<D, NREP, BF16, PAGED> walk{a, nullptr, nullptr, nullptr, 0, g, t_end, grp, col};
+    __shared__ int sh_pages[kMaxChunkPages];
+    auto setup_walk = [&]() {
+        if constexpr (PAGED) {
+            // The chunk's page ids, once per workgroup; an id outside the pool (a
+            // table the caller left unassigned) is clamped so no load can fault.
+            const int p0 = t_begin >> 6, np = ((t_end - 1) >> 6) - p0 + 1;
+            const int32_t* row = a.block_table + (size_t)cache_row * a.max_pages + p0;
+            for (int i = threadIdx.x; i < np; i += THREADS) sh_pages[i] = min(max(row[i], 0), a.num_pages - 1);
+            __syncthreads();
+            walk.pages = sh_pages;
+            walk.page0 = p0;
+        } else {
+            const size_t off = ((size_t)seq * a.n_kv + g) * (size_t)a.T * TileWalker<D, NREP, BF16, PAGED>::ROW_BYTES;
+            walk.kbase = static_cast<const char*>(a.k) + off;
+            walk.vbase = static_cast<const char*>(a.v) + off;
+        }
+    };
+    constexpr int STRIDE = W * TILE;
+    const int first = t_begin + wave * TILE;
+    const int n_tiles = first < t_end ? (t_end - first + STRIDE - 1) / STRIDE : 0;   // wave-uniform
+    TileRegs<G::R> ra, rb;
+    bool first_loaded = false;
+
+    // FUSED prologue.  Every global load of the step's own data (q, k, v,
+    // norm weights, cos/sin) is issued first, so their latency overlaps the
+    // page-id load; the first K/V tile is then in flight while q and k are
+    // normalised and rotated.  The new K/V row goes to the cache and, encoded
+    // as stored, to LDS: the tile that holds it takes the row from LDS, so
+    // nothing waits for the stores.  (Measured: each wave computing every q
+    // head itself, with the K/V row computed by the wave whose tile holds it
+    // and no barrier, was slower: 7.6 against 7.3 us per fp32 step.)
+    constexpr int KV_SLICES = D * G::kElemBytes / 16;                 // 16-byte slices of a row
+    __shared__ __align__(16) float sh_q[FUSED ? NREP : 1][FUSED ? D : 4];
+    __shared__ u32x4 sh_knew[FUSED ? KV_SLICES : 1];
+    __shared__ u32x4 sh_vnew[FUSED ? KV_SLICES : 1];
+    const bool owner = FUSED && t_begin <= pos && pos < t_end;   // this chunk holds the new token
+    if constexpr (FUSED) {
+        using RP = RowPairs<D>;
+        constexpr int NP = RP::NP;
+        constexpr int QPW = (NREP + W - 1) / W;                   // q heads per wave
+        const bool writer = owner && wave == W - 1;
+        const bool rope_on = a.cos_t && pos < a.rope_max_pos;
+        RP qr[QPW], kr;
+        float vl[NP], vh[NP], wql[NP], wqh[NP], wkl[NP], wkh[NP], cs[NP], sn[NP];
+#pragma unroll
+        for (int j = 0; j < QPW; ++j) {
+            const int h = wave + j * W;
+            if (h < NREP) qr[j].load(a.q + ((size_t)seq * a.n_q + g * NREP + h) * D, lane);
+        }
+        const size_t kv_src = ((size_t)seq * a.n_kv + g) * D;
+        if (writer) {
+            kr.load(a.k_new + kv_src, lane);
+            RP::load_pairs(a.v_new + kv_src, lane, vl, vh);
+            if (a.wk) RP::load_pairs(a.wk, lane, wkl, wkh);
+        }
+        if (a.wq) RP::load_pairs(a.wq, lane, wql, wqh);
+        if (rope_on) {
+            RP::load_row(a.cos_t + (size_t)pos * (D / 2), lane, cs);
+            RP::load_row(a.sin_t + (size_t)pos * (D / 2), lane, sn);
+        }
+        int page = -1;
+        if (writer) page = a.block_table[(size_t)cache_row * a.max_pages + (pos >> 6)];
+        setup_walk();                         // its barrier also waits for the loads above
+        if constexpr (kPrefetch) {
+            if (n_tiles > 0) {
+                walk.load(first, ra);
+                first_loaded = true;
+            }
+        }
+        // q of every head of the group: RMSNorm + RoPE at pos, into LDS.
+#pragma unroll
+        for (int j = 0; j < QPW; ++j) {
+            const int h = wave + j * W;
+            if (h < NREP) {
+                if (a.wq) qr[j].rms_norm_with(wql, wqh, a.eps);
+                if (rope_on) qr[j].rope_with(cs, sn);
+                qr[j].store(&sh_q[h][0], lane);
+                if (a.q_out && owner) qr[j].store(a.q_out + ((size_t)seq * a.n_q + g * NREP + h) * D, lane);
+            }
+        }
+        if (writer) {
+            // K (normed, rotated) and V (as given) of the new token at pos; the
+            // host has checked that the row has a page there.
+            if (a.wk) kr.rms_norm_with(wkl, wkh, a.eps);
+            if (rope_on) kr.rope_with(cs, sn);
+            constexpr int H = D / 2;
+            const bool paged_ok = page >= 0 && page < a.num_pages;
+            const size_t row = (((size_t)(paged_ok ? page : 0) * a.n_kv + g) * 64 + (pos & 63)) * D;
+#pragma unroll
+            for (int c = 0; c < NP; ++c) {
+                const int i = lane + c * kWave;
+                if (i < H) {
+                    if constexpr (BF16) {
+                        const uint16_t k0 = f32_to_bf16_rne(kr.lo[c]), k1 = f32_to_bf16_rne(kr.hi[c]);
+                        const uint16_t v0 = f32_to_bf16_rne(vl[c]), v1 = f32_to_bf16_rne(vh[c]);
+                        uint16_t* lk = reinterpret_cast<uint16_t*>(sh_knew);
+                        uint16_t* lv = reinterpret_cast<uint16_t*>(sh_vnew);
+                        lk[i] = k0; lk[i + H] = k1; lv[i] = v0; lv[i + H] = v1;
+                        if (paged_ok) {
+                            uint16_t* kd = const_cast<uint16_t*>(static_cast<const uint16_t*>(a.k)) + row;
+                            uint16_t* vd = const_cast<uint16_t*>(static_cast<const uint16_t*>(a.v)) + row;
+                            kd[i] = k0; kd[i + H] = k1; vd[i] = v0; vd[i + H] = v1;
+                        }
+                    } else {
+                        float* lk = reinterpret_cast<float*>(sh_knew);
+                        float* lv = reinterpret_cast<float*>(sh_vnew);
+                        lk[i] = kr.lo[c]; lk[i + H] = kr.hi[c]; lv[i] = vl[c]; lv[i + H] = vh[c];
+                        if (paged_ok) {
+                            float* kd = const_cast<float*>(static_cast<const float*>(a.k)) + row;
+                            float* vd = const_cast<float*>(static_cast<const float*>(a.v)) + row;
+                            kd[i] = kr.lo[c]; kd[i + H] = kr.hi[c]; vd[i] = vl[c]; vd[i + H] = vh[c];
+                        }
+                    }
+                }
+            }
+        }
+        // LDS only: the tile loads and the cache stores stay in flight.
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+    // The tile at t0 that holds the new token takes its row from LDS (rows past
+    // the end re-read that row too).
+    auto patch = [&](TileRegs<G::R>& regs, int t0) {
+        if constexpr (FUSED) {
+            if (t0 <= pos && pos < t0 + TILE) {      // wave-uniform
+                const int last = t_end - t0 - 1;
+#pragma unroll
+                for (int r = 0; r < G::R; ++r) {
+                    if (t0 + min(r * G::RPW + grp, last) == pos) {
+                        regs.k[r] = sh_knew[col];
+                        regs.v[r] = sh_vnew[col];
+                    }
+                }
+            }
+        }
+    };
+
     // q slice of every head of the group, pre-multiplied by scale.
     float qv[NREP][E];
 #pragma unroll
     for (int h = 0; h < NREP; ++h) {
-        const float* qp = a.q + ((size_t)seq * a.n_q + g * NREP + h) * D + col * E;
+        const float* qp;
+        if constexpr (FUSED) qp = &sh_q[h][col * E];
+        else qp = a.q + ((size_t)seq * a.n_q + g * NREP + h) * D + col * E;
 #pragma unroll
         for (int e = 0; e < E; e += 4) {
             float4 t = *reinterpret_cast<const float4*>(qp + e);
@@ -274,33 +442,14 @@ split_kv_decode_kernel(DecodeArgs a) {
         for (int e = 0; e < E; ++e) o[h][e] = 0.f;
     }
 
-    TileWalker<D, NREP, BF16, PAGED> walk{a, nullptr, nullptr, nullptr, 0, g, t_end, grp, col};
-    __shared__ int sh_pages[kMaxChunkPages];
-    if constexpr (PAGED) {
-        // The chunk's page ids, once per workgroup; an id outside the pool (a
-        // table the caller left unassigned) is clamped so no load can fault.
-        const int p0 = t_begin >> 6, np = ((t_end - 1) >> 6) - p0 + 1;
-        const int32_t* row = a.block_table + (size_t)cache_row * a.max_pages + p0;
-        for (int i = threadIdx.x; i < np; i += THREADS) sh_pages[i] = min(max(row[i], 0), a.num_pages - 1);
-        __syncthreads();
-        walk.pages = sh_pages;
-        walk.page0 = p0;
-    } else {
-        const size_t off = ((size_t)seq * a.n_kv + g) * (size_t)a.T * TileWalker<D, NREP, BF16, PAGED>::ROW_BYTES;
-        walk.kbase = static_cast<const char*>(a.k) + off;
-        walk.vbase = static_cast<const char*>(a.v) + off;
-    }
+    if constexpr (!FUSED) setup_walk();
 
-    constexpr int STRIDE = W * TILE;
-    const int first = t_begin + wave * TILE;
-    const int n_tiles = first < t_end ? (t_end - first + STRIDE - 1) / STRIDE : 0;   // wave-uniform
     if (n_tiles > 0) {
         if constexpr (kPrefetch) {
             // Two register tiles, alternating: the loads of tile i+1 are issued
             // before tile i is reduced.  No tile is loaded twice (a repeated
             // non-temporal load misses the cache and costs HBM bytes).
-            TileRegs<G::R> ra, rb;
-            walk.load(first, ra);
+            if (!first_loaded) walk.load(first, ra);
             if constexpr (PAGED) {
                 // Loads behind wave-uniform branches.  The compiler's wait
                 // before reducing tile i then covers the path without tile
@@ -311,9 +460,11 @@ split_kv_decode_kernel(DecodeArgs a) {
                 for (int i = 0; i < n_tiles; i += 2) {
                     const int ta = first + i * STRIDE;
                     if (i + 1 < n_tiles) walk.load(ta + STRIDE, rb);
+                    patch(ra, ta);
                     consume<D, NREP, BF16>(ra, t_end - ta, grp, qv, m, l, o);
                     if (i + 1 >= n_tiles) break;
                     if (i + 2 < n_tiles) walk.load(ta + 2 * STRIDE, ra);
+                    patch(rb, ta + STRIDE);
                     consume<D, NREP, BF16>(rb, t_end - ta - STRIDE, grp, qv, m, l, o);
                 }
             } else {
@@ -339,9 +490,10 @@ split_kv_decode_kernel(DecodeArgs a) {
             }
         } else {
             for (int i = 0; i < n_tiles; ++i) {
-                TileRegs<G::R> ra;
-                walk.load(first + i * STRIDE, ra);
-                consume<D, NREP, BF16>(ra, t_end - first - i * STRIDE, grp, qv, m, l, o);
+                TileRegs<G::R> rt;
+                walk.load(first + i * STRIDE, rt);
+                patch(rt, first + i * STRIDE);
+                consume<D, NREP, BF16>(rt, t_end - first - i * STRIDE, grp, qv, m, l, o);
             }
         }
     }
@@ -396,6 +548,11 @@ split_kv_decode_kernel(DecodeArgs a) {
             }
         }
     }
+    if constexpr (FUSED) {
+        // Commit: one workgroup per sequence; no workgroup of this launch
+        // reads the device length.
+        if (a.commit && owner && g == 0 && threadIdx.x == 0) a.lens_out[cache_row] = pos + 1;
+    }
 }
 
 // Log-sum-exp merge of the chunk partials of one (sequence, query head):
@@ -405,7 +562,7 @@ split_kv_decode_kernel(DecodeArgs a) {
 // serialised across the device).  MT threads read the partials as float4
 // columns, PARTS chunks at a time, so one round trip covers up to MT/(D/4)
 // chunks.
-template <int D, bool PAGED, int MT>
+template <int D, bool PAGED, int MT, bool FUSED = false>
 __global__ void __launch_bounds__(MT)
 lse_merge_kernel(DecodeArgs a) {
     constexpr int V4 = D / 4;
@@ -413,7 +570,9 @@ lse_merge_kernel(DecodeArgs a) {
     const int bh = blockIdx.x;
     const int seq = bh / a.n_q;
     int len;
-    if constexpr (PAGED) {
+    if constexpr (FUSED) {
+        len = min(min(a.pos.row[seq] + 1, a.max_pages * 64), a.n_split * a.chunk);
+    } else if constexpr (PAGED) {
         const int row = a.rows.row[seq];
         len = min(min(a.seq_lens[row] + a.n_pending, a.max_pages * 64), a.n_split * a.chunk);
     } else {
@@ -537,7 +696,7 @@ void carve_ws(DecodeArgs& a, void* ws, long long bh) {
     a.part_o = a.part_ml + (size_t)bh * a.n_split * 2;
 }
 
-template <int D, int NREP, bool BF16, bool PAGED>
+template <int D, int NREP, bool BF16, bool PAGED, bool FUSED>
 sa_status launch_decode(const DecodeArgs& a, int n_seq, hipStream_t st) {
     constexpr int W = waves_for<D, NREP>();
     dim3 grid(a.n_split, a.n_kv, n_seq);
@@ -548,38 +707,49 @@ sa_status launch_decode(const DecodeArgs& a, int n_seq, hipStream_t st) {
         } else {
             hipLaunchKernelGGL((split_kv_decode_kernel<D, NREP, BF16, PAGED, W>), grid, dim3(W * kWave), 0, st, a);
         }
+    } else if constexpr (PAGED && NREP <= 4 && NREP * D <= 512) {
+        // Paged launches that fit one round of workgroups (short sequences, a
+        // decode step of a few rows) use eight waves: half the tiles per
+        // wave, so fewer dependent load round trips.
+        if ((long long)a.n_split * a.n_kv * n_seq <= device_cu_count()) {
+            hipLaunchKernelGGL((split_kv_decode_kernel<D, NREP, BF16, PAGED, kWavesOneRound, FUSED>), grid,
+                               dim3(kWavesOneRound * kWave), 0, st, a);
+        } else {
+            hipLaunchKernelGGL((split_kv_decode_kernel<D, NREP, BF16, PAGED, W, FUSED>), grid, dim3(W * kWave), 0, st,
+                               a);
+        }
     } else {
-        hipLaunchKernelGGL((split_kv_decode_kernel<D, NREP, BF16, PAGED, W>), grid, dim3(W * kWave), 0, st, a);
+        hipLaunchKernelGGL((split_kv_decode_kernel<D, NREP, BF16, PAGED, W, FUSED>), grid, dim3(W * kWave), 0, st, a);
     }
     SA_CHECK_LAUNCH();
     if (a.n_split > 1) {
         const dim3 mgrid(n_seq * a.n_q);
         if (a.n_split >= 64)
-            hipLaunchKernelGGL((lse_merge_kernel<D, PAGED, 1024>), mgrid, dim3(1024), 0, st, a);
+            hipLaunchKernelGGL((lse_merge_kernel<D, PAGED, 1024, FUSED>), mgrid, dim3(1024), 0, st, a);
         else
-            hipLaunchKernelGGL((lse_merge_kernel<D, PAGED, 256>), mgrid, dim3(256), 0, st, a);
+            hipLaunchKernelGGL((lse_merge_kernel<D, PAGED, 256, FUSED>), mgrid, dim3(256), 0, st, a);
         SA_CHECK_LAUNCH();
     }
     return SA_OK;
 }
 
-template <int D, bool BF16, bool PAGED>
+template <int D, bool BF16, bool PAGED, bool FUSED>
 sa_status dispatch_nrep(const DecodeArgs& a, int n_seq, int nrep, hipStream_t st) {
     switch (nrep) {
-        case 1: return launch_decode<D, 1, BF16, PAGED>(a, n_seq, st);
-        case 2: return launch_decode<D, 2, BF16, PAGED>(a, n_seq, st);
-        case 4: return launch_decode<D, 4, BF16, PAGED>(a, n_seq, st);
-        case 8: return launch_decode<D, 8, BF16, PAGED>(a, n_seq, st);
+        case 1: return launch_decode<D, 1, BF16, PAGED, FUSED>(a, n_seq, st);
+        case 2: return launch_decode<D, 2, BF16, PAGED, FUSED>(a, n_seq, st);
+        case 4: return launch_decode<D, 4, BF16, PAGED, FUSED>(a, n_seq, st);
+        case 8: return launch_decode<D, 8, BF16, PAGED, FUSED>(a, n_seq, st);
         default: return fail(SA_EINVAL, "n_q_heads / n_kv_heads must be 1, 2, 4 or 8");
     }
 }
 
-template <bool BF16, bool PAGED>
+template <bool BF16, bool PAGED, bool FUSED = false>
 sa_status dispatch_decode(const DecodeArgs& a, int n_seq, int d, int nrep, hipStream_t st) {
     switch (d) {
-        case 64: return dispatch_nrep<64, BF16, PAGED>(a, n_seq, nrep, st);
-        case 128: return dispatch_nrep<128, BF16, PAGED>(a, n_seq, nrep, st);
-        case 256: return dispatch_nrep<256, BF16, PAGED>(a, n_seq, nrep, st);
+        case 64: return dispatch_nrep<64, BF16, PAGED, FUSED>(a, n_seq, nrep, st);
+        case 128: return dispatch_nrep<128, BF16, PAGED, FUSED>(a, n_seq, nrep, st);
+        case 256: return dispatch_nrep<256, BF16, PAGED, FUSED>(a, n_seq, nrep, st);
         default: return fail(SA_EINVAL, "head_dim must be 64, 128 or 256");
     }
 }
@@ -668,6 +838,51 @@ sa_status decode_paged(const PagedView& c, const float* q, int n_seq, const int3
             SA_TRY((dispatch_decode<true, true>(a, m, c.d, n_q / c.n_kv, st)));
         } else {
             SA_TRY((dispatch_decode<false, true>(a, m, c.d, n_q / c.n_kv, st)));
+        }
+    }
+    return SA_OK;
+}
+
+sa_status decode_paged_fused(const PagedView& c, const float* q, int n_seq, const int32_t* seq_ids, int n_q,
+                             const FusedAppend& f, int max_len, long long total_len, float scale, float* out,
+                             void* ws, size_t ws_bytes, hipStream_t st) {
+    if (!q || !out || !f.k || !f.v || !f.pos || !f.lens) return fail(SA_EINVAL, "null pointer");
+    if (n_seq <= 0 || n_q <= 0 || n_q % c.n_kv) return fail(SA_EINVAL, "bad head counts");
+    if (!aligned16(q) || !aligned16(out)) return fail(SA_EINVAL, "q and out must be 16-byte aligned");
+    if (max_len <= 0) max_len = 1;
+    DecodeArgs a{};
+    a.k = c.k_pool; a.v = c.v_pool;
+    a.block_table = c.block_table; a.seq_lens = c.seq_lens;
+    a.n_kv = c.n_kv; a.n_q = n_q; a.max_pages = c.max_pages; a.n_pending = 1;
+    a.num_pages = c.num_pages;
+    a.scale = scale;
+    a.wq = f.wq; a.wk = f.wk; a.eps = f.eps; a.cos_t = f.cos_t; a.sin_t = f.sin_t;
+    a.rope_max_pos = f.rope_max_pos; a.lens_out = f.lens; a.commit = f.commit ? 1 : 0;
+    // The same chunking as decode_paged with one pending token.
+    a.chunk = pick_chunk(total_len * c.n_kv, (long long)c.max_pages * 64, (long long)kMaxChunkPages * 64);
+    if (a.chunk > kMaxChunkPages * 64) return fail(SA_EINVAL, "max_pages_per_seq too large for the split cap");
+    a.n_split = (max_len + a.chunk - 1) / a.chunk;
+    const long long bh = (long long)std::min(n_seq, kRowsPerLaunch) * n_q;
+    const size_t need = ws_bytes_for(bh, a.n_split, c.d);
+    if (need > 0) {
+        if (!ws || ws_bytes < need) return fail(SA_ENOMEM, "workspace too small for split-KV partials");
+        carve_ws(a, ws, bh);
+    }
+    for (int i0 = 0; i0 < n_seq; i0 += kRowsPerLaunch) {
+        const int m = std::min(kRowsPerLaunch, n_seq - i0);
+        for (int i = 0; i < m; ++i) {
+            a.rows.row[i] = seq_ids ? seq_ids[i0 + i] : i0 + i;
+            a.pos.row[i] = f.pos[i0 + i];
+        }
+        a.q = q + (size_t)i0 * n_q * c.d;
+        a.out = out + (size_t)i0 * n_q * c.d;
+        a.q_out = f.q_out ? f.q_out + (size_t)i0 * n_q * c.d : nullptr;
+        a.k_new = f.k + (size_t)i0 * c.n_kv * c.d;
+        a.v_new = f.v + (size_t)i0 * c.n_kv * c.d;
+        if (c.bf16) {
+            SA_TRY((dispatch_decode<true, true, true>(a, m, c.d, n_q / c.n_kv, st)));
+        } else {
+            SA_TRY((dispatch_decode<false, true, true>(a, m, c.d, n_q / c.n_kv, st)));
         }
     }
     return SA_OK;

@@ -118,66 +118,6 @@ struct AppendArgs {
     float eps;
 };
 
-// One head row held by a wave as rotate-half pairs: lane j owns elements
-// i and i + D/2 for i = j, j + 64, ...
-template <int D>
-struct RowPairs {
-    static constexpr int H = D / 2;
-    static constexpr int NP = (H + kWave - 1) / kWave;
-    float lo[NP], hi[NP];
-
-    __device__ __forceinline__ void load(const float* x, int lane) {
-#pragma unroll
-        for (int c = 0; c < NP; ++c) {
-            const int i = lane + c * kWave;
-            lo[c] = (i < H) ? x[i] : 0.f;
-            hi[c] = (i < H) ? x[i + H] : 0.f;
-        }
-    }
-    // y = (x / sqrt(mean(x^2) + eps)) * w, eps inside the sqrt (reference
-    // tensor_cpp/src/qwen3_ops.cpp:716-717), or with eps_outside
-    // y = (x / (sqrt(mean(x^2)) + eps)) * w, as the reference's AVX2 layer
-    // (tensor_cpp/src/qwen3_ops_avx.cpp:537, :566).
-    __device__ __forceinline__ void rms_norm(const float* w, float eps, int lane, bool eps_outside = false) {
-        float ss = 0.f;
-#pragma unroll
-        for (int c = 0; c < NP; ++c) ss = fmaf(lo[c], lo[c], fmaf(hi[c], hi[c], ss));
-        ss = group_reduce<OpSum, 1, kWave>(ss);
-        const float rms = eps_outside ? sqrtf(ss / (float)D) + eps : sqrtf(ss / (float)D + eps);
-#pragma unroll
-        for (int c = 0; c < NP; ++c) {
-            const int i = lane + c * kWave;
-            if (i < H) {
-                lo[c] = (lo[c] / rms) * w[i];
-                hi[c] = (hi[c] / rms) * w[i + H];
-            }
-        }
-    }
-    // x' = x cos + rotate_half(x) sin with rotate_half(x) = [-x2, x1], cos/sin
-    // of row pos (reference tensor_cpp/src/qwen3_ops.cpp:30-64, 110-188).
-    __device__ __forceinline__ void rope(const float* cos_t, const float* sin_t, int pos, int lane) {
-#pragma unroll
-        for (int c = 0; c < NP; ++c) {
-            const int i = lane + c * kWave;
-            if (i < H) {
-                const float cs = cos_t[(size_t)pos * H + i];
-                const float sn = sin_t[(size_t)pos * H + i];
-                const float l2 = lo[c] * cs - hi[c] * sn;
-                const float h2 = hi[c] * cs + lo[c] * sn;
-                lo[c] = l2;
-                hi[c] = h2;
-            }
-        }
-    }
-    __device__ __forceinline__ void store(float* y, int lane) const {
-#pragma unroll
-        for (int c = 0; c < NP; ++c) {
-            const int i = lane + c * kWave;
-            if (i < H) { y[i] = lo[c]; y[i + H] = hi[c]; }
-        }
-    }
-};
-
 template <int D>
 __global__ void __launch_bounds__(256)
 qk_norm_rope_kernel(const float* x, int n_rows, const int32_t* pos, const float* w, float eps,
@@ -552,6 +492,46 @@ extern "C" sa_status sa_paged_decode(const sa_kvcache* c, int layer, const float
     pv.bf16 = c->desc.kv_dtype == SA_DTYPE_BF16;
     return decode_paged(pv, q, n_seq, seq_ids, n_q_heads, n_pending, max_len, total, scale, out, ws,
                         ws_bytes, as_stream(stream));
+}
+
+extern "C" sa_status sa_append_decode(sa_kvcache* c, int layer, const float* q, const float* k, const float* v,
+                                      int n_seq, const int32_t* seq_ids, int n_q_heads, const float* q_norm_w,
+                                      const float* k_norm_w, float eps, const float* rope_cos,
+                                      const float* rope_sin, int rope_max_pos, float scale, float* out,
+                                      float* q_out, void* ws, size_t ws_bytes, int commit, sa_stream_t stream) {
+    clear_error();
+    if (!valid_cache(c)) return fail(SA_EINVAL, "invalid cache");
+    if (layer < 0 || layer >= c->desc.num_layers) return fail(SA_ERANGE, "Layer index out of range");
+    if (!q || !k || !v || !out) return fail(SA_EINVAL, "null q, k, v or out");
+    if (n_seq <= 0) return fail(SA_EINVAL, "n_seq must be positive");
+    if (n_q_heads <= 0 || n_q_heads % c->desc.num_kv_heads) return fail(SA_EINVAL, "bad head counts");
+    if ((rope_cos == nullptr) != (rope_sin == nullptr)) return fail(SA_EINVAL, "cos and sin go together");
+    if (rope_cos && rope_max_pos <= 0) return fail(SA_EINVAL, "RoPE table needs rope_max_pos > 0");
+    Verdict vd = c->pt.check_append(seq_ids, n_seq, 1, rope_cos ? rope_max_pos : 0);
+    if (!vd.ok()) return refused(vd);
+    int max_len = 0;
+    long long total = 0;
+    vd = c->pt.check_decode(seq_ids, n_seq, 1, &max_len, &total);
+    if (!vd.ok()) return refused(vd);
+    std::vector<int32_t> pos(n_seq);
+    for (int i = 0; i < n_seq; ++i) pos[i] = c->pt.len(seq_ids ? seq_ids[i] : i);
+    PagedView pv;
+    pv.k_pool = k_pool_of(c, layer); pv.v_pool = v_pool_of(c, layer);
+    pv.block_table = c->d_table; pv.seq_lens = c->d_lens;
+    pv.n_kv = c->desc.num_kv_heads; pv.d = c->desc.head_dim;
+    pv.max_pages = c->desc.max_pages_per_seq; pv.num_pages = c->desc.num_pages;
+    pv.bf16 = c->desc.kv_dtype == SA_DTYPE_BF16;
+    FusedAppend f{};
+    f.k = k; f.v = v; f.wq = q_norm_w; f.wk = k_norm_w; f.eps = eps;
+    f.cos_t = rope_cos; f.sin_t = rope_sin; f.rope_max_pos = rope_max_pos;
+    f.q_out = q_out; f.lens = c->d_lens; f.pos = pos.data(); f.commit = commit != 0;
+    SA_TRY(decode_paged_fused(pv, q, n_seq, seq_ids, n_q_heads, f, max_len, total, scale, out, ws, ws_bytes,
+                              as_stream(stream)));
+    if (commit) {
+        vd = c->pt.commit(seq_ids, n_seq, 1);   // checked above: cannot be refused
+        if (!vd.ok()) return refused(vd);
+    }
+    return SA_OK;
 }
 
 extern "C" sa_status sa_kvcache_gather(const sa_kvcache* c, int layer, int seq, int len, float* k_out,

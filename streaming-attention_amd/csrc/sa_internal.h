@@ -91,6 +91,93 @@ __device__ __forceinline__ float group_reduce(float v) {
     return v;
 }
 
+// One head row held by a wave as rotate-half pairs: lane j owns elements
+// i and i + D/2 for i = j, j + 64, ...
+template <int D>
+struct RowPairs {
+    static constexpr int H = D / 2;
+    static constexpr int NP = (H + kWave - 1) / kWave;
+    float lo[NP], hi[NP];
+
+    __device__ __forceinline__ void load(const float* x, int lane) {
+#pragma unroll
+        for (int c = 0; c < NP; ++c) {
+            const int i = lane + c * kWave;
+            lo[c] = (i < H) ? x[i] : 0.f;
+            hi[c] = (i < H) ? x[i + H] : 0.f;
+        }
+    }
+    // y = (x / sqrt(mean(x^2) + eps)) * w, eps inside the sqrt (reference
+    // tensor_cpp/src/qwen3_ops.cpp:716-717), or with eps_outside
+    // y = (x / (sqrt(mean(x^2)) + eps)) * w, as the reference's AVX2 layer
+    // (tensor_cpp/src/qwen3_ops_avx.cpp:537, :566).
+    __device__ __forceinline__ void rms_norm(const float* w, float eps, int lane, bool eps_outside = false) {
+        float wl[NP], wh[NP];
+        load_pairs(w, lane, wl, wh);
+        rms_norm_with(wl, wh, eps, eps_outside);
+    }
+    // The same with this lane's weight pairs already loaded (load_pairs).
+    // Products and sums are rounded as written (no contraction), so every
+    // kernel that uses these rows computes the same bits.
+    __device__ __forceinline__ void rms_norm_with(const float (&wl)[NP], const float (&wh)[NP], float eps,
+                                                  bool eps_outside = false) {
+#pragma clang fp contract(off)
+        float ss = 0.f;
+#pragma unroll
+        for (int c = 0; c < NP; ++c) ss = fmaf(lo[c], lo[c], fmaf(hi[c], hi[c], ss));
+        ss = group_reduce<OpSum, 1, kWave>(ss);
+        const float rms = eps_outside ? sqrtf(ss / (float)D) + eps : sqrtf(ss / (float)D + eps);
+#pragma unroll
+        for (int c = 0; c < NP; ++c) {
+            lo[c] = (lo[c] / rms) * wl[c];
+            hi[c] = (hi[c] / rms) * wh[c];
+        }
+    }
+    // x' = x cos + rotate_half(x) sin with rotate_half(x) = [-x2, x1], cos/sin
+    // of row pos (reference tensor_cpp/src/qwen3_ops.cpp:30-64, 110-188).
+    __device__ __forceinline__ void rope(const float* cos_t, const float* sin_t, int pos, int lane) {
+        float cs[NP], sn[NP];
+        load_row(cos_t + (size_t)pos * H, lane, cs);
+        load_row(sin_t + (size_t)pos * H, lane, sn);
+        rope_with(cs, sn);
+    }
+    // The same with this lane's cos/sin already loaded (load_row of row pos).
+    __device__ __forceinline__ void rope_with(const float (&cs)[NP], const float (&sn)[NP]) {
+#pragma clang fp contract(off)
+#pragma unroll
+        for (int c = 0; c < NP; ++c) {
+            const float l2 = lo[c] * cs[c] - hi[c] * sn[c];
+            const float h2 = hi[c] * cs[c] + lo[c] * sn[c];
+            lo[c] = l2;
+            hi[c] = h2;
+        }
+    }
+    // This lane's elements i and i + D/2 (i = lane, lane + 64, ...) of x[D].
+    __device__ static __forceinline__ void load_pairs(const float* x, int lane, float (&l)[NP], float (&h)[NP]) {
+#pragma unroll
+        for (int c = 0; c < NP; ++c) {
+            const int i = lane + c * kWave;
+            l[c] = (i < H) ? x[i] : 0.f;
+            h[c] = (i < H) ? x[i + H] : 0.f;
+        }
+    }
+    // This lane's elements i = lane, lane + 64, ... of a row of D/2.
+    __device__ static __forceinline__ void load_row(const float* x, int lane, float (&v)[NP]) {
+#pragma unroll
+        for (int c = 0; c < NP; ++c) {
+            const int i = lane + c * kWave;
+            v[c] = (i < H) ? x[i] : 0.f;
+        }
+    }
+    __device__ __forceinline__ void store(float* y, int lane) const {
+#pragma unroll
+        for (int c = 0; c < NP; ++c) {
+            const int i = lane + c * kWave;
+            if (i < H) { y[i] = lo[c]; y[i + H] = hi[c]; }
+        }
+    }
+};
+
 // Cache rows of the sequences of one launch, passed by value in the kernel
 // arguments (the host has checked every one of them against the page table).
 constexpr int kRowsPerLaunch = 64;
@@ -115,6 +202,33 @@ size_t paged_ws(int n_seq, int n_q, int n_kv, int d, int max_pages);
 sa_status decode_paged(const PagedView& c, const float* q, int n_seq, const int32_t* seq_ids,
                        int n_q, int n_pending, int max_len, long long total_len, float scale,
                        float* out, void* ws, size_t ws_bytes, hipStream_t st);
+
+// The append half of a fused decode step: the new token of every sequence
+// (raw q [n_seq][n_q][D] is decode_paged's q; k, v [n_seq][n_kv][D]), its
+// per-head RMSNorm weights (NULL: none) and RoPE tables (NULL: none), the
+// position of the token in each sequence (its committed length, host array
+// in call order), and whether to commit it (seq_lens[row] = pos + 1).
+struct FusedAppend {
+    const float* k;
+    const float* v;
+    const float* wq;
+    const float* wk;
+    float eps;
+    const float* cos_t;
+    const float* sin_t;
+    int rope_max_pos;
+    float* q_out;              // NULL, or receives the normed, rotated q
+    int32_t* lens;             // the cache's device lengths (written on commit)
+    const int32_t* pos;        // host, [n_seq]
+    bool commit;
+};
+
+// decode_paged with the step's append folded in: one launch per
+// kRowsPerLaunch sequences when every sequence fits one chunk, plus the LSE
+// merge launch otherwise.  max_len / total_len count the new token.
+sa_status decode_paged_fused(const PagedView& c, const float* q, int n_seq, const int32_t* seq_ids, int n_q,
+                             const FusedAppend& f, int max_len, long long total_len, float scale, float* out,
+                             void* ws, size_t ws_bytes, hipStream_t st);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 

@@ -153,10 +153,11 @@ def test_paged_decode_seq_ids_subset(sa, oracle, synth):
     cache.close()
 
 
-def run_layer_decode_loop(sa, synth, bf16, steps=100, prompt=128, seed=40):
-    """One layer, B=1, 16q/8kv, D=128: prompt append, then `steps` decode steps.
-    Returns (GPU outputs [steps, 16, 128], the dense fp32 K/V the oracle needs,
-    the roped q of each step)."""
+def run_layer_decode_loop(sa, synth, bf16, steps=100, prompt=128, seed=40, fused=False):
+    """One layer, B=1, 16q/8kv, D=128: prompt append, then `steps` decode steps
+    (append, decode, commit as three calls, or fused: one sa_append_decode
+    call that commits).  Returns (GPU outputs [steps, 16, 128], the dense fp32
+    K/V the oracle needs, the roped q of each step)."""
     cache = sa.KVCache(1, HKV, D, 1, (prompt + steps + 63) // 64, (prompt + steps + 63) // 64,
                        sa.SA_DTYPE_BF16 if bf16 else sa.SA_DTYPE_F32)
     cos, sin = sa.rope_tables(prompt + steps, D, 1e6)
@@ -173,10 +174,17 @@ def run_layer_decode_loop(sa, synth, bf16, steps=100, prompt=128, seed=40):
     v_all = synth.normal(seed, 7, (steps, 1, 1, HKV, D))
     ws = torch.zeros(max(cache.decode_ws_bytes(1, HQ), 1), dtype=torch.uint8, device="cuda")
     out = torch.empty(1, HQ, D, device="cuda")
+    q_r = torch.empty(1, HQ, D, device="cuda")
     for t in range(steps):
-        q_r = cache.append(0, dev(q_all[t]), dev(k_all[t]), dev(v_all[t]), wq, wk, 1e-6, rope=(cos, sin))
-        cache.decode(0, q_r.view(1, HQ, D), float(SCALE), n_pending=1, out=out, ws=ws)
-        cache.commit(1, n_seqs=1)
+        if fused:
+            cache.append_decode(0, dev(q_all[t]).view(1, HQ, D), dev(k_all[t]).view(1, HKV, D),
+                                dev(v_all[t]).view(1, HKV, D), float(SCALE), wq, wk, 1e-6, rope=(cos, sin), out=out,
+                                q_out=q_r, ws=ws, commit=True)
+        else:
+            q_r = cache.append(0, dev(q_all[t]), dev(k_all[t]), dev(v_all[t]), wq, wk, 1e-6, rope=(cos, sin))
+            cache.decode(0, q_r.view(1, HQ, D), float(SCALE), n_pending=1, out=out, ws=ws)
+            cache.commit(1, n_seqs=1)
+        assert cache.length(0) == prompt + t + 1
         outs.append(host(out).copy())
         qs.append(host(q_r).reshape(HQ, D))
     gk, gv = cache.gather(0, 0, prompt + steps)
@@ -185,9 +193,10 @@ def run_layer_decode_loop(sa, synth, bf16, steps=100, prompt=128, seed=40):
             (kp, vp, q_all, k_all, v_all, host(wq), host(wk)))
 
 
-def test_layer_decode_loop_fp32(sa, oracle, synth):
+@pytest.mark.parametrize("fused", [False, True])
+def test_layer_decode_loop_fp32(sa, oracle, synth, fused):
     prompt, steps = 128, 100
-    outs, gk, gv, qs, raw = run_layer_decode_loop(sa, synth, False, steps, prompt)
+    outs, gk, gv, qs, raw = run_layer_decode_loop(sa, synth, False, steps, prompt, fused=fused)
     kp, vp, q_all, k_all, v_all, wq, wk = raw
     cos, sin = oracle.rope_tables(prompt + steps, D, 1e6)
     # oracle K/V: normed + roped keys at their positions, raw values
@@ -207,12 +216,13 @@ def test_layer_decode_loop_fp32(sa, oracle, synth):
         assert_f32(outs[t], want)
 
 
-def test_layer_decode_loop_bf16(sa, oracle, synth):
+@pytest.mark.parametrize("fused", [False, True])
+def test_layer_decode_loop_bf16(sa, oracle, synth, fused):
     """bf16 KV: relative L2 <= 2e-2 per step, and a greedy readout of the
     attention output (fixed random projection to 512 logits) picks the same
     token as the oracle on the same bf16 K/V for 32 steps."""
     prompt, steps = 128, 32
-    outs, gk, gv, qs, raw = run_layer_decode_loop(sa, synth, True, steps, prompt)
+    outs, gk, gv, qs, raw = run_layer_decode_loop(sa, synth, True, steps, prompt, fused=fused)
     kp, vp, q_all, k_all, v_all, wq, wk = raw
     cos, sin = oracle.rope_tables(prompt + steps, D, 1e6)
     N = prompt + steps

@@ -1,9 +1,9 @@
 """Decode steps captured into a HIP graph and replayed.
 
-Each step (fused q/k norm + RoPE + append, paged decode, commit) is a fixed
-set of launches whose parameters the host derives from the committed
-lengths, so a capture of n steps replays them exactly from the same starting
-length.  A replay advances the lengths on the device only; the caller sets
+Each step (fused q/k norm + RoPE + append, paged decode, commit; or the same
+as one sa_append_decode launch) is a fixed set of launches whose parameters
+the host derives from the committed lengths, so a capture of n steps replays
+them exactly from the same starting length.  A replay advances the lengths on the device only; the caller sets
 the host's view (sa_kvcache_set_len) before and after.  The replays run several times with eager work and synchronisations
 in between, and every replay's per-step outputs must equal the eager run's
 bit for bit (the same kernels with the same arguments).
@@ -17,8 +17,9 @@ import torch
 pytestmark = pytest.mark.gpu
 
 
+@pytest.mark.parametrize("fused", [False, True])
 @pytest.mark.parametrize("kv", ["f32", "bf16"])
-def test_graph_replay_equals_eager(sa, synth, kv):
+def test_graph_replay_equals_eager(sa, synth, kv, fused):
     HQ, HKV, D, P, N = 8, 4, 128, 70, 24
     dt = sa.SA_DTYPE_F32 if kv == "f32" else sa.SA_DTYPE_BF16
     cache = sa.KVCache(1, HKV, D, 1, 2, 2, dt)
@@ -42,9 +43,13 @@ def test_graph_replay_equals_eager(sa, synth, kv):
 
     def steps(outs):
         for t in range(N):
-            cache.append(0, q[t], k[t], v[t], wq, wk, 1e-6, rope=(cos, sin), q_out=qo)
-            cache.decode(0, qo.view(1, HQ, D), sc, n_pending=1, out=outs[t], ws=ws)
-            cache.commit(1, n_seqs=1)
+            if fused:
+                cache.append_decode(0, q[t].view(1, HQ, D), k[t].view(1, HKV, D), v[t].view(1, HKV, D), sc, wq, wk,
+                                    1e-6, rope=(cos, sin), out=outs[t], ws=ws, commit=True)
+            else:
+                cache.append(0, q[t], k[t], v[t], wq, wk, 1e-6, rope=(cos, sin), q_out=qo)
+                cache.decode(0, qo.view(1, HQ, D), sc, n_pending=1, out=outs[t], ws=ws)
+                cache.commit(1, n_seqs=1)
 
     eager = torch.empty(N, 1, HQ, D, device="cuda")
     prompt()
