@@ -4,7 +4,8 @@
 // (tensor_cpp/src/qwen3_ops.cpp:620-1014), qwen3_mlp (:265-296), and the ops
 // they call: embedding (tensor_cpp/src/ops.cpp:278-313), linear (:315-372),
 // rms_norm (:375-417).  The attention block itself runs on
-// sa_qknorm_rope_append + sa_paged_decode.
+// sa_append_decode (decode step) and sa_qknorm_rope_append + the causal
+// prefill kernel (prompt).
 //
 // Layout: the batch of B <= 64 token rows stays fp32 in a residual stream
 // x[B][hidden]; every projection is one GEMM Y = X W^T with bf16 weights in
@@ -750,10 +751,12 @@ extern "C" sa_status sa_qwen3_decode_step(sa_qwen3* m, sa_kvcache* cache, const 
         hipLaunchKernelGGL(qkv_split_kernel, dim3(M, (s.Nqkv + 1023) / 1024), dim3(256), 0, st, m->part, s.qkv.S,
                            M, s.Nq, s.Nk, m->q, m->k, m->v);
         SA_CHECK_LAUNCH();
-        SA_TRY(sa_qknorm_rope_append(cache, l, m->q, m->k, m->v, M, 1, nullptr, s.Hq, L.q_norm, L.k_norm, eps,
-                                     m->rope_cos, m->rope_sin, d.max_pos, m->q_rope, stream));
-        SA_TRY(sa_paged_decode(cache, l, m->q_rope, M, nullptr, s.Hq, 1, scale, m->attn, m->ws, m->ws_bytes,
-                               stream));
+        // q/k norm + RoPE, the K/V append and the paged decode in one launch
+        // per 64 sequences (plus the LSE merge of multi-chunk sequences); the
+        // last layer's call also commits the token.
+        SA_TRY(sa_append_decode(cache, l, m->q, m->k, m->v, M, nullptr, s.Hq, L.q_norm, L.k_norm, eps, m->rope_cos,
+                                m->rope_sin, d.max_pos, scale, m->attn, nullptr, m->ws, m->ws_bytes,
+                                l + 1 == d.num_layers ? 1 : 0, stream));
         SA_TRY(gemm(m->attn, M, L.o, s.o, m->part, st));
         hipLaunchKernelGGL(residual_norm_kernel, dim3(M), dim3(256), 0, st, m->part, s.o.S, M, s.H, m->x,
                            L.post_norm, eps, m->h);
@@ -776,5 +779,5 @@ extern "C" sa_status sa_qwen3_decode_step(sa_qwen3* m, sa_kvcache* cache, const 
     hipLaunchKernelGGL(argmax_final_kernel, dim3(M), dim3(64), 0, st, m->am_val, m->am_idx, kArgBlocks,
                        next_tokens);
     SA_CHECK_LAUNCH();
-    return sa_kvcache_commit(cache, nullptr, M, 1, stream);
+    return SA_OK;   // the last layer's sa_append_decode committed the token
 }
