@@ -5,6 +5,7 @@
 // correctness grid T x d with U(-1,1) inputs and a 1e-5 max-abs bar, thread
 // variants against serial at 1e-4, plus the KV cache and Qwen3 attention path.
 // Prints one line per check; exit status is the number of failures.
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -309,13 +310,59 @@ static void test_qwen3_attention() {
            }));
 }
 
+// The Tensor members of the reference's tensor.h (tensor_cpp/src/tensor.cpp):
+// element-wise arithmetic, reductions, shapes, factories, and matmul (GPU)
+// against a double-precision host product.
+static void test_tensor() {
+    Rng rng(7);
+    Tensor a(rng.vec(6), Shape({2, 3})), b(rng.vec(6), Shape({2, 3}));
+    bool ok = true;
+    const Tensor s = a + b, d = a - b, m = a * b, q = a / b, sc = a * 2.0f + 1.0f;
+    for (size_t i = 0; i < 6; ++i)
+        ok = ok && s[i] == a[i] + b[i] && d[i] == a[i] - b[i] && m[i] == a[i] * b[i] && q[i] == a[i] / b[i] &&
+             sc[i] == a[i] * 2.0f + 1.0f;
+    report("tensor element-wise", ok);
+    report("tensor shape mismatch throws", throws<std::invalid_argument>([&] { (void)(a + Tensor(Shape({3, 2}))); }));
+    Tensor acc = a;
+    acc += b;
+    acc *= 0.5f;
+    ok = true;
+    for (size_t i = 0; i < 6; ++i) ok = ok && acc[i] == (a[i] + b[i]) * 0.5f;
+    report("tensor in-place", ok);
+    double sum = 0;
+    for (size_t i = 0; i < 6; ++i) sum += a[i];
+    report("tensor reductions", std::fabs(a.sum() - sum) < 1e-6 && std::fabs(a.mean() - sum / 6) < 1e-6 &&
+                                    a.max() == *std::max_element(a.data(), a.data() + 6) &&
+                                    a.min() == *std::min_element(a.data(), a.data() + 6));
+    const Tensor t = a.transpose();
+    report("tensor transpose / index", t.shape() == Shape({3, 2}) && t({2, 1}) == a({1, 2}) && t({0, 1}) == a[3]);
+    const Tensor u = a.unsqueeze(0);
+    report("tensor squeeze / unsqueeze", u.shape() == Shape({1, 2, 3}) && u.squeeze().shape() == Shape({2, 3}));
+    const Tensor e = Tensor::eye(3, 4);
+    report("tensor eye / ones", e({2, 2}) == 1.0f && e({2, 3}) == 0.0f && e.sum() == 3.0f &&
+                                    Tensor::ones(Shape({2, 2})).sum() == 4.0f);
+    const size_t M = 37, K = 130, N = 67;
+    Tensor x(rng.vec(M * K), Shape({M, K})), w(rng.vec(K * N), Shape({K, N}));
+    const Tensor y = x.matmul(w);
+    double err = 0, ref_max = 0;
+    for (size_t i = 0; i < M; ++i)
+        for (size_t j = 0; j < N; ++j) {
+            double r = 0;
+            for (size_t k = 0; k < K; ++k) r += (double)x[i * K + k] * w[k * N + j];
+            err = std::max(err, std::fabs(r - y[i * N + j]));
+            ref_max = std::max(ref_max, std::fabs(r));
+        }
+    report("tensor matmul on the GPU", y.shape() == Shape({M, N}) && err <= 1e-5 * ref_max,
+           "max err " + std::to_string(err));
+}
+
 int main() {
     const struct {
         const char* name;
         void (*fn)();
     } suites[] = {{"correctness", test_correctness}, {"thread variants", test_thread_variants}, {"edges", test_edges},
                   {"kv cache", test_kv_cache},       {"ops", test_ops},                       {"rope", test_rope},
-                  {"qwen3 attention", test_qwen3_attention}};
+                  {"qwen3 attention", test_qwen3_attention}, {"tensor", test_tensor}};
     for (const auto& s : suites) {
         std::printf("== %s\n", s.name);
         std::fflush(stdout);
