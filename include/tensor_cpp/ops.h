@@ -13,11 +13,17 @@
  * Supported attention shapes: single-query decode (q_len = 1) and causal
  * prefill from position 0 (q_len = kv_len).  self_attention accepts a null or
  * all-zero mask with q_len = 1, or the causal mask with q_len = kv_len; any
- * other mask throws std::invalid_argument.
+ * other mask throws std::invalid_argument.  cross_attention takes any q_len
+ * and kv_len (every query row sees every key).
+ *
+ * The reference's all_reduce_sum and broadcast (MPI collectives, ops.h:338-339)
+ * are not here: this library serves one GPU per process.
  */
 #ifndef SA_AMD_TENSOR_CPP_OPS_H
 #define SA_AMD_TENSOR_CPP_OPS_H
 
+#include <cmath>
+#include <complex>
 #include <stdexcept>
 #include <vector>
 
@@ -53,6 +59,16 @@ namespace ops {
  * On the GPU. */
 Tensor add(const Tensor& input, const Tensor& other, float alpha = 1.0f);
 
+/* Index of the largest element (reference tensor_cpp/src/ops.cpp:213-272),
+ * the first of equal maxima.  dim = -1: over the whole tensor -> shape [1].
+ * dim = ndim - 1 (ndim >= 2): one index per leading row, shaped as the
+ * reference shapes it: the leading dims with keepdim, else those before the
+ * last two, [1] if none remain; where that shape does not hold the row count
+ * (say [B, V] with B > 1 and no keepdim) TensorL throws
+ * std::invalid_argument, as the reference's does.  Other dims throw
+ * std::runtime_error.  A host scan: the qwen3 functions return host logits. */
+TensorL argmax(const Tensor& input, int dim = -1, bool keepdim = false);
+
 /* Rows of weight [num_embeddings, dim] picked by indices -> [indices..., dim];
  * an index outside the table throws std::out_of_range unless it equals
  * padding_idx (a zero row) (reference tensor_cpp/src/ops.cpp:278-309).  A copy
@@ -67,12 +83,43 @@ Tensor linear(const Tensor& input, const Tensor& weight, const Tensor* bias = nu
  * (reference tensor_cpp/src/ops.cpp:375-418).  Only dim = -1 (the last). */
 Tensor rms_norm(const Tensor& input, const Tensor* weight = nullptr, float eps = 1e-8f, int dim = -1);
 
+/* Rotary embedding on [batch, seq, heads, dim] (reference
+ * tensor_cpp/include/tensor_cpp/ops.h:99-111, tensor_cpp/src/ops.cpp:424-487):
+ * element i of a head is paired with element i + dim/2 and the pair is
+ * rotated by the angle t * theta^(-i / dim) at sequence index t (the
+ * reference's frequencies, i / dim rather than the 2i / dim of
+ * compute_rope_freqs).  apply rotates the first seq_len positions on the GPU
+ * and returns zeros for positions past seq_len, as the reference.  dim must
+ * be even (the constructor throws std::invalid_argument otherwise, as the
+ * reference); apply takes dim 64, 128 or 256 and seq_len up to max_seq_len
+ * and the input's seq axis (std::invalid_argument otherwise). */
+class RotaryEmbedding {
+public:
+    RotaryEmbedding(size_t dim, size_t max_seq_len = 2048, float theta = 10000.0f);
+    Tensor apply(const Tensor& input, size_t seq_len);
+
+private:
+    size_t dim_;
+    size_t max_seq_len_;
+    float theta_;
+    std::vector<float> cos_, sin_;   // [max_seq_len][dim / 2]
+
+    void precompute_freqs_cis();
+};
+
 /* x * silu(gate), elementwise on the GPU (reference tensor_cpp/src/ops.cpp:493-509). */
 Tensor swiglu(const Tensor& x, const Tensor& gate);
 
 /* softmax(scale * Q K^T + mask) V (reference tensor_cpp/src/ops.cpp:514-641). */
 Tensor self_attention(const Tensor& query, const Tensor& key, const Tensor& value,
                       const Tensor* mask = nullptr, float scale = 1.0f);
+
+/* softmax(scale * Q K^T) V with query [batch, heads, q_len, head_dim] and
+ * key/value [batch, kv_heads, kv_len, head_dim] (reference
+ * tensor_cpp/src/ops.cpp:647-738).  The reference takes a mask argument and
+ * does not read it; so here. */
+Tensor cross_attention(const Tensor& query, const Tensor& key, const Tensor& value,
+                       const Tensor* mask = nullptr, float scale = 1.0f);
 
 /* Single-query helpers (reference tensor_cpp/src/ops.cpp:742-958). */
 std::vector<float> naive_attention_serial(const float* Q, const float* K, const float* V, int T, int d);

@@ -53,6 +53,10 @@ _REF_SIGS = {
     "ref_qwen3_forward": (_I, [_I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _I] + [_P] * 12 + [_I, _P]),
     "ref_set_threads": (None, [_I]),
     "ref_qwen3_forward_file": (_I, [C.c_char_p, _F, _I, _I, _I, _P, _P]),
+    "ref_load_weights": (_I, [C.c_char_p, _P, _P, C.c_int64]),
+    "ref_rotary": (_I, [_P, _I, _I, _I, _I, _I, _F, _I, _P]),
+    "ref_argmax": (C.c_long, [_P, _P, _I, _I, _I, _P, C.c_long, _P, _P]),
+    "ref_cross_attention": (None, [_P, _P, _P, _I, _I, _I, _I, _I, _F, _P]),
     "ref_time_decode_layer": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
 }
 
@@ -294,6 +298,46 @@ class Reference:
         if rc != 0:
             raise RuntimeError("reference loader or forward raised")
         return logits
+
+    def load_weights(self, path):
+        """(meta [7], flat fp32 weights) as the reference's load_qwen3_weights
+        reads them (layout: ref_load_weights in oracle/ref_shim.cpp)."""
+        import os
+        meta = np.zeros(7, np.int64)
+        if self.lib.ref_load_weights(os.fsencode(str(path)), _p(meta), None, 0) != 0:
+            raise RuntimeError("reference loader raised")
+        out = np.empty(int(meta[6]), np.float32)
+        if self.lib.ref_load_weights(os.fsencode(str(path)), _p(meta), _p(out), out.size) != 0:
+            raise RuntimeError("reference loader raised")
+        return meta, out
+
+    def rotary(self, x, max_seq, theta, seq_len):
+        """ops::RotaryEmbedding(D, max_seq, theta).apply(x [B][S][H][D], seq_len)."""
+        x = _f32(x)
+        B, S, H, D = x.shape
+        out = np.empty_like(x)
+        if self.lib.ref_rotary(_p(x), B, S, H, D, max_seq, float(theta), seq_len, _p(out)) != 0:
+            raise RuntimeError("reference RotaryEmbedding raised")
+        return out
+
+    def argmax(self, x, dim=-1, keepdim=False):
+        """ops::argmax -> (indices, shape), or None where the reference raises."""
+        x = _f32(x)
+        dims = np.asarray(x.shape, np.int64)
+        idx = np.zeros(max(1, x.size), np.int64)
+        shape = np.zeros(8, np.int64)
+        nd = C.c_int(0)
+        n = self.lib.ref_argmax(_p(x), _p(dims), x.ndim, dim, int(keepdim), _p(idx), idx.size, _p(shape),
+                                C.byref(nd))
+        return None if n < 0 else (idx[:n].copy(), tuple(int(s) for s in shape[:nd.value]))
+
+    def cross_attention(self, q, k, v, scale):
+        """ops::cross_attention(q [B][H][Sq][D], k/v [B][H][Sk][D], nullptr, scale)."""
+        q, k, v = _f32(q), _f32(k), _f32(v)
+        B, H, Sq, D = q.shape
+        out = np.empty_like(q)
+        self.lib.ref_cross_attention(_p(q), _p(k), _p(v), B, H, Sq, k.shape[2], D, float(scale), _p(out))
+        return out
 
     def set_threads(self, n):
         """omp_set_num_threads(n) for the reference's later OpenMP regions."""

@@ -365,4 +365,81 @@ int ref_qwen3_forward_file(const char* path, float eps, int B, int P, int n_step
     }
 }
 
+// load_qwen3_weights (tensor_cpp/src/qwen3_loader.cpp:163-296) itself:
+// meta[7] = num_layers, heads, kv heads, head_dim, hidden, vocab and the
+// float count of the flat copy; with out non-null and cap large enough, out
+// receives embed_tokens, norm_weight, lm_head, then per layer
+// input_layernorm, post_attention_layernorm, qkv_projs, q_proj, k_proj,
+// v_proj, q_norm, k_norm, o_proj, gate_proj, up_proj, down_proj.  Returns -1
+// on a reference exception.
+int ref_load_weights(const char* path, int64_t* meta, float* out, int64_t cap) {
+    try {
+        const q3::Qwen3Weights w = q3::load_qwen3_weights(path);
+        std::vector<const Tensor*> parts = {&w.embed_tokens, &w.norm_weight, &w.lm_head};
+        for (const auto& L : w.layers)
+            for (const Tensor* t : {&L.input_layernorm_weight, &L.post_attention_layernorm_weight, &L.qkv_projs,
+                                    &L.q_proj, &L.k_proj, &L.v_proj, &L.q_norm_weight, &L.k_norm_weight, &L.o_proj,
+                                    &L.gate_proj, &L.up_proj, &L.down_proj})
+                parts.push_back(t);
+        int64_t total = 0;
+        for (const Tensor* t : parts) total += (int64_t)t->size();
+        const int64_t m[7] = {(int64_t)w.num_layers, (int64_t)w.num_attention_heads, (int64_t)w.num_key_value_heads,
+                              (int64_t)w.head_dim, (int64_t)w.hidden_size, (int64_t)w.vocab_size, total};
+        std::memcpy(meta, m, sizeof(m));
+        if (out && cap >= total)
+            for (const Tensor* t : parts) {
+                std::memcpy(out, t->data(), t->size() * sizeof(float));
+                out += t->size();
+            }
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+// ops::RotaryEmbedding(D, max_seq, theta).apply(x [B][S][H][D], seq_len)
+// (tensor_cpp/src/ops.cpp:424-487).  Returns -1 on a reference exception.
+int ref_rotary(const float* x, int B, int S, int H, int D, int max_seq, float theta, int seq_len, float* out) {
+    try {
+        tensor_cpp::ops::RotaryEmbedding rope((size_t)D, (size_t)max_seq, theta);
+        Tensor in(std::vector<float>(x, x + (size_t)B * S * H * D), Shape({(size_t)B, (size_t)S, (size_t)H, (size_t)D}));
+        put(rope.apply(in, (size_t)seq_len), out);
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+// ops::argmax(x of shape dims[nd], dim, keepdim) (tensor_cpp/src/ops.cpp:213-272):
+// idx receives the indices (up to cap), shape_out[8] the result's dims, *out_nd
+// their count.  Returns the index count, or -1 on a reference exception.
+long ref_argmax(const float* x, const int64_t* dims, int nd, int dim, int keepdim, int64_t* idx, long cap,
+                int64_t* shape_out, int* out_nd) {
+    try {
+        std::vector<size_t> d(dims, dims + nd);
+        size_t n = 1;
+        for (size_t v : d) n *= v;
+        Tensor in(std::vector<float>(x, x + n), Shape(d));
+        TensorL r = tensor_cpp::ops::argmax(in, dim, keepdim != 0);
+        const long count = (long)r.size();
+        for (long i = 0; i < count && i < cap; ++i) idx[i] = r[i];
+        *out_nd = (int)r.shape().ndim();
+        for (int i = 0; i < *out_nd && i < 8; ++i) shape_out[i] = (int64_t)r.shape()[i];
+        return count;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+// ops::cross_attention(q [B][H][Sq][D], k/v [B][H][Sk][D], mask = nullptr,
+// scale) (tensor_cpp/src/ops.cpp:647-738).
+void ref_cross_attention(const float* q, const float* k, const float* v, int B, int H, int Sq, int Sk, int D,
+                         float scale, float* out) {
+    const Shape qs({(size_t)B, (size_t)H, (size_t)Sq, (size_t)D}), ks({(size_t)B, (size_t)H, (size_t)Sk, (size_t)D});
+    Tensor tq(std::vector<float>(q, q + qs.total()), qs);
+    Tensor tk(std::vector<float>(k, k + ks.total()), ks);
+    Tensor tv(std::vector<float>(v, v + ks.total()), ks);
+    put(tensor_cpp::ops::cross_attention(tq, tk, tv, nullptr, scale), out);
+}
+
 }  // extern "C"

@@ -1,5 +1,5 @@
 // Attention operators of the reference's ops namespace on the GPU
-// (reference tensor_cpp/src/ops.cpp:514-641, 742-1017, 1027-1599).
+// (reference tensor_cpp/src/ops.cpp:514-738, 742-1017, 1027-1599).
 #include "tensor_cpp/ops.h"
 
 #include <cmath>
@@ -127,6 +127,11 @@ Tensor self_attention(const Tensor& query, const Tensor& key, const Tensor& valu
         case MaskKind::kCausal: return causal_prefill(query, key, value, d, scale);
         default: throw std::invalid_argument("self_attention supports no mask, an all-zero mask or the causal mask");
     }
+}
+
+Tensor cross_attention(const Tensor& query, const Tensor& key, const Tensor& value, const Tensor* /*mask*/,
+                       float scale) {
+    return decode_rows(query, key, value, check_qkv(query, key, value), scale);
 }
 
 std::vector<float> naive_attention_serial(const float* Q, const float* K, const float* V, int T, int d) {

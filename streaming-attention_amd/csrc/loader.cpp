@@ -24,22 +24,14 @@
 #include <string>
 #include <vector>
 
+#include "safetensors.h"
 #include "sa_internal.h"
 #include "sa_qwen3.h"
 
 namespace sa {
 namespace {
 
-struct Entry {
-    std::string dtype;
-    std::vector<int64_t> shape;
-    uint64_t begin = 0, end = 0;
-    int64_t numel() const {
-        int64_t n = 1;
-        for (int64_t s : shape) n *= s;
-        return n;
-    }
-};
+using Entry = StEntry;
 
 // Recursive-descent reader of the header JSON.  Strings support the JSON
 // escapes (\uXXXX as UTF-8, surrogate pairs included); numbers other than
@@ -243,104 +235,109 @@ private:
     }
 };
 
-// A read-only mapping of the checkpoint with its parsed and checked header.
-class Checkpoint {
-public:
-    ~Checkpoint() {
-        if (map_ != MAP_FAILED && map_ != nullptr) munmap(map_, size_);
-        if (fd_ >= 0) close(fd_);
-    }
+}  // namespace
 
-    sa_status open_file(const char* path) {
-        if (!path) return fail(SA_EINVAL, "null path");
-        fd_ = ::open(path, O_RDONLY);
-        if (fd_ < 0) return fail(SA_EIO, std::string("cannot open ") + path + ": " + std::strerror(errno));
-        struct stat st{};
-        if (fstat(fd_, &st) != 0) return fail(SA_EIO, std::string("cannot stat ") + path);
-        size_ = static_cast<size_t>(st.st_size);
-        if (size_ < 8) return fail(SA_EIO, "file shorter than the 8-byte header length");
-        map_ = mmap(nullptr, size_, PROT_READ, MAP_PRIVATE, fd_, 0);
-        if (map_ == MAP_FAILED) return fail(SA_EIO, std::string("cannot map ") + path);
-        const unsigned char* b = static_cast<const unsigned char*>(map_);
-        uint64_t n = 0;
-        for (int i = 7; i >= 0; --i) n = (n << 8) | b[i];
-        if (n > size_ - 8) return fail(SA_EIO, "header length past the end of the file");
-        data_ = b + 8 + n;
-        data_size_ = size_ - 8 - n;
-        HeaderParser parser(reinterpret_cast<const char*>(b + 8), n);
-        if (!parser.parse(tensors_)) return fail(SA_EIO, "safetensors header: " + parser.error());
-        for (const auto& kv : tensors_) {
-            const Entry& t = kv.second;
-            const int es = elem_size(t.dtype);
-            for (int64_t s : t.shape)
-                if (s < 0) return fail(SA_EIO, kv.first + ": negative dimension");
-            if (t.end > data_size_) return fail(SA_EIO, kv.first + ": data range past the end of the file");
-            if (es > 0 && t.end - t.begin != static_cast<uint64_t>(t.numel()) * es)
-                return fail(SA_EIO, kv.first + ": byte range does not match shape and dtype");
+Checkpoint::~Checkpoint() {
+    if (map_ != MAP_FAILED && map_ != nullptr) munmap(map_, size_);
+    if (fd_ >= 0) close(fd_);
+}
+
+sa_status Checkpoint::open_file(const char* path) {
+    if (!path) return fail(SA_EINVAL, "null path");
+    fd_ = ::open(path, O_RDONLY);
+    if (fd_ < 0) return fail(SA_EIO, std::string("cannot open ") + path + ": " + std::strerror(errno));
+    struct stat st{};
+    if (fstat(fd_, &st) != 0) return fail(SA_EIO, std::string("cannot stat ") + path);
+    size_ = static_cast<size_t>(st.st_size);
+    if (size_ < 8) return fail(SA_EIO, "file shorter than the 8-byte header length");
+    map_ = mmap(nullptr, size_, PROT_READ, MAP_PRIVATE, fd_, 0);
+    if (map_ == MAP_FAILED) return fail(SA_EIO, std::string("cannot map ") + path);
+    const unsigned char* b = static_cast<const unsigned char*>(map_);
+    uint64_t n = 0;
+    for (int i = 7; i >= 0; --i) n = (n << 8) | b[i];
+    if (n > size_ - 8) return fail(SA_EIO, "header length past the end of the file");
+    data_ = b + 8 + n;
+    data_size_ = size_ - 8 - n;
+    HeaderParser parser(reinterpret_cast<const char*>(b + 8), n);
+    if (!parser.parse(tensors_)) return fail(SA_EIO, "safetensors header: " + parser.error());
+    for (const auto& kv : tensors_) {
+        const Entry& t = kv.second;
+        const int es = elem_size(t.dtype);
+        for (int64_t s : t.shape)
+            if (s < 0) return fail(SA_EIO, kv.first + ": negative dimension");
+        if (t.end > data_size_) return fail(SA_EIO, kv.first + ": data range past the end of the file");
+        if (es > 0 && t.end - t.begin != static_cast<uint64_t>(t.numel()) * es)
+            return fail(SA_EIO, kv.first + ": byte range does not match shape and dtype");
+    }
+    return SA_OK;
+}
+
+int Checkpoint::elem_size(const std::string& dtype) { return dtype == "BF16" ? 2 : dtype == "F32" ? 4 : 0; }
+
+const StEntry* Checkpoint::find(const std::string& name) const {
+    auto it = tensors_.find(name);
+    return it == tensors_.end() ? nullptr : &it->second;
+}
+
+sa_status Checkpoint::need(const std::string& name, const std::vector<int64_t>& shape, const StEntry** out) const {
+    const Entry* t = find(name);
+    if (!t) return fail(SA_EINVAL, "tensor not found: " + name);
+    if (elem_size(t->dtype) == 0) return fail(SA_EINVAL, name + ": dtype " + t->dtype + " not supported (BF16, F32)");
+    if (t->shape != shape) {
+        std::string got, want;
+        for (int64_t s : t->shape) got += std::to_string(s) + ",";
+        for (int64_t s : shape) want += std::to_string(s) + ",";
+        return fail(SA_EINVAL, name + ": shape [" + got + "] where [" + want + "] was expected");
+    }
+    *out = t;
+    return SA_OK;
+}
+
+void Checkpoint::to_f32(const StEntry& t, float* dst) const {
+    const unsigned char* src = bytes(t);
+    const size_t n = static_cast<size_t>(t.numel());
+    if (t.dtype == "F32") {
+        std::memcpy(dst, src, n * 4);
+        return;
+    }
+    for (size_t i = 0; i < n; ++i) {   // bf16 is the top half of an fp32
+        uint16_t b;
+        std::memcpy(&b, src + 2 * i, 2);
+        const uint32_t u = static_cast<uint32_t>(b) << 16;
+        std::memcpy(dst + i, &u, 4);
+    }
+}
+
+int Checkpoint::num_layers() const {
+    int n = 0;
+    const std::string pre = "model.layers.";
+    for (const auto& kv : tensors_) {
+        const std::string& k = kv.first;
+        if (k.compare(0, pre.size(), pre) != 0) continue;
+        size_t i = pre.size();
+        long v = 0;
+        bool digits = false;
+        while (i < k.size() && k[i] >= '0' && k[i] <= '9' && v < 1000000) {
+            v = v * 10 + (k[i++] - '0');
+            digits = true;
         }
-        return SA_OK;
+        if (digits && i < k.size() && k[i] == '.') n = std::max<long>(n, v + 1);
     }
+    return n;
+}
 
-    static int elem_size(const std::string& dtype) { return dtype == "BF16" ? 2 : dtype == "F32" ? 4 : 0; }
+std::string layer_tensor_name(int i, const char* leaf) { return "model.layers." + std::to_string(i) + "." + leaf; }
 
-    const Entry* find(const std::string& name) const {
-        auto it = tensors_.find(name);
-        return it == tensors_.end() ? nullptr : &it->second;
-    }
-    // The tensor `name` with exactly the given shape, in a supported dtype.
-    sa_status need(const std::string& name, std::vector<int64_t> shape, const Entry** out) const {
-        const Entry* t = find(name);
-        if (!t) return fail(SA_EINVAL, "tensor not found: " + name);
-        if (elem_size(t->dtype) == 0) return fail(SA_EINVAL, name + ": dtype " + t->dtype + " not supported (BF16, F32)");
-        if (t->shape != shape) {
-            std::string got, want;
-            for (int64_t s : t->shape) got += std::to_string(s) + ",";
-            for (int64_t s : shape) want += std::to_string(s) + ",";
-            return fail(SA_EINVAL, name + ": shape [" + got + "] where [" + want + "] was expected");
-        }
-        *out = t;
-        return SA_OK;
-    }
-    const unsigned char* bytes(const Entry& t) const { return data_ + t.begin; }
-    int num_layers() const {
-        int n = 0;
-        const std::string pre = "model.layers.";
-        for (const auto& kv : tensors_) {
-            const std::string& k = kv.first;
-            if (k.compare(0, pre.size(), pre) != 0) continue;
-            size_t i = pre.size();
-            long v = 0;
-            bool digits = false;
-            while (i < k.size() && k[i] >= '0' && k[i] <= '9' && v < 1000000) {
-                v = v * 10 + (k[i++] - '0');
-                digits = true;
-            }
-            if (digits && i < k.size() && k[i] == '.') n = std::max<long>(n, v + 1);
-        }
-        return n;
-    }
-
-private:
-    int fd_ = -1;
-    void* map_ = nullptr;
-    size_t size_ = 0;
-    const unsigned char* data_ = nullptr;
-    size_t data_size_ = 0;
-    std::map<std::string, Entry> tensors_;
-};
-
-std::string layer_name(int i, const char* leaf) { return "model.layers." + std::to_string(i) + "." + leaf; }
-
-sa_status read_desc(const Checkpoint& ck, sa_qwen3_desc* d) {
+sa_status read_qwen3_desc(const Checkpoint& ck, sa_qwen3_desc* d) {
     const Entry* embed = ck.find("model.embed_tokens.weight");
     if (!embed) return fail(SA_EINVAL, "tensor not found: model.embed_tokens.weight");
     if (embed->shape.size() != 2) return fail(SA_EINVAL, "model.embed_tokens.weight must be 2-D");
     const int n_layers = ck.num_layers();
     if (n_layers <= 0) return fail(SA_EINVAL, "no model.layers.* tensors");
-    const Entry* qn = ck.find(layer_name(0, "self_attn.q_norm.weight"));
-    const Entry* qp = ck.find(layer_name(0, "self_attn.q_proj.weight"));
-    const Entry* kp = ck.find(layer_name(0, "self_attn.k_proj.weight"));
-    const Entry* gp = ck.find(layer_name(0, "mlp.gate_proj.weight"));
+    const Entry* qn = ck.find(layer_tensor_name(0, "self_attn.q_norm.weight"));
+    const Entry* qp = ck.find(layer_tensor_name(0, "self_attn.q_proj.weight"));
+    const Entry* kp = ck.find(layer_tensor_name(0, "self_attn.k_proj.weight"));
+    const Entry* gp = ck.find(layer_tensor_name(0, "mlp.gate_proj.weight"));
     if (!qn || !qp || !kp || !gp) return fail(SA_EINVAL, "layer 0 lacks q_norm, q_proj, k_proj or gate_proj");
     if (qn->shape.size() != 1 || qp->shape.size() != 2 || kp->shape.size() != 2 || gp->shape.size() != 2)
         return fail(SA_EINVAL, "layer 0 tensors have unexpected ranks");
@@ -361,6 +358,8 @@ sa_status read_desc(const Checkpoint& ck, sa_qwen3_desc* d) {
     *d = r;
     return SA_OK;
 }
+
+namespace {
 
 uint16_t f32_to_bf16_rne(float f) {
     uint32_t u;
@@ -400,12 +399,7 @@ sa_status upload(sa_qwen3* model, int layer, sa_qwen3_tensor which, size_t off, 
             SA_HIP_TRY(hipMemcpy(dst, src, n * 4, hipMemcpyHostToDevice));
         } else {
             std::vector<float> h(n);
-            for (size_t i = 0; i < n; ++i) {
-                uint16_t b;
-                std::memcpy(&b, src + 2 * i, 2);
-                const uint32_t u = static_cast<uint32_t>(b) << 16;
-                std::memcpy(&h[i], &u, 4);
-            }
+            ck.to_f32(t, h.data());
             SA_HIP_TRY(hipMemcpy(dst, h.data(), n * 4, hipMemcpyHostToDevice));
         }
     }
@@ -423,7 +417,7 @@ extern "C" sa_status sa_qwen3_desc_from_safetensors(const char* path, sa_qwen3_d
     Checkpoint ck;
     sa_status s = ck.open_file(path);
     if (s != SA_OK) return s;
-    return read_desc(ck, desc);
+    return read_qwen3_desc(ck, desc);
 }
 
 extern "C" sa_status sa_qwen3_load_safetensors(sa_qwen3* model, const char* path) {
@@ -435,7 +429,7 @@ extern "C" sa_status sa_qwen3_load_safetensors(sa_qwen3* model, const char* path
     Checkpoint ck;
     if ((s = ck.open_file(path)) != SA_OK) return s;
     sa_qwen3_desc fd{};
-    if ((s = read_desc(ck, &fd)) != SA_OK) return s;
+    if ((s = read_qwen3_desc(ck, &fd)) != SA_OK) return s;
     if (fd.num_layers != md.num_layers || fd.hidden != md.hidden || fd.intermediate != md.intermediate ||
         fd.vocab != md.vocab || fd.n_q_heads != md.n_q_heads || fd.n_kv_heads != md.n_kv_heads ||
         fd.head_dim != md.head_dim)
@@ -461,17 +455,17 @@ extern "C" sa_status sa_qwen3_load_safetensors(sa_qwen3* model, const char* path
         if ((s = put(0, SA_QW_LM_HEAD, 0, "model.embed_tokens.weight", {V, H})) != SA_OK) return s;
     }
     for (int l = 0; l < md.num_layers; ++l) {
-        if ((s = put(l, SA_QW_IN_NORM, 0, layer_name(l, "input_layernorm.weight"), {H})) != SA_OK ||
-            (s = put(l, SA_QW_POST_NORM, 0, layer_name(l, "post_attention_layernorm.weight"), {H})) != SA_OK ||
-            (s = put(l, SA_QW_QKV, 0, layer_name(l, "self_attn.q_proj.weight"), {Nq, H})) != SA_OK ||
-            (s = put(l, SA_QW_QKV, Nq * H, layer_name(l, "self_attn.k_proj.weight"), {Nk, H})) != SA_OK ||
-            (s = put(l, SA_QW_QKV, (Nq + Nk) * H, layer_name(l, "self_attn.v_proj.weight"), {Nk, H})) != SA_OK ||
-            (s = put(l, SA_QW_Q_NORM, 0, layer_name(l, "self_attn.q_norm.weight"), {D})) != SA_OK ||
-            (s = put(l, SA_QW_K_NORM, 0, layer_name(l, "self_attn.k_norm.weight"), {D})) != SA_OK ||
-            (s = put(l, SA_QW_O, 0, layer_name(l, "self_attn.o_proj.weight"), {H, Nq})) != SA_OK ||
-            (s = put(l, SA_QW_GATE_UP, 0, layer_name(l, "mlp.gate_proj.weight"), {I, H})) != SA_OK ||
-            (s = put(l, SA_QW_GATE_UP, I * H, layer_name(l, "mlp.up_proj.weight"), {I, H})) != SA_OK ||
-            (s = put(l, SA_QW_DOWN, 0, layer_name(l, "mlp.down_proj.weight"), {H, I})) != SA_OK)
+        if ((s = put(l, SA_QW_IN_NORM, 0, layer_tensor_name(l, "input_layernorm.weight"), {H})) != SA_OK ||
+            (s = put(l, SA_QW_POST_NORM, 0, layer_tensor_name(l, "post_attention_layernorm.weight"), {H})) != SA_OK ||
+            (s = put(l, SA_QW_QKV, 0, layer_tensor_name(l, "self_attn.q_proj.weight"), {Nq, H})) != SA_OK ||
+            (s = put(l, SA_QW_QKV, Nq * H, layer_tensor_name(l, "self_attn.k_proj.weight"), {Nk, H})) != SA_OK ||
+            (s = put(l, SA_QW_QKV, (Nq + Nk) * H, layer_tensor_name(l, "self_attn.v_proj.weight"), {Nk, H})) != SA_OK ||
+            (s = put(l, SA_QW_Q_NORM, 0, layer_tensor_name(l, "self_attn.q_norm.weight"), {D})) != SA_OK ||
+            (s = put(l, SA_QW_K_NORM, 0, layer_tensor_name(l, "self_attn.k_norm.weight"), {D})) != SA_OK ||
+            (s = put(l, SA_QW_O, 0, layer_tensor_name(l, "self_attn.o_proj.weight"), {H, Nq})) != SA_OK ||
+            (s = put(l, SA_QW_GATE_UP, 0, layer_tensor_name(l, "mlp.gate_proj.weight"), {I, H})) != SA_OK ||
+            (s = put(l, SA_QW_GATE_UP, I * H, layer_tensor_name(l, "mlp.up_proj.weight"), {I, H})) != SA_OK ||
+            (s = put(l, SA_QW_DOWN, 0, layer_tensor_name(l, "mlp.down_proj.weight"), {H, I})) != SA_OK)
             return s;
     }
     return SA_OK;

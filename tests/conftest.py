@@ -30,6 +30,14 @@ def ref():
 
 
 @pytest.fixture(scope="session")
+def ref_opt():
+    """The compiled reference where oracle/_ref is built, else None (for tests
+    whose other checks stand without it)."""
+    from oracle import Reference
+    return Reference() if Reference.available() else None
+
+
+@pytest.fixture(scope="session")
 def synth():
     from util import load_synth
     return load_synth()

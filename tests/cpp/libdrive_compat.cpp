@@ -3,13 +3,16 @@
 // exactly as oracle/ref_shim.cpp drives the reference, behind the same plain
 // array arguments, so tests can put the GPU results beside the reference's
 // golden vectors.  Built as tests/cpp/bin/libdrive_compat.so.
+#include <cstdint>
 #include <cstring>
 #include <exception>
+#include <stdexcept>
 #include <string>
 #include <vector>
 
 #include "tensor_cpp/kv_cache.h"
 #include "tensor_cpp/ops.h"
+#include "tensor_cpp/qwen3_loader.h"
 #include "tensor_cpp/qwen3_ops.h"
 #include "tensor_cpp/qwen3_ops_avx.h"
 
@@ -29,6 +32,17 @@ Tensor make(const float* p, std::vector<size_t> dims) {
 
 int failed(const std::exception& e) {
     g_error = e.what();
+    return -1;
+}
+
+// "E:" + what() with E the exception's kind: I invalid_argument, O out_of_range,
+// R runtime_error (other than those), X anything else.
+int failed_kind(const std::exception& e) {
+    const char* k = dynamic_cast<const std::invalid_argument*>(&e) ? "I:"
+                    : dynamic_cast<const std::out_of_range*>(&e)   ? "O:"
+                    : dynamic_cast<const std::runtime_error*>(&e)  ? "R:"
+                                                                   : "X:";
+    g_error = std::string(k) + e.what();
     return -1;
 }
 
@@ -205,6 +219,97 @@ int drv_qwen3_forward_nocache(int nl, int H, int I, int V, int Hq, int Hkv, int 
         return 0;
     } catch (const std::exception& e) {
         return failed(e);
+    }
+}
+
+// load_qwen3_weights(path).  meta[7] receives num_layers, heads, kv heads,
+// head_dim, hidden, vocab and the float count of the flat copy; when out is
+// non-null and cap covers that count, out receives embed_tokens, norm_weight,
+// lm_head, then per layer input_layernorm, post_attention_layernorm,
+// qkv_projs, q_proj, k_proj, v_proj, q_norm, k_norm, o_proj, gate_proj,
+// up_proj, down_proj, each row-major.  Returns 0, or -1 with the exception's
+// kind and text in drv_last_error.
+int drv_load_weights(const char* path, int64_t* meta, float* out, int64_t cap) {
+    try {
+        const q3::Qwen3Weights w = q3::load_qwen3_weights(path);
+        std::vector<const Tensor*> parts = {&w.embed_tokens, &w.norm_weight, &w.lm_head};
+        for (const auto& L : w.layers)
+            for (const Tensor* t : {&L.input_layernorm_weight, &L.post_attention_layernorm_weight, &L.qkv_projs,
+                                    &L.q_proj, &L.k_proj, &L.v_proj, &L.q_norm_weight, &L.k_norm_weight, &L.o_proj,
+                                    &L.gate_proj, &L.up_proj, &L.down_proj})
+                parts.push_back(t);
+        int64_t total = 0;
+        for (const Tensor* t : parts) total += (int64_t)t->size();
+        const int64_t m[7] = {(int64_t)w.num_layers, (int64_t)w.num_attention_heads, (int64_t)w.num_key_value_heads,
+                              (int64_t)w.head_dim, (int64_t)w.hidden_size, (int64_t)w.vocab_size, total};
+        std::memcpy(meta, m, sizeof(m));
+        if (out && cap >= total)
+            for (const Tensor* t : parts) {
+                std::memcpy(out, t->data(), t->size() * sizeof(float));
+                out += t->size();
+            }
+        return 0;
+    } catch (const std::exception& e) {
+        return failed_kind(e);
+    }
+}
+
+// test_qwen3_forward(path, tokens [B][N]) -> hidden [B][N][hidden].
+int drv_test_forward(const char* path, const int* tokens, int B, int N, float* hidden, int64_t cap) {
+    try {
+        std::vector<long> ids((size_t)B * N);
+        for (size_t i = 0; i < ids.size(); ++i) ids[i] = tokens[i];
+        const Tensor h = q3::test_qwen3_forward(path, ids, {(size_t)B, (size_t)N});
+        if ((int64_t)h.size() > cap) throw std::length_error("hidden buffer too small");
+        std::memcpy(hidden, h.data(), h.size() * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) {
+        return failed_kind(e);
+    }
+}
+
+// ops::RotaryEmbedding(D, max_seq, theta).apply(x [B][S][H][D], seq_len).
+int drv_rotary(const float* x, int B, int S, int H, int D, int max_seq, float theta, int seq_len, float* out) {
+    try {
+        tensor_cpp::ops::RotaryEmbedding rope((size_t)D, (size_t)max_seq, theta);
+        const Tensor y = rope.apply(make(x, {(size_t)B, (size_t)S, (size_t)H, (size_t)D}), (size_t)seq_len);
+        std::memcpy(out, y.data(), y.size() * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) {
+        return failed_kind(e);
+    }
+}
+
+// ops::argmax, the arguments and results of ref_argmax in oracle/ref_shim.cpp.
+long drv_argmax(const float* x, const int64_t* dims, int nd, int dim, int keepdim, int64_t* idx, long cap,
+                int64_t* shape_out, int* out_nd) {
+    try {
+        const TensorL r = tensor_cpp::ops::argmax(make(x, std::vector<size_t>(dims, dims + nd)), dim, keepdim != 0);
+        const long count = (long)r.size();
+        for (long i = 0; i < count && i < cap; ++i) idx[i] = r[i];
+        *out_nd = (int)r.shape().ndim();
+        for (int i = 0; i < *out_nd && i < 8; ++i) shape_out[i] = (int64_t)r.shape()[i];
+        return count;
+    } catch (const std::exception& e) {
+        return failed_kind(e);
+    }
+}
+
+// ops::cross_attention(q [B][Hq][Sq][D], k/v [B][Hkv][Sk][D], mask, scale);
+// mask [Sq][Sk] or null.
+int drv_cross_attention(const float* q, const float* k, const float* v, int B, int Hq, int Hkv, int Sq, int Sk, int D,
+                        float scale, const float* mask, float* out) {
+    try {
+        const Tensor tq = make(q, {(size_t)B, (size_t)Hq, (size_t)Sq, (size_t)D});
+        const Tensor tk = make(k, {(size_t)B, (size_t)Hkv, (size_t)Sk, (size_t)D});
+        const Tensor tv = make(v, {(size_t)B, (size_t)Hkv, (size_t)Sk, (size_t)D});
+        Tensor tm;
+        if (mask) tm = make(mask, {(size_t)Sq, (size_t)Sk});
+        const Tensor y = tensor_cpp::ops::cross_attention(tq, tk, tv, mask ? &tm : nullptr, scale);
+        std::memcpy(out, y.data(), y.size() * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) {
+        return failed_kind(e);
     }
 }
 

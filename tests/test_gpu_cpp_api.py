@@ -1,9 +1,9 @@
 """GPU: the C++ mirror of the reference API (attention.h, KVCache, ops,
 qwen3 attention path), exercised by tests/cpp/test_compat.cpp against the
-oracle (one PASS/FAIL line per check), and the reference's own attention
-unit test (tensor_cpp/tests/unit/test_streaming_attention.cpp), compiled
-unchanged against include/ and linked to the library by oracle/Makefile
-(ref-on-lib), run on the GPU kernels."""
+oracle (one PASS/FAIL line per check), and three of the reference's own unit
+tests (tensor_cpp/tests/unit/test_streaming_attention.cpp, test_ops.cpp,
+test_avx_ops.cpp), compiled unchanged against include/ and linked to the
+library by oracle/Makefile (ref-on-lib), run on the GPU kernels."""
 from __future__ import annotations
 
 import subprocess
@@ -14,7 +14,8 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 EXE = Path(__file__).resolve().parent / "cpp" / "bin" / "test_compat"
-REF_TEST = Path(__file__).resolve().parents[1] / "oracle" / "_ref" / "test_streaming_attention_on_sa_amd"
+REF_BIN = Path(__file__).resolve().parents[1] / "oracle" / "_ref"
+REF_TEST = REF_BIN / "test_streaming_attention_on_sa_amd"
 
 
 def test_cpp_api_mirror():
@@ -36,3 +37,30 @@ def test_reference_unit_test_on_the_gpu():
     print(r.stdout[-4000:])
     assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
     assert r.stdout.count("Status: OK") == 4
+
+
+def _run_reference_program(name, tmp_path):
+    exe = REF_BIN / f"{name}_on_sa_amd"
+    if not exe.exists():
+        pytest.skip("built only where the reference sources are mounted (make -C oracle ref-on-lib)")
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=600, cwd=tmp_path)
+    print(r.stdout[-4000:])
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    return r.stdout
+
+
+def test_reference_ops_unit_test_on_the_gpu(tmp_path):
+    """The reference's operator suite (add, argmax, embedding, linear, rms_norm,
+    RotaryEmbedding, swiglu, self_attention, Tensor matmul): every case must
+    report PASSED and none ERROR."""
+    out = _run_reference_program("test_ops", tmp_path)
+    assert "All tests PASSED" in out and "ERROR" not in out
+    assert "Failed: 0" in out
+
+
+def test_reference_avx_ops_unit_test_on_the_gpu(tmp_path):
+    """The reference's checks of matmul_avx (relative 1e-3 against a scalar
+    product), dot_avx (1e-4), add_avx (1e-6) and rms_norm_avx (1e-5 against
+    ops::rms_norm), all four through the library."""
+    out = _run_reference_program("test_avx_ops", tmp_path)
+    assert out.count("Status: PASSED") == 4 and "FAILED" not in out

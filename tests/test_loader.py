@@ -126,3 +126,93 @@ def test_desc_missing_tensor(tmp_path, synth):
     st, _, pkg = _desc(None, path)
     assert st == pkg.SA_EINVAL
     assert b"q_norm" in pkg.lib().sa_last_error()
+
+
+# --- load_qwen3_weights of include/tensor_cpp/qwen3_loader.h (host tensors) ---
+
+DRIVER = __import__("pathlib").Path(__file__).resolve().parent / "cpp" / "bin" / "libdrive_compat.so"
+
+
+@pytest.fixture(scope="module")
+def drv():
+    if not DRIVER.exists():
+        pytest.fail("driver missing: python streaming-attention_amd/build.py --tests")
+    lib = C.CDLL(str(DRIVER))
+    lib.drv_last_error.restype = C.c_char_p
+    lib.drv_load_weights.argtypes = [C.c_char_p, C.c_void_p, C.c_void_p, C.c_int64]
+    lib.drv_load_weights.restype = C.c_int
+    return lib
+
+
+def load_mirror(drv, path):
+    """(meta [7], flat fp32 weights) from the mirror's load_qwen3_weights, or
+    raises RuntimeError with the exception's kind and text."""
+    meta = np.zeros(7, np.int64)
+    if drv.drv_load_weights(str(path).encode(), meta.ctypes.data, None, 0) != 0:
+        raise RuntimeError(drv.drv_last_error().decode())
+    out = np.empty(int(meta[6]), np.float32)
+    assert drv.drv_load_weights(str(path).encode(), meta.ctypes.data, out.ctypes.data, out.size) == 0
+    return meta, out
+
+
+def flat_expected(w, cfg, tie):
+    """The flat layout of drv_load_weights / ref_load_weights from the weights dict."""
+    Hq, Hkv, D, I = cfg["n_q_heads"], cfg["n_kv_heads"], cfg["head_dim"], cfg["intermediate"]
+    parts = [w["embed"], w["final_norm"], w["embed"] if tie else w["lm_head"]]
+    for L in w["layers"]:
+        q, k, v = np.split(L["qkv"], [Hq * D, (Hq + Hkv) * D])
+        parts += [L["in_norm"], L["post_norm"], L["qkv"], q, k, v, L["q_norm"], L["k_norm"], L["o"],
+                  L["gate_up"][:I], L["gate_up"][I:], L["down"]]
+    return np.concatenate([np.asarray(p, np.float32).ravel() for p in parts])
+
+
+def test_mirror_loader_equals_reference_loader(drv, ref, ref_ckpt):
+    """On the reference's model shape (28 layers, 16/8 heads of 128, BF16) the
+    mirror's load_qwen3_weights returns, bit for bit, the tensors and config
+    the reference's own loader returns."""
+    path, w = ref_ckpt
+    meta_ref, flat_ref = ref.load_weights(path)
+    meta, flat = load_mirror(drv, path)
+    assert meta.tolist() == meta_ref.tolist()
+    assert np.array_equal(flat.view(np.uint32), flat_ref.view(np.uint32))
+    assert np.array_equal(flat, flat_expected(w, REF_CFG, tie=False))
+
+
+@pytest.mark.parametrize("dtype,tie", [("BF16", False), ("F32", True), ("F32", False)])
+def test_mirror_loader_reads_any_shape(drv, tmp_path, synth, dtype, tie):
+    """GQA 8/2, head_dim 64, three layers, F32 or BF16, tied or separate lm_head:
+    the shape comes from the file, F32 values arrive unrounded, a tied
+    checkpoint gets the embedding as lm_head."""
+    from oracle.qwen3_model import synth_weights
+    cfg = dict(num_layers=3, hidden=128, intermediate=96, vocab=192, n_q_heads=8, n_kv_heads=2, head_dim=64,
+               rms_eps=1e-6, rope_theta=1e6)
+    w = synth_weights(synth, cfg, seed=5, std=0.1)
+    if dtype == "BF16":
+        w = ck.bf16_exact(w)
+    path = tmp_path / "m.safetensors"
+    ck.write(path, w, cfg, dtype=dtype, tie=tie)
+    meta, flat = load_mirror(drv, path)
+    assert meta[:6].tolist() == [3, 8, 2, 64, 128, 192]
+    assert np.array_equal(flat, flat_expected(w, cfg, tie))
+
+
+def test_mirror_loader_errors(drv, tmp_path, synth):
+    """The reference's messages for a file it cannot open and a missing tensor
+    (std::runtime_error both); a wrong shape names the tensor."""
+    from oracle.qwen3_model import synth_weights
+    cfg = dict(num_layers=2, hidden=64, intermediate=64, vocab=96, n_q_heads=4, n_kv_heads=2, head_dim=64,
+               rms_eps=1e-6, rope_theta=1e6)
+    w = synth_weights(synth, cfg, seed=6, std=0.1)
+    with pytest.raises(RuntimeError, match=r"^R:Failed to open safetensors file: .*nope\.safetensors"):
+        load_mirror(drv, tmp_path / "nope.safetensors")
+    ck.write(tmp_path / "a.safetensors", w, cfg, drop=("model.layers.1.mlp.up_proj.weight",))
+    with pytest.raises(RuntimeError, match=r"^R:Tensor not found: model\.layers\.1\.mlp\.up_proj\.weight$"):
+        load_mirror(drv, tmp_path / "a.safetensors")
+    ck.write(tmp_path / "b.safetensors", w, cfg, drop=("model.norm.weight",))
+    with pytest.raises(RuntimeError, match=r"^R:Tensor not found: model\.norm\.weight$"):
+        load_mirror(drv, tmp_path / "b.safetensors")
+    bad = dict(w, layers=[dict(L) for L in w["layers"]])
+    bad["layers"][1]["down"] = bad["layers"][1]["down"][:, :32]
+    ck.write(tmp_path / "c.safetensors", bad, cfg)
+    with pytest.raises(RuntimeError, match=r"^R:model\.layers\.1\.mlp\.down_proj\.weight: shape"):
+        load_mirror(drv, tmp_path / "c.safetensors")
