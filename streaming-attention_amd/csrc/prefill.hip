@@ -21,7 +21,9 @@
 // rescales its accumulators only when some score exceeds the current max by
 // more than 2^8, and then after the PV product (exact), so the common tile
 // has no branch between softmax and PV.  P is rounded to bf16 for the PV
-// product; the row sums use the fp32 p.
+// product; the row sums use the fp32 p.  Prompts too short to give every CU
+// a workgroup run 32-query workgroups that split each key range between two
+// wave groups and merge the halves in LDS.
 //
 // fp32 inputs (v_mfma_f32_16x16x4f32): a wave owns 32 queries as two
 // 16-query blocks, a workgroup 128 queries, eager rescale.
@@ -423,141 +425,105 @@ prefill_bf16_kernel(PrefillArgs pa) {
 // Measured at L = 8192 (16/8 heads, same box, interleaved): 251 us against
 // 258-264 us for the same schedule with a per-tile row max, a scaled fma per
 // score and fp32 row sums (34 VALU per half-tile instead of about 75).
-template <int W, int NS>
-__global__ void __launch_bounds__(W * 64)
-prefill_bf16_fold_kernel(PrefillArgs pa) {
-    constexpr int NKS = 8;          // k-steps of the score product
-    constexpr int NDB = 4;          // 32-row d blocks of O^T
-    constexpr int NI = 16 / W;      // loads per wave, tensor and tile (64 lanes x 16 bytes each)
-    extern __shared__ __align__(16) unsigned char smem[];
-    lds_u8_t* const lsm = (lds_u8_t*)smem;
-
-    const int L = pa.L;
-    const Work wk = map_work(pa, blockIdx.x);
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int n = lane & 31;
-    const int hh = lane >> 5;
-
-    const int wph = W / pa.gh;
-    const int qtile = wph * 32;
-    const int h = wk.h0 + wave / wph;
-    const uint16_t* Q = static_cast<const uint16_t*>(pa.q) + wk.b * pa.qs[0] + h * pa.qs[1];
-    const uint16_t* K = static_cast<const uint16_t*>(pa.k) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
-    const uint16_t* V = static_cast<const uint16_t*>(pa.v) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
-    const int kv_row = static_cast<int>(pa.kvs[2]);
-
-    const int q_wave0 = wk.qt * qtile + (wave % wph) * 32;
-    const int n_kt = (min(L, (wk.qt + 1) * qtile) - 1) / kKTile + 1;
-    const int wave_kt = q_wave0 < L ? (q_wave0 + 31) / kKTile + 1 : 0;
-
-    int d_row[NI], d_col[NI];
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-        const int r = 4 * (wave * NI + i) + lane / 16;
-        d_row[i] = r;
-        d_col[i] = 8 * ((lane % 16) ^ dma_swz(r & 15));
-    }
-    auto dma_tile = [&](int kt, int stage) {
-        const int key0 = kt * kKTile;
-        lds_u8_t* sb = lsm + stage * kDmaStageBytes;
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const long long e = (long long)min(key0 + d_row[i], L - 1) * kv_row + d_col[i];
-            lds_u8_t* dst = sb + (wave * NI + i) * 1024;
-            dma16(K + e, dst);
-            dma16(V + e, dst + kDmaTileBytes);
-        }
-    };
-#pragma unroll
-    for (int s = 0; s < (W == 8 ? NS : NS - 1); ++s) dma_tile(s, s);
-
-    // q' = bf16(q * scale * log2 e): the scores come out in the log2 domain.
+// One wave's share of the folded-softmax kernels: the scores of its 32
+// queries against the 32-key halves of a K/V tile staged in LDS (K rows
+// permuted by dma_swz, V^T read with ds_read_b64_tr_b16), the folded softmax
+// with its lazy raise of the running max, and the O^T accumulators.
+struct FoldWave {
+    static constexpr int NKS = 8;   // k-steps of the score product
+    static constexpr int NDB = 4;   // 32-row d blocks of O^T
+    int n, hh;                      // this lane's query column in the wave's block, and its half
+    int q0;                         // the wave's first query
     bf16x8_t qf[NKS];
-    {
-        const float sq = pa.scale * kLog2eP;
-        const int qi = min(q_wave0 + n, L - 1);
-        const uint16_t* qrow = Q + qi * pa.qs[2] + 8 * hh;
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-            const u32x4_t raw = *reinterpret_cast<const u32x4_t*>(qrow + ks * 16);
-            float x[8];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                x[2 * i] = bf16_lo(raw[i]) * sq;
-                x[2 * i + 1] = bf16_hi(raw[i]) * sq;
-            }
-            qf[ks] = pack_bf16x8(x);
-        }
-    }
     f32x16_t acc[NDB];
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) acc[db] = f32x16_t{};
-    float ms = -INFINITY;      // running max of this query (log2 domain) at the last raise
-    float lp = 0.f;            // this lane's part of the row sum
-    float cap = -1.f;          // kSumCap once ms is finite: the first tile always raises
-    f32x16_t negm = {};        // -ms in every element (0 while ms = -inf): the score chain's start
-
+    float ms;                       // running max of this query (log2 domain) at the last raise
+    float lp;                       // this lane's part of the row sum
+    float cap;                      // kSumCap once ms is finite: the first tile always raises
+    f32x16_t negm;                  // -ms in every element (0 while ms = -inf): the score chain's start
     int k_off[NKS];
-    {
-        const int r = swap_bits23(n);
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) k_off[ks] = r * kDmaRowBytes + (((2 * ks + hh) ^ dma_swz(r & 15)) << 4);
-    }
     int v_off[2][NDB];
-    {
-        const int g = lane >> 4, j = lane & 15;
+
+    // q' = bf16(q * scale * log2 e) for query q_first + n (clamped to the
+    // sequence) of the head whose rows start at Q with row stride q_row; the
+    // scores then come out in the log2 domain.
+    __device__ __forceinline__ void init(const uint16_t* Q, long long q_row, int q_first, int L, float scale,
+                                         int lane) {
+        n = lane & 31;
+        hh = lane >> 5;
+        q0 = q_first;
+        {
+            const float sq = scale * kLog2eP;
+            const int qi = min(q0 + n, L - 1);
+            const uint16_t* qrow = Q + qi * q_row + 8 * hh;
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int r = 8 * hh + 4 * u + j / 4;
+            for (int ks = 0; ks < NKS; ++ks) {
+                const u32x4_t raw = *reinterpret_cast<const u32x4_t*>(qrow + ks * 16);
+                float x[8];
 #pragma unroll
-            for (int db = 0; db < NDB; ++db) {
-                const int col = 32 * db + 16 * (g & 1) + 4 * (j & 3);
-                v_off[u][db] = kDmaTileBytes + r * kDmaRowBytes + (((col >> 3) ^ dma_swz(r & 15)) << 4) + (col & 7) * 2;
+                for (int i = 0; i < 4; ++i) {
+                    x[2 * i] = bf16_lo(raw[i]) * sq;
+                    x[2 * i + 1] = bf16_hi(raw[i]) * sq;
+                }
+                qf[ks] = pack_bf16x8(x);
+            }
+        }
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) acc[db] = f32x16_t{};
+        ms = -INFINITY;
+        lp = 0.f;
+        cap = -1.f;
+        negm = f32x16_t{};
+        {
+            const int r = swap_bits23(n);
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) k_off[ks] = r * kDmaRowBytes + (((2 * ks + hh) ^ dma_swz(r & 15)) << 4);
+        }
+        {
+            const int g = lane >> 4, j = lane & 15;
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int r = 8 * hh + 4 * u + j / 4;
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) {
+                    const int col = 32 * db + 16 * (g & 1) + 4 * (j & 3);
+                    v_off[u][db] =
+                        kDmaTileBytes + r * kDmaRowBytes + (((col >> 3) ^ dma_swz(r & 15)) << 4) + (col & 7) * 2;
+                }
             }
         }
     }
-    auto lds_k = [&](const lds_u8_t* sb, int kb, int ks) {
+
+    __device__ __forceinline__ bf16x8_t lds_k(const lds_u8_t* sb, int kb, int ks) const {
         return *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(sb + kb * 32 * kDmaRowBytes +
                                                                                      k_off[ks]);
-    };
-    auto lds_vt = [&](const lds_u8_t* sb, int kb, int t, int db) {
+    }
+    __device__ __forceinline__ bf16x8_t lds_vt(const lds_u8_t* sb, int kb, int t, int db) const {
         const lds_u8_t* p = sb + (kb * 32 + t * 16) * kDmaRowBytes;
         const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(p + v_off[0][db]));
         const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(p + v_off[1][db]));
         return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-    };
-
-    constexpr int VM = (NS - 2) * 2 * NI;
-    static_assert(VM == 0 || VM == 4 || VM == 8, "vmcnt literal");
-    auto next_tile_ready = [&]() {
-        if constexpr (VM == 0) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        else if constexpr (VM == 4) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        else asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    };
-    if constexpr (W == 8) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else next_tile_ready();   // tile 0
+    }
 
     // Scores of one 32-key half, biased by -m: element j is key 16 (j/8) +
-    // 8 hh + j%8 of the half for query q_wave0 + n.
-    auto scores = [&](const bf16x8_t (&kf)[NKS]) {
+    // 8 hh + j%8 of the half for query q0 + n.
+    __device__ __forceinline__ f32x16_t scores(const bf16x8_t (&kf)[NKS]) const {
         f32x16_t s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0], qf[0], negm, 0, 0, 0);
 #pragma unroll
         for (int ks = 1; ks < NKS; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qf[ks], s, 0, 0, 0);
         return s;
-    };
+    }
     // P = 2^s as the PV product's B operand, and this lane's sum of it.
-    auto softmax = [&](const f32x16_t& s, bf16x8_t (&pb)[2]) {
+    __device__ __forceinline__ static float softmax(const f32x16_t& s, bf16x8_t (&pb)[2]) {
         float p[16];
 #pragma unroll
         for (int j = 0; j < 16; ++j) p[j] = __builtin_amdgcn_exp2f(s[j]);
         pb[0] = pack_bf16x8(p);
         pb[1] = pack_bf16x8(p + 8);
         return sum_bf16x8(pb[1], sum_bf16x8(pb[0], 0.f));
-    };
+    }
     // Raise m to the row max of this half when the sum left the cap (or m is
     // still -inf): O and the row sum are rescaled and P recomputed.
-    auto settle = [&](const f32x16_t& s, bf16x8_t (&pb)[2], float& rs) {
+    __device__ __forceinline__ void settle(const f32x16_t& s, bf16x8_t (&pb)[2], float& rs) {
         if (!__any(!(rs <= cap))) return;
         float mt = s[0];
 #pragma unroll
@@ -582,12 +548,18 @@ prefill_bf16_fold_kernel(PrefillArgs pa) {
         cap = m_new == -INFINITY ? -1.f : kSumCap;
 #pragma unroll
         for (int j = 0; j < 16; ++j) negm[j] = b_new;
-    };
+    }
+    __device__ __forceinline__ void pv(const bf16x8_t (&vf)[NDB][2], const bf16x8_t (&pb)[2]) {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][t], pb[t], acc[db], 0, 0, 0);
+    }
 
-    // One tile from stage sb (W = 4, leftover tiles and the diagonal): per
-    // 32-key half, scores, mask, P, settle, PV.
-    auto tile = [&](int kt, const lds_u8_t* sb, auto diag_tag) {
-        constexpr bool DIAG = decltype(diag_tag)::value;
+    // Tile kt (keys 64 kt ..) from LDS stage sb, per 32-key half: scores,
+    // mask (the diagonal tile only), P, settle, PV.
+    template <bool DIAG>
+    __device__ __forceinline__ void tile(int kt, const lds_u8_t* sb) {
         bf16x8_t kf[NKS];
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) kf[ks] = lds_k(sb, 0, ks);
@@ -597,7 +569,7 @@ prefill_bf16_fold_kernel(PrefillArgs pa) {
             if constexpr (DIAG) {
 #pragma unroll
                 for (int j = 0; j < 16; ++j)
-                    if (kt * kKTile + 32 * kb + 16 * (j / 8) + 8 * hh + (j % 8) > q_wave0 + n) s[j] = -INFINITY;
+                    if (kt * kKTile + 32 * kb + 16 * (j / 8) + 8 * hh + (j % 8) > q0 + n) s[j] = -INFINITY;
             }
             bf16x8_t vf[NDB][2];
 #pragma unroll
@@ -612,13 +584,101 @@ prefill_bf16_fold_kernel(PrefillArgs pa) {
 #pragma unroll
                 for (int ks = 0; ks < NKS; ++ks) kf[ks] = lds_k(sb, 1, ks);
             }
-#pragma unroll
-            for (int db = 0; db < NDB; ++db)
-#pragma unroll
-                for (int t = 0; t < 2; ++t)
-                    acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[db][t], pb[t], acc[db], 0, 0, 0);
+            pv(vf, pb);
         }
+    }
+
+    // O / l for query q0 + n (when inside the sequence), row-major from orow0
+    // (the head's first output row) with row stride o_row.
+    __device__ __forceinline__ void store(float* orow0, long long o_row, int L) const {
+        const float l = lp + __shfl_xor(lp, 32, 64);
+        const int qi = q0 + n;
+        if (qi >= L) return;
+        const float inv = 1.0f / l;
+        float* orow = orow0 + qi * o_row + 4 * hh;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+                *reinterpret_cast<float4*>(orow + 32 * db + 8 * jj) =
+                    make_float4(acc[db][4 * jj] * inv, acc[db][4 * jj + 1] * inv, acc[db][4 * jj + 2] * inv,
+                                acc[db][4 * jj + 3] * inv);
+    }
+};
+
+// Per-lane rows and columns of the tile loads of a W-wave workgroup: load i
+// of a wave copies 4 rows x 256 bytes (16 lanes per row), 16 / W loads per
+// wave cover a 64-row tile.
+template <int W>
+struct DmaMap {
+    static constexpr int NI = 16 / W;
+    int row[NI], col[NI];
+    __device__ __forceinline__ DmaMap(int wave, int lane) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int r = 4 * (wave * NI + i) + lane / 16;
+            row[i] = r;
+            col[i] = 8 * ((lane % 16) ^ dma_swz(r & 15));
+        }
+    }
+    // K and V rows key0 .. key0 + 63 (clamped to the sequence) into the tile
+    // slot sb: K at sb, V at sb + kDmaTileBytes.
+    __device__ __forceinline__ void load(const uint16_t* K, const uint16_t* V, int kv_row, int key0, int L,
+                                         int wave, lds_u8_t* sb) const {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const long long e = (long long)min(key0 + row[i], L - 1) * kv_row + col[i];
+            lds_u8_t* dst = sb + (wave * NI + i) * 1024;
+            dma16(K + e, dst);
+            dma16(V + e, dst + kDmaTileBytes);
+        }
+    }
+};
+
+template <int W, int NS>
+__global__ void __launch_bounds__(W * 64)
+prefill_bf16_fold_kernel(PrefillArgs pa) {
+    constexpr int NDB = FoldWave::NDB;
+    constexpr int NI = DmaMap<W>::NI;   // loads per wave, tensor and tile (64 lanes x 16 bytes each)
+    extern __shared__ __align__(16) unsigned char smem[];
+    lds_u8_t* const lsm = (lds_u8_t*)smem;
+
+    const int L = pa.L;
+    const Work wk = map_work(pa, blockIdx.x);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
+    const int wph = W / pa.gh;
+    const int qtile = wph * 32;
+    const int h = wk.h0 + wave / wph;
+    const uint16_t* Q = static_cast<const uint16_t*>(pa.q) + wk.b * pa.qs[0] + h * pa.qs[1];
+    const uint16_t* K = static_cast<const uint16_t*>(pa.k) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
+    const uint16_t* V = static_cast<const uint16_t*>(pa.v) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
+    const int kv_row = static_cast<int>(pa.kvs[2]);
+
+    const int q_wave0 = wk.qt * qtile + (wave % wph) * 32;
+    const int n_kt = (min(L, (wk.qt + 1) * qtile) - 1) / kKTile + 1;
+    const int wave_kt = q_wave0 < L ? (q_wave0 + 31) / kKTile + 1 : 0;
+
+    const DmaMap<W> dm(wave, lane);
+    auto dma_tile = [&](int kt, int stage) {
+        dm.load(K, V, kv_row, kt * kKTile, L, wave, lsm + stage * kDmaStageBytes);
     };
+#pragma unroll
+    for (int s = 0; s < (W == 8 ? NS : NS - 1); ++s) dma_tile(s, s);
+
+    FoldWave fw;
+    fw.init(Q, pa.qs[2], q_wave0, L, pa.scale, lane);
+
+    constexpr int VM = (NS - 2) * 2 * NI;
+    static_assert(VM == 0 || VM == 4 || VM == 8, "vmcnt literal");
+    auto next_tile_ready = [&]() {
+        if constexpr (VM == 0) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        else if constexpr (VM == 4) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+    if constexpr (W == 8) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else next_tile_ready();   // tile 0
 
     if constexpr (W == 8) {
         // Ping-pong schedule: waves w and w + 4 share a SIMD (read from
@@ -638,28 +698,21 @@ prefill_bf16_fold_kernel(PrefillArgs pa) {
 #pragma unroll
         for (int db = 0; db < NDB; ++db) pv_v[db][0] = pv_v[db][1] = bf16x8_t{};
         pv_p[0] = pv_p[1] = bf16x8_t{};
-        auto flush = [&]() {
-#pragma unroll
-            for (int db = 0; db < NDB; ++db)
-#pragma unroll
-                for (int t = 0; t < 2; ++t)
-                    acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pv_v[db][t], pv_p[t], acc[db], 0, 0, 0);
-        };
         auto end_tile = [&](int kt, int stage) {
             asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
             if (kt + NS < n_kt) dma_tile(kt + NS, stage);
         };
         auto half = [&](int kt, int stage, int kb) {
             const lds_u8_t* sb = lsm + stage * kDmaStageBytes;
-            bf16x8_t kf[NKS];
+            bf16x8_t kf[FoldWave::NKS];
 #pragma unroll
-            for (int ks = 0; ks < NKS; ++ks) kf[ks] = lds_k(sb, kb, ks);
-            flush();
+            for (int ks = 0; ks < FoldWave::NKS; ++ks) kf[ks] = fw.lds_k(sb, kb, ks);
+            fw.pv(pv_v, pv_p);
 #pragma unroll
             for (int db = 0; db < NDB; ++db)
 #pragma unroll
-                for (int t = 0; t < 2; ++t) pv_v[db][t] = lds_vt(sb, kb, t, db);
-            const f32x16_t s = scores(kf);
+                for (int t = 0; t < 2; ++t) pv_v[db][t] = fw.lds_vt(sb, kb, t, db);
+            const f32x16_t s = fw.scores(kf);
             auto sync = [&]() {
                 __builtin_amdgcn_sched_barrier(0);
                 if (kb == 0) asm volatile("s_barrier" ::: "memory");
@@ -667,9 +720,9 @@ prefill_bf16_fold_kernel(PrefillArgs pa) {
                 __builtin_amdgcn_sched_barrier(0);
             };
             if (late) sync();
-            float rs = softmax(s, pv_p);
-            settle(s, pv_p, rs);
-            lp += rs;
+            float rs = FoldWave::softmax(s, pv_p);
+            fw.settle(s, pv_p, rs);
+            fw.lp += rs;
             if (!late) sync();
         };
         const int kt_pp = (wk.qt * qtile + 31) / kKTile / NS * NS;
@@ -680,17 +733,17 @@ prefill_bf16_fold_kernel(PrefillArgs pa) {
                 half(kt + s, s, 1);
             }
         }
-        flush();
+        fw.pv(pv_v, pv_p);
         for (int kt = kt_pp; kt < n_kt; ++kt) {
             const int stage = kt % NS;
-            if (kt + 1 < wave_kt) tile(kt, lsm + stage * kDmaStageBytes, std::false_type{});
+            if (kt + 1 < wave_kt) fw.tile<false>(kt, lsm + stage * kDmaStageBytes);
             end_tile(kt, stage);
         }
     } else {
         auto step = [&](int kt, int stage) {
             const bool more = kt + NS - 1 < n_kt;
             if (more) dma_tile(kt + NS - 1, (stage + NS - 1) % NS);
-            if (kt + 1 < wave_kt) tile(kt, lsm + stage * kDmaStageBytes, std::false_type{});
+            if (kt + 1 < wave_kt) fw.tile<false>(kt, lsm + stage * kDmaStageBytes);
             if (more) next_tile_ready();
             else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
         };
@@ -700,21 +753,112 @@ prefill_bf16_fold_kernel(PrefillArgs pa) {
             for (int s = 0; s < NS; ++s) step(kt + s, s);
         }
     }
-    if (wave_kt > 0) tile(wave_kt - 1, lsm + ((wave_kt - 1) % NS) * kDmaStageBytes, std::true_type{});
+    if (wave_kt > 0) fw.tile<true>(wave_kt - 1, lsm + ((wave_kt - 1) % NS) * kDmaStageBytes);
 
-    const float l = lp + __shfl_xor(lp, 32, 64);
-    const int qi = q_wave0 + n;
-    if (qi < L) {
-        const float inv = 1.0f / l;
-        float* orow = pa.out + wk.b * pa.os[0] + h * pa.os[1] + qi * pa.os[2] + 4 * hh;
+    fw.store(pa.out + wk.b * pa.os[0] + h * pa.os[1], pa.os[2], L);
+}
+
+
+// ===========================================================================
+// bf16 kernel, head_dim 128, short prompts: each 32-query tile's key range
+// split across wave groups of one workgroup
+// ===========================================================================
+// When even 4-wave workgroups leave CUs idle, the chain of key tiles that
+// one workgroup walks sets the time (about 1.2 us per tile with one wave per
+// SIMD, on top of a fixed ~6 us).  A workgroup here serves 32 queries of GH
+// query heads of one KV group; its W = KS x GH waves form KS groups, group g
+// walking tiles g, g + KS, ... of the shared key range, so a chain is
+// ceil(n_kt / KS) tiles long.  One step stages the KS tiles of the groups
+// (NS = 2 steps resident, loaded straight into LDS); the diagonal tile, the
+// last one, stays in its stage after the loop and its group applies the
+// mask there.  The groups' (m, l, O) partials then meet in LDS, where group
+// 0 merges them (O = sum 2^(m_g - M) O_g, l likewise, M the largest m_g) and
+// writes the output.  No second launch and no global workspace.
+template <int KS, int GH>
+__global__ void __launch_bounds__(KS * GH * 64)
+prefill_bf16_split_kernel(PrefillArgs pa) {
+    constexpr int W = KS * GH;
+    constexpr int NDB = FoldWave::NDB;
+    constexpr int STEP_BYTES = KS * kDmaStageBytes;
+    extern __shared__ __align__(16) unsigned char smem[];
+    lds_u8_t* const lsm = (lds_u8_t*)smem;
+
+    const int L = pa.L;
+    const Work wk = map_work(pa, blockIdx.x);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = wave / GH;                  // key group
+    const int hl = wave % GH;                 // head of the workgroup's set
+    const int h = wk.h0 + hl;
+    const uint16_t* Q = static_cast<const uint16_t*>(pa.q) + wk.b * pa.qs[0] + h * pa.qs[1];
+    const uint16_t* K = static_cast<const uint16_t*>(pa.k) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
+    const uint16_t* V = static_cast<const uint16_t*>(pa.v) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
+    const int kv_row = static_cast<int>(pa.kvs[2]);
+
+    const int q0 = wk.qt * 32;
+    const int n_kt = (min(L, q0 + 32) - 1) / kKTile + 1;   // tiles through the diagonal
+    const int n_steps = (n_kt + KS - 1) / KS;
+
+    const DmaMap<W> dm(wave, lane);
+    auto dma_step = [&](int t, int stage) {
+        lds_u8_t* sb = lsm + stage * STEP_BYTES;
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+            if (t * KS + s < n_kt) dm.load(K, V, kv_row, (t * KS + s) * kKTile, L, wave, sb + s * kDmaStageBytes);
+    };
+    dma_step(0, 0);
+    FoldWave fw;
+    fw.init(Q, pa.qs[2], q0, L, pa.scale, lane);
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");   // step 0 resident
+
+    // Step t: the loads of step t + 1 go out, then this group's tile of step
+    // t unless it is the diagonal; every load has landed at the barrier.
+    auto step = [&](int t, int stage) {
+        if (t + 1 < n_steps) dma_step(t + 1, stage ^ 1);
+        const int kt = t * KS + g;
+        if (kt + 1 < n_kt) fw.tile<false>(kt, lsm + stage * STEP_BYTES + g * kDmaStageBytes);
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+    for (int t = 0; t < n_steps; t += 2) {
+        step(t, 0);
+        step(t + 1, 1);
+    }
+    const int kd = n_kt - 1;
+    if (g == kd % KS) fw.tile<true>(kd, lsm + ((kd / KS) & 1) * STEP_BYTES + g * kDmaStageBytes);
+
+    // Partials of groups 1 .. KS-1 into LDS, [element][lane] per wave (the
+    // stages are free once every wave is past the diagonal tile).
+    constexpr int NE = NDB * 16 + 2;
+    float* const part = reinterpret_cast<float*>(smem);
+    __syncthreads();
+    if (g > 0) {
+        float* p = part + ((g - 1) * GH + hl) * NE * 64 + lane;
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj)
-                *reinterpret_cast<float4*>(orow + 32 * db + 8 * jj) =
-                    make_float4(acc[db][4 * jj] * inv, acc[db][4 * jj + 1] * inv, acc[db][4 * jj + 2] * inv,
-                                acc[db][4 * jj + 3] * inv);
+            for (int j = 0; j < 16; ++j) p[(db * 16 + j) * 64] = fw.acc[db][j];
+        p[(NE - 2) * 64] = fw.ms;
+        p[(NE - 1) * 64] = fw.lp;
     }
+    __syncthreads();
+    if (g != 0) return;
+    // Group 0 always holds tile 0, so its m is finite; a group without a
+    // tile carries m = -inf and weight 0.
+#pragma unroll
+    for (int o = 1; o < KS; ++o) {
+        const float* p = part + ((o - 1) * GH + hl) * NE * 64 + lane;
+        const float mo = p[(NE - 2) * 64], lo = p[(NE - 1) * 64];
+        const float m = fmaxf(fw.ms, mo);
+        const float a = __builtin_amdgcn_exp2f(fw.ms - m);
+        const float b = mo == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mo - m);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) fw.acc[db][j] = fw.acc[db][j] * a + p[(db * 16 + j) * 64] * b;
+        fw.lp = fw.lp * a + lo * b;
+        fw.ms = m;
+    }
+    fw.store(pa.out + wk.b * pa.os[0] + h * pa.os[1], pa.os[2], L);
 }
 
 // ===========================================================================
@@ -968,6 +1112,23 @@ sa_status launch_bf16_dma(const PrefillArgs& pa, dim3 grid, hipStream_t st) {
     return SA_OK;
 }
 
+// The split kernel: KS = 2 key groups of GH = 2 heads, 2 stages of 2 tiles
+// (128 KiB of LDS, one workgroup per CU).  Measured against an 8-wave
+// variant whose four groups take 32-key halves of the same tiles (2 waves per
+// SIMD): equal at L = 1024, slower below; per CU both are bound by the
+// heaviest query tile's tile count at one tile per ~1.2 us per SIMD.
+constexpr int kSplitKS = 2;
+constexpr int kSplitGH = 2;
+
+sa_status launch_bf16_split(const PrefillArgs& pa, dim3 grid, hipStream_t st) {
+    constexpr int bytes = 2 * kSplitKS * kDmaStageBytes;
+    sa_status s = opt_in_lds<&prefill_bf16_split_kernel<kSplitKS, kSplitGH>>(bytes);
+    if (s != SA_OK) return s;
+    hipLaunchKernelGGL((prefill_bf16_split_kernel<kSplitKS, kSplitGH>), grid, dim3(kSplitKS * kSplitGH * 64), bytes,
+                       st, pa);
+    return SA_OK;
+}
+
 // Workgroups of W waves serve gh = gcd(Hq / Hkv, W) query heads, W / gh
 // waves of 32 queries per head.
 long long bf16_grid(const PrefillArgs& pa, int B, int W) {
@@ -984,6 +1145,29 @@ sa_status launch(PrefillArgs pa, int B, bool bf16, int D, hipStream_t st) {
     // SA_PREFILL_WAVES=4 or 8 forces the workgroup size (tests cover both).
     const char* forced = std::getenv("SA_PREFILL_WAVES");
     const int fw = forced ? std::atoi(forced) : 0;
+    // Shorter prompts still (the 4-wave grid has at most one workgroup per
+    // CU), head_dim 128, GQA groups of an even size: the split kernel, whose
+    // 32-query workgroups walk each half of their key range in one of two
+    // wave groups.  Measured (16/8 heads, graph-replayed calls): L = 512 /
+    // 1024 / 2048 take 12.1 / 18.5 / 37.6 us against 15.4 / 24.8 / 43.5 us
+    // with 4-wave workgroups; L = 128 8.3 us either way.
+    // SA_PREFILL_SPLIT=1 / 0 forces it on (where the shape allows) / off.
+    const char* fsplit = std::getenv("SA_PREFILL_SPLIT");
+    const bool split_shape = bf16 && D == 128 && (pa.Hq / pa.Hkv) % kSplitGH == 0;
+    const bool split = split_shape && (fsplit ? std::atoi(fsplit) != 0
+                                              : !forced && bf16_grid(pa, B, kBfWSmall) <= device_cu_count());
+    if (split) {
+        pa.gh = kSplitGH;
+        pa.n_qt = (pa.L + 31) / 32;
+        const int groups = B * pa.Hkv;
+        pa.xcd_groups = groups % 8 == 0 ? groups / 8 : 0;
+        const long long n_wg = (long long)B * (pa.Hq / pa.gh) * pa.n_qt;
+        if (n_wg > 0x7fffffffLL) return fail(SA_ERANGE, "prefill grid too large");
+        const sa_status s = launch_bf16_split(pa, dim3(static_cast<unsigned>(n_wg)), st);
+        if (s != SA_OK) return s;
+        SA_CHECK_LAUNCH();
+        return SA_OK;
+    }
     const int W = fw == kBfW || fw == kBfWSmall ? fw
                   : bf16 && bf16_grid(pa, B, kBfW) < 2LL * device_cu_count() ? kBfWSmall : kBfW;
     pa.gh = bf16 ? std::gcd(pa.Hq / pa.Hkv, W) : 1;

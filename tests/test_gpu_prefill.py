@@ -68,6 +68,19 @@ def test_prefill_fp32_8192_rows(sa, oracle, synth):
     assert rel_l2(got, want) <= 1e-5
 
 
+def variant(monkeypatch, v):
+    """The bf16 kernel a launch takes: "4" / "8" force the workgroup width of
+    the unsplit kernels, "split" the kernel that splits each 32-query tile's
+    key range over two wave groups (head_dim 128, even GQA groups; other
+    shapes fall back to the unsplit kernels)."""
+    if v == "split":
+        monkeypatch.delenv("SA_PREFILL_WAVES", raising=False)
+        monkeypatch.setenv("SA_PREFILL_SPLIT", "1")
+    else:
+        monkeypatch.setenv("SA_PREFILL_WAVES", v)
+        monkeypatch.setenv("SA_PREFILL_SPLIT", "0")
+
+
 def roped(oracle, x):
     """x [B, H, L, D] rotated at positions 0 .. L-1 (theta 1e6), as the
     prompt's q and k are after the decoder layer's RoPE."""
@@ -116,7 +129,7 @@ def test_prefill_last_row_is_decode(sa, synth):
     assert np.abs(out[:, :, L - 1] - dec).max() <= 1e-5
 
 
-@pytest.mark.parametrize("waves", ["4", "8"])
+@pytest.mark.parametrize("waves", ["4", "8", "split"])
 @pytest.mark.parametrize("Hq,Hkv,D,L", [(4, 4, 128, 300), (8, 2, 128, 513), (16, 8, 64, 300),
                                         (2, 1, 64, 700), (16, 16, 128, 257), (16, 8, 128, 300),
                                         (32, 4, 128, 200)])
@@ -124,10 +137,11 @@ def test_prefill_bf16_shapes(sa, oracle, synth, monkeypatch, Hq, Hkv, D, L, wave
     """bf16 at other head layouts, D = 64, batch 2, L off the tile sizes; 16/8
     heads at batch 2 also exercise the per-XCD mapping of KV groups.  Both
     workgroup sizes (the launch picks 4 waves for grids that would not fill
-    the CUs twice, 8 otherwise) run every shape.  D = 128 with GQA groups of
-    2 or more runs the kernel that loads tiles straight into LDS; D = 64 and
-    the group of 1 run the register-staged one."""
-    monkeypatch.setenv("SA_PREFILL_WAVES", waves)
+    the CUs twice, 8 otherwise) run every shape, and so does the split-key
+    kernel of short prompts.  D = 128 with GQA groups of 2 or more runs the
+    kernels that load tiles straight into LDS; D = 64 and the group of 1 run
+    the register-staged one."""
+    variant(monkeypatch, waves)
     q, k, v = inputs(synth, L, Hq, Hkv, D, seed=55)
     q2 = synth.bf16_round(np.concatenate([q, synth.normal(56, 1, q.shape)], 0))
     k2 = synth.bf16_round(np.concatenate([k, synth.normal(56, 2, k.shape)], 0))
@@ -142,12 +156,14 @@ def test_prefill_bf16_shapes(sa, oracle, synth, monkeypatch, Hq, Hkv, D, L, wave
     assert err.max() <= 4e-2
 
 
-@pytest.mark.parametrize("waves", ["4", "8"])
-@pytest.mark.parametrize("L", [1, 17, 64, 65, 129])
+@pytest.mark.parametrize("waves", ["4", "8", "split"])
+@pytest.mark.parametrize("L", [1, 17, 64, 65, 129, 191, 192, 193])
 def test_prefill_bf16_short(sa, oracle, synth, monkeypatch, L, waves):
-    """Prompts of one to three 64-key tiles at 16/8 heads, D = 128: fewer tiles
-    than the load-to-LDS kernel keeps in flight, rows past L clamped."""
-    monkeypatch.setenv("SA_PREFILL_WAVES", waves)
+    """Prompts of one to four 64-key tiles at 16/8 heads, D = 128: fewer tiles
+    than the load-to-LDS kernels keep in flight, rows past L clamped, and for
+    the split kernel key groups with no tile, an odd tile count and the
+    diagonal in either group."""
+    variant(monkeypatch, waves)
     q, k, v = inputs(synth, L, seed=58)
     qb, kb, vb = synth.bf16_round(q), synth.bf16_round(k), synth.bf16_round(v)
     sc = np.float32(1 / np.sqrt(128))
@@ -159,13 +175,13 @@ def test_prefill_bf16_short(sa, oracle, synth, monkeypatch, L, waves):
         np.testing.assert_allclose(out[:, :, 0], np.repeat(vb[:, :, 0], 2, axis=1), rtol=0, atol=1e-6)
 
 
-@pytest.mark.parametrize("waves", ["4", "8"])
+@pytest.mark.parametrize("waves", ["4", "8", "split"])
 @pytest.mark.parametrize("scale", [-0.3, 0.0])
 @pytest.mark.parametrize("bf16", [False, True])
 def test_prefill_scale_sign(sa, oracle, synth, monkeypatch, scale, bf16, waves):
     """Negative and zero scales (zero: uniform average over the prefix), at
-    both bf16 workgroup sizes."""
-    monkeypatch.setenv("SA_PREFILL_WAVES", waves)
+    both bf16 workgroup sizes and in the split kernel."""
+    variant(monkeypatch, waves)
     L = 200
     q, k, v = inputs(synth, L, 4, 2, 128, seed=57)
     if bf16:
