@@ -11,8 +11,8 @@
  * GPU computation.
  *
  * Differences from the reference, all deliberate:
- *   - d must be 64, 128 or 256 (the kernels' head sizes); other values throw
- *     std::invalid_argument instead of computing.
+ *   - d must be 8, 16, 32, 64, 128 or 256 (the kernels' head sizes); other
+ *     values throw std::invalid_argument instead of computing.
  *   - block_size must be positive (the reference divides by it).
  *   - T <= 0 returns zeros for every variant (streaming_attention_omp of the
  *     reference returns NaN for T = 0).

@@ -9,6 +9,11 @@
  *
  * Layouts are row-major.  "token-major" means [seq][token][head][head_dim],
  * which is what a Q/K/V projection writes before any transpose.
+ *
+ * Head sizes (head_dim, d, D): 8, 16, 32, 64, 128 or 256 for single-query
+ * attention, decode, the KV cache and QK-norm/RoPE; the fused decode step
+ * (sa_append_decode) takes 64, 128 or 256; causal prefill 16, 32, 64 or 128
+ * in fp32 and 64 or 128 in bf16.  Other sizes return SA_EINVAL.
  */
 #ifndef SA_AMD_H
 #define SA_AMD_H
@@ -116,7 +121,7 @@ sa_status sa_decode_dense_f32(const float* q, const float* k, const float* v,
 typedef struct sa_kv_desc {
     int num_layers;
     int num_kv_heads;
-    int head_dim;           /* 64, 128 or 256 */
+    int head_dim;           /* 8, 16, 32, 64, 128 or 256 */
     int max_seqs;
     int max_pages_per_seq;
     int num_pages;          /* pages in the pool shared by all sequences */

@@ -14,7 +14,8 @@
  * prefill from position 0 (q_len = kv_len).  self_attention accepts a null or
  * all-zero mask with q_len = 1, or the causal mask with q_len = kv_len; any
  * other mask throws std::invalid_argument.  cross_attention takes any q_len
- * and kv_len (every query row sees every key).
+ * and kv_len (every query row sees every key).  head_dim: 8, 16, 32, 64, 128
+ * or 256 without a mask, 16, 32, 64 or 128 for causal prefill.
  *
  * The reference's all_reduce_sum and broadcast (MPI collectives, ops.h:338-339)
  * are not here: this library serves one GPU per process.
@@ -91,8 +92,8 @@ Tensor rms_norm(const Tensor& input, const Tensor* weight = nullptr, float eps =
  * compute_rope_freqs).  apply rotates the first seq_len positions on the GPU
  * and returns zeros for positions past seq_len, as the reference.  dim must
  * be even (the constructor throws std::invalid_argument otherwise, as the
- * reference); apply takes dim 64, 128 or 256 and seq_len up to max_seq_len
- * and the input's seq axis (std::invalid_argument otherwise). */
+ * reference); apply takes dim 8, 16, 32, 64, 128 or 256 and seq_len up to
+ * max_seq_len and the input's seq axis (std::invalid_argument otherwise). */
 class RotaryEmbedding {
 public:
     RotaryEmbedding(size_t dim, size_t max_seq_len = 2048, float theta = 10000.0f);

@@ -14,7 +14,7 @@
  * logits.  Also here: qwen3_attention_with_cache, the part of the layer
  * between the projections and o_proj, for callers with their own projections.
  *
- * Shapes the GPU path takes: head_dim 64 or 128; with a non-empty cache one
+ * Shapes the GPU path takes: head_dim 16, 32, 64 or 128; with a non-empty cache one
  * token per call (as the reference, whose concat appends one token).  Others
  * throw std::invalid_argument.
  */

@@ -14,8 +14,8 @@ namespace {
 std::vector<float> run_single(const float* Q, const float* K, const float* V, int T, int d,
                               int block_size) {
     using namespace sa_compat;
-    if (d != 64 && d != 128 && d != 256)
-        throw std::invalid_argument("d must be 64, 128 or 256 (got " + std::to_string(d) + ")");
+    if (d != 8 && d != 16 && d != 32 && d != 64 && d != 128 && d != 256)
+        throw std::invalid_argument("d must be 8, 16, 32, 64, 128 or 256 (got " + std::to_string(d) + ")");
     if (block_size <= 0) throw std::invalid_argument("block_size must be positive");
     std::vector<float> out(d, 0.0f);
     if (T <= 0) return out;

@@ -107,10 +107,12 @@ void expect_vector(const Tensor& t, size_t n, const char* name) {
     if (t.size() != n) bad(std::string(name) + " must have " + std::to_string(n) + " entries");
 }
 
-// Head counts and size the GPU kernels take (causal prefill: head_dim 64 or 128).
+// Head counts and size the GPU kernels take (fp32 causal prefill: head_dim
+// 16, 32, 64 or 128).
 void check_heads(size_t Hq, size_t Hkv, size_t D) {
     if (Hq == 0 || Hkv == 0 || Hq % Hkv) bad("num_attention_heads must be a multiple of num_key_value_heads");
-    if (D != 64 && D != 128) bad("head_dim must be 64 or 128 on the GPU (got " + std::to_string(D) + ")");
+    if (D != 16 && D != 32 && D != 64 && D != 128)
+        bad("head_dim must be 16, 32, 64 or 128 on the GPU (got " + std::to_string(D) + ")");
 }
 
 Geometry geometry(const Tensor& hidden, size_t Hq, size_t Hkv, size_t D) {

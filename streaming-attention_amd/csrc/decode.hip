@@ -505,11 +505,15 @@ split_kv_decode_kernel(DecodeArgs a) {
     }
 
     // Sum the row groups of this wave: l and O were accumulated per group.
+    // l is uniform inside a group; O holds a different column slice in each
+    // lane of a group, so its sum pairs lanes by xor only (the mirror steps of
+    // group_reduce would mix columns when a row spans fewer than 16 lanes:
+    // fp32 D <= 32, bf16 D <= 64).
 #pragma unroll
     for (int h = 0; h < NREP; ++h) {
         l[h] = group_reduce<OpSum, LPR, kWave>(l[h]);
 #pragma unroll
-        for (int e = 0; e < E; ++e) o[h][e] = group_reduce<OpSum, LPR, kWave>(o[h][e]);
+        for (int e = 0; e < E; ++e) o[h][e] = group_reduce_xor<OpSum, LPR, kWave>(o[h][e]);
     }
 
     __shared__ float sh_m[W][NREP];
@@ -756,17 +760,30 @@ sa_status dispatch_nrep(const DecodeArgs& a, int n_seq, int nrep, hipStream_t st
     }
 }
 
+// Head sizes 8 .. 256 (powers of two): a K/V row is D / E lanes of 16-byte
+// loads, 64 / (D / E) rows per wave-load.  The fused decode step takes the
+// sizes of the model path, 64 .. 256.
 template <bool BF16, bool PAGED, bool FUSED = false>
 sa_status dispatch_decode(const DecodeArgs& a, int n_seq, int d, int nrep, hipStream_t st) {
+    if constexpr (!FUSED) {
+        switch (d) {
+            case 8: return dispatch_nrep<8, BF16, PAGED, false>(a, n_seq, nrep, st);
+            case 16: return dispatch_nrep<16, BF16, PAGED, false>(a, n_seq, nrep, st);
+            case 32: return dispatch_nrep<32, BF16, PAGED, false>(a, n_seq, nrep, st);
+            default: break;
+        }
+    }
     switch (d) {
         case 64: return dispatch_nrep<64, BF16, PAGED, FUSED>(a, n_seq, nrep, st);
         case 128: return dispatch_nrep<128, BF16, PAGED, FUSED>(a, n_seq, nrep, st);
         case 256: return dispatch_nrep<256, BF16, PAGED, FUSED>(a, n_seq, nrep, st);
-        default: return fail(SA_EINVAL, "head_dim must be 64, 128 or 256");
+        default:
+            return fail(SA_EINVAL, FUSED ? "head_dim must be 64, 128 or 256"
+                                         : "head_dim must be 8, 16, 32, 64, 128 or 256");
     }
 }
 
-bool supported_d(int d) { return d == 64 || d == 128 || d == 256; }
+bool supported_d(int d) { return d == 8 || d == 16 || d == 32 || d == 64 || d == 128 || d == 256; }
 
 }  // namespace
 
@@ -778,7 +795,7 @@ sa_status decode_dense(const float* q, const float* k, const float* v, int batch
     if (!q || !out || (T > 0 && (!k || !v))) return fail(SA_EINVAL, "null pointer");
     if (batch <= 0 || n_q <= 0 || n_kv <= 0 || n_q % n_kv)
         return fail(SA_EINVAL, "bad head counts");
-    if (!supported_d(d)) return fail(SA_EINVAL, "head_dim must be 64, 128 or 256");
+    if (!supported_d(d)) return fail(SA_EINVAL, "head_dim must be 8, 16, 32, 64, 128 or 256");
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
         return fail(SA_EINVAL, "q, k, v and out must be 16-byte aligned");
     if (T <= 0) {

@@ -240,8 +240,9 @@ extern "C" sa_status sa_kvcache_create(const sa_kv_desc* d, sa_kvcache** out) {
         return fail(SA_EINVAL, "cache dimensions must be positive");
     if (d->max_pages_per_seq > (1 << 18))
         return fail(SA_EINVAL, "max_pages_per_seq must be at most 262144 (16M tokens)");
-    if (d->head_dim != 64 && d->head_dim != 128 && d->head_dim != 256)
-        return fail(SA_EINVAL, "head_dim must be 64, 128 or 256");
+    if (d->head_dim != 8 && d->head_dim != 16 && d->head_dim != 32 && d->head_dim != 64 && d->head_dim != 128 &&
+        d->head_dim != 256)
+        return fail(SA_EINVAL, "head_dim must be 8, 16, 32, 64, 128 or 256");
     if (d->kv_dtype != SA_DTYPE_F32 && d->kv_dtype != SA_DTYPE_BF16)
         return fail(SA_EINVAL, "kv_dtype must be F32 or BF16");
     auto* c = new sa_kvcache();
@@ -457,6 +458,9 @@ extern "C" sa_status sa_qknorm_rope_append(sa_kvcache* c, int layer, const float
         if (bf) hipLaunchKernelGGL((qknorm_rope_append_kernel<DD, true>), grid, dim3(256), 0, st, a); \
         else hipLaunchKernelGGL((qknorm_rope_append_kernel<DD, false>), grid, dim3(256), 0, st, a); \
         break;
+            SA_APPEND_CASE(8)
+            SA_APPEND_CASE(16)
+            SA_APPEND_CASE(32)
             SA_APPEND_CASE(64)
             SA_APPEND_CASE(128)
             SA_APPEND_CASE(256)
@@ -507,6 +511,7 @@ extern "C" sa_status sa_append_decode(sa_kvcache* c, int layer, const float* q, 
     if (n_q_heads <= 0 || n_q_heads % c->desc.num_kv_heads) return fail(SA_EINVAL, "bad head counts");
     if ((rope_cos == nullptr) != (rope_sin == nullptr)) return fail(SA_EINVAL, "cos and sin go together");
     if (rope_cos && rope_max_pos <= 0) return fail(SA_EINVAL, "RoPE table needs rope_max_pos > 0");
+    if (c->desc.head_dim < 64) return fail(SA_EINVAL, "the fused decode step takes head_dim 64, 128 or 256");
     Verdict vd = c->pt.check_append(seq_ids, n_seq, 1, rope_cos ? rope_max_pos : 0);
     if (!vd.ok()) return refused(vd);
     int max_len = 0;
@@ -573,20 +578,20 @@ extern "C" sa_status sa_qk_norm_rope_ex(const float* x, int n_rows, int D, const
     const dim3 grid((n_rows + 3) / 4);
     const bool outside = mode == SA_NORM_EPS_OUTSIDE;
     switch (D) {
-        case 64:
-            hipLaunchKernelGGL(qk_norm_rope_kernel<64>, grid, dim3(256), 0, st, x, n_rows, pos, norm_w, eps,
-                               outside, rope_cos, rope_sin, rope_max_pos, y);
-            break;
-        case 128:
-            hipLaunchKernelGGL(qk_norm_rope_kernel<128>, grid, dim3(256), 0, st, x, n_rows, pos, norm_w, eps,
-                               outside, rope_cos, rope_sin, rope_max_pos, y);
-            break;
-        case 256:
-            hipLaunchKernelGGL(qk_norm_rope_kernel<256>, grid, dim3(256), 0, st, x, n_rows, pos, norm_w, eps,
-                               outside, rope_cos, rope_sin, rope_max_pos, y);
-            break;
+#define SA_NORM_ROPE_CASE(DD)                                                                          \
+    case DD:                                                                                           \
+        hipLaunchKernelGGL(qk_norm_rope_kernel<DD>, grid, dim3(256), 0, st, x, n_rows, pos, norm_w, eps, \
+                           outside, rope_cos, rope_sin, rope_max_pos, y);                              \
+        break;
+        SA_NORM_ROPE_CASE(8)
+        SA_NORM_ROPE_CASE(16)
+        SA_NORM_ROPE_CASE(32)
+        SA_NORM_ROPE_CASE(64)
+        SA_NORM_ROPE_CASE(128)
+        SA_NORM_ROPE_CASE(256)
+#undef SA_NORM_ROPE_CASE
         default:
-            return fail(SA_EINVAL, "head_dim must be 64, 128 or 256");
+            return fail(SA_EINVAL, "head_dim must be 8, 16, 32, 64, 128 or 256");
     }
     SA_CHECK_LAUNCH();
     return SA_OK;

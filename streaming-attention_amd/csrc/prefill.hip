@@ -1129,6 +1129,13 @@ sa_status launch_bf16_split(const PrefillArgs& pa, dim3 grid, hipStream_t st) {
     return SA_OK;
 }
 
+template <int D>
+sa_status launch_f32(const PrefillArgs& pa, dim3 grid, hipStream_t st) {
+    sa_status s = opt_in_lds<&prefill_f32_kernel<D>>(F32Lds<D>::BYTES);
+    if (s == SA_OK) hipLaunchKernelGGL(prefill_f32_kernel<D>, grid, dim3(kFThreads), F32Lds<D>::BYTES, st, pa);
+    return s;
+}
+
 // Workgroups of W waves serve gh = gcd(Hq / Hkv, W) query heads, W / gh
 // waves of 32 queries per head.
 long long bf16_grid(const PrefillArgs& pa, int B, int W) {
@@ -1193,14 +1200,13 @@ sa_status launch(PrefillArgs pa, int B, bool bf16, int D, hipStream_t st) {
     } else if (bf16) {
         s = D == 64 ? launch_bf16<64, kBfQB, kBfWSmall>(pa, grid, st)
                     : launch_bf16<128, kBfQB, kBfWSmall>(pa, grid, st);
-    } else if (D == 64) {
-        s = opt_in_lds<&prefill_f32_kernel<64>>(F32Lds<64>::BYTES);
-        if (s == SA_OK)
-            hipLaunchKernelGGL(prefill_f32_kernel<64>, grid, dim3(kFThreads), F32Lds<64>::BYTES, st, pa);
     } else {
-        s = opt_in_lds<&prefill_f32_kernel<128>>(F32Lds<128>::BYTES);
-        if (s == SA_OK)
-            hipLaunchKernelGGL(prefill_f32_kernel<128>, grid, dim3(kFThreads), F32Lds<128>::BYTES, st, pa);
+        switch (D) {
+            case 16: s = launch_f32<16>(pa, grid, st); break;
+            case 32: s = launch_f32<32>(pa, grid, st); break;
+            case 64: s = launch_f32<64>(pa, grid, st); break;
+            default: s = launch_f32<128>(pa, grid, st); break;
+        }
     }
     if (s != SA_OK) return s;
     SA_CHECK_LAUNCH();
@@ -1214,7 +1220,9 @@ sa_status prefill(const void* q, const void* k, const void* v, sa_dtype dtype, i
     if (batch <= 0 || n_q_heads <= 0 || n_kv_heads <= 0 || n_q_heads % n_kv_heads)
         return fail(SA_EINVAL, "bad head counts");
     if (dtype != SA_DTYPE_F32 && dtype != SA_DTYPE_BF16) return fail(SA_EINVAL, "dtype must be F32 or BF16");
-    if (D != 64 && D != 128) return fail(SA_EINVAL, "prefill head_dim must be 64 or 128");
+    if (dtype == SA_DTYPE_BF16 ? D != 64 && D != 128 : D != 16 && D != 32 && D != 64 && D != 128)
+        return fail(SA_EINVAL, dtype == SA_DTYPE_BF16 ? "bf16 prefill head_dim must be 64 or 128"
+                                                      : "fp32 prefill head_dim must be 16, 32, 64 or 128");
     if (L <= 0) return SA_OK;
     const int elem = dtype == SA_DTYPE_BF16 ? 2 : 4;
     const int64_t align_in = 16 / elem, align_out = 4;

@@ -67,10 +67,14 @@ constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i within 8
 constexpr int kDppMirror = 0x140;     // lane i <-> 15-i within 16
 
-__device__ __forceinline__ float swz_xor16(float v) {
-    // ds_swizzle bit mode: and_mask 0x1f, or_mask 0, xor_mask 0x10
-    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+// Lane i <-> i ^ M within 32 lanes (ds_swizzle bit mode: and_mask 0x1f,
+// or_mask 0, xor_mask M).
+template <int M>
+__device__ __forceinline__ float swz_xor(float v) {
+    static_assert(M > 0 && M < 32, "ds_swizzle xor masks stay inside 32 lanes");
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), (M << 10) | 0x1F));
 }
+__device__ __forceinline__ float swz_xor16(float v) { return swz_xor<16>(v); }
 __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
 
 struct OpSum { __device__ static float apply(float a, float b) { return a + b; } };
@@ -87,6 +91,21 @@ __device__ __forceinline__ float group_reduce(float v) {
     if constexpr (FROM <= 4 && TO > 4) v = Op::apply(v, dpp<kDppHalfMirror>(v));
     if constexpr (FROM <= 8 && TO > 8) v = Op::apply(v, dpp<kDppMirror>(v));
     if constexpr (FROM <= 16 && TO > 16) v = Op::apply(v, swz_xor16(v));
+    if constexpr (FROM <= 32 && TO > 32) v = Op::apply(v, xor32(v));
+    return v;
+}
+
+// The same reduction for values that differ inside the groups of FROM lanes
+// (say, one column of a row per lane): every step pairs lane i with lane
+// i ^ mask, so lanes are combined only with lanes of the same position in
+// their group.
+template <class Op, int FROM, int TO>
+__device__ __forceinline__ float group_reduce_xor(float v) {
+    if constexpr (FROM <= 1 && TO > 1) v = Op::apply(v, dpp<kDppXor1>(v));
+    if constexpr (FROM <= 2 && TO > 2) v = Op::apply(v, dpp<kDppXor2>(v));
+    if constexpr (FROM <= 4 && TO > 4) v = Op::apply(v, swz_xor<4>(v));
+    if constexpr (FROM <= 8 && TO > 8) v = Op::apply(v, swz_xor<8>(v));
+    if constexpr (FROM <= 16 && TO > 16) v = Op::apply(v, swz_xor<16>(v));
     if constexpr (FROM <= 32 && TO > 32) v = Op::apply(v, xor32(v));
     return v;
 }

@@ -68,7 +68,7 @@ MODEL_CASES = [
     dict(cfg=dict(num_layers=3, hidden=128, intermediate=256, vocab=512, n_q_heads=4, n_kv_heads=4,
                   head_dim=32, rms_eps=1e-6, rope_theta=1e6, max_pos=64),
          seed=8, std=0.1, batch=3, prompt=3, steps=5),
-    # head_dim 64 and 128: the head sizes the GPU attention kernels take
+    # head_dim 64 and 128: also the head sizes of the bf16 device model
     dict(cfg=dict(num_layers=2, hidden=128, intermediate=192, vocab=320, n_q_heads=4, n_kv_heads=2,
                   head_dim=64, rms_eps=1e-6, rope_theta=1e6, max_pos=64),
          seed=9, std=0.1, batch=2, prompt=6, steps=4),

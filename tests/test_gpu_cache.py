@@ -134,6 +134,50 @@ def test_paged_decode_matches_oracle(sa, oracle, synth, bf16):
     cache.close()
 
 
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("d,hq,hkv", [(8, 4, 2), (16, 4, 2), (32, 4, 4), (32, 16, 2), (64, 16, 8), (256, 8, 8)])
+def test_head_dims_append_gather_decode(sa, oracle, synth, bf16, d, hq, hkv):
+    """Head sizes other than 128 through the cache, in fp32 and bf16: the
+    fused q/k norm + RoPE append (against the oracle), the gather (bit-exact
+    round trip of what the append stored) and the paged decode (against the
+    oracle's STANDARD decode on the stored K/V), on shuffled pages, lengths
+    1 .. 700.  A K/V row then spans 1 to 64 lanes of a wave."""
+    lens = [1, 63, 64, 65, 700]
+    dt = sa.SA_DTYPE_BF16 if bf16 else sa.SA_DTYPE_F32
+    cache = sa.KVCache(1, hkv, d, len(lens), 16, 64, dt)
+    perm = synth.permutation(90 + d, 1, 64)
+    off = 0
+    cos, sin = sa.rope_tables(1024, d, 1e6)
+    ocos, osin = oracle.rope_tables(1024, d, 1e6)
+    wk = (1 + synth.normal(91, d, d, 0.1)).astype(np.float32)
+    for s, L in enumerate(lens):
+        n = (L + 63) // 64
+        cache.set_pages(s, perm[off:off + n])
+        off += n
+        k = synth.normal(92 + d, s, (1, L, hkv, d))
+        v = synth.normal(93 + d, s, (1, L, hkv, d))
+        cache.append(0, None, dev(k), dev(v), None, dev(wk), 1e-6, rope=(cos, sin), seq_ids=[s])
+        cache.commit(L, seqs=[s])
+        gk, gv = cache.gather(0, s, L)
+        want_k = oracle.apply_rope(oracle.rms_norm_rows(k[0].reshape(-1, d), wk, 1e-6),
+                                   np.repeat(np.arange(L), hkv), ocos, osin).reshape(L, hkv, d).transpose(1, 0, 2)
+        want_v = v[0].transpose(1, 0, 2)
+        if bf16:
+            np.testing.assert_array_equal(host(gv), synth.bf16_round(want_v))
+            assert rel_l2(host(gk), want_k) <= 4e-3
+        else:
+            np.testing.assert_array_equal(host(gv), want_v)
+            assert_f32(host(gk), want_k, 1e-5, 1e-6)
+    q = synth.normal(94 + d, 1, (len(lens), hq, d))
+    sc = float(1 / np.sqrt(d))
+    out = host(cache.decode(0, dev(q), sc))
+    for s, L in enumerate(lens):
+        gk, gv = cache.gather(0, s, L)
+        want = oracle.decode_gqa(q[s][None], host(gk)[None], host(gv)[None], np.float32(sc))[0]
+        assert_f32(out[s], want)
+    cache.close()
+
+
 def test_paged_decode_seq_ids_subset(sa, oracle, synth):
     """Decode a permuted subset of cache rows through host seq_ids."""
     cache = sa.KVCache(1, HKV, D, 4, 20, 64, sa.SA_DTYPE_F32)
@@ -314,7 +358,7 @@ def test_cache_errors(sa):
     cache.close()
 
 
-@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("d", [8, 16, 32, 64, 128, 256])
 @pytest.mark.parametrize("norm,rope", [(True, True), (True, False), (False, True), (False, False)])
 def test_qk_norm_rope_standalone(sa, oracle, synth, d, norm, rope):
     """sa_qk_norm_rope against the oracle's RMSNorm and rotate-half RoPE; rows

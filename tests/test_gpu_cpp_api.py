@@ -1,9 +1,10 @@
 """GPU: the C++ mirror of the reference API (attention.h, KVCache, ops,
 qwen3 attention path), exercised by tests/cpp/test_compat.cpp against the
-oracle (one PASS/FAIL line per check), and three of the reference's own unit
-tests (tensor_cpp/tests/unit/test_streaming_attention.cpp, test_ops.cpp,
-test_avx_ops.cpp), compiled unchanged against include/ and linked to the
-library by oracle/Makefile (ref-on-lib), run on the GPU kernels."""
+oracle (one PASS/FAIL line per check), and four of the reference's own unit
+tests (tensor_cpp/tests/unit/test_streaming_attention.cpp, test_attention.cpp,
+test_ops.cpp, test_avx_ops.cpp), compiled unchanged against include/ and
+linked to the library by oracle/Makefile (ref-on-lib), run on the GPU
+kernels."""
 from __future__ import annotations
 
 import subprocess
@@ -47,6 +48,15 @@ def _run_reference_program(name, tmp_path):
     print(r.stdout[-4000:])
     assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
     return r.stdout
+
+
+def test_reference_attention_unit_test_on_the_gpu(tmp_path):
+    """The reference's self/cross attention suite (head_dim 8 .. 128, query
+    lengths 4 .. 64, key lengths up to 20 beyond the queries), which throws
+    on any failure."""
+    out = _run_reference_program("test_attention", tmp_path)
+    assert "All Attention Tests PASSED" in out
+    assert out.count("Status: OK") >= 6
 
 
 def test_reference_ops_unit_test_on_the_gpu(tmp_path):

@@ -73,7 +73,7 @@ def run_rotary(drv, x, max_seq, theta, seq_len):
 
 
 @pytest.mark.parametrize("B,S,H,D,seq_len,theta", [(2, 10, 3, 64, 7, 10000.0), (1, 40, 2, 128, 40, 1e6),
-                                                   (3, 5, 4, 256, 1, 10000.0)])
+                                                   (3, 5, 4, 256, 1, 10000.0), (2, 9, 8, 16, 9, 10000.0)])
 def test_rotary_embedding(drv, ref_opt, synth, B, S, H, D, seq_len, theta):
     x = synth.normal(71, D + S, (B, S, H, D))
     rc, got = run_rotary(drv, x, 64, theta, seq_len)
@@ -92,7 +92,7 @@ def test_rotary_embedding_refusals(drv, synth):
     assert run_rotary(drv, x, 3, 1e4, 4)[0] == -1                 # past max_seq_len
     assert run_rotary(drv, synth.normal(72, 2, (1, 4, 1, 7)), 64, 1e4, 4)[0] == -1   # odd dim: constructor
     assert drv.drv_last_error() == b"I:Rotary embedding dimension must be even"
-    assert run_rotary(drv, synth.normal(72, 3, (1, 4, 1, 32)), 64, 1e4, 4)[0] == -1  # dim outside 64/128/256
+    assert run_rotary(drv, synth.normal(72, 3, (1, 4, 1, 96)), 64, 1e4, 4)[0] == -1  # not a kernel head size
     assert drv.drv_last_error().startswith(b"I:")
 
 

@@ -105,7 +105,8 @@ def test_prefill_bf16(sa, oracle, synth, L, rope):
     assert rel_l2(out[:, :, rows], want) <= 2e-2
 
 
-@pytest.mark.parametrize("Hq,Hkv,D", [(4, 4, 128), (8, 2, 128), (16, 8, 64), (2, 1, 64)])
+@pytest.mark.parametrize("Hq,Hkv,D", [(4, 4, 128), (8, 2, 128), (16, 8, 64), (2, 1, 64), (4, 2, 32), (8, 2, 16),
+                                     (4, 4, 16)])
 def test_prefill_shapes(sa, oracle, synth, Hq, Hkv, D):
     L = 300
     q, k, v = inputs(synth, L, Hq, Hkv, D, seed=52)
@@ -200,3 +201,16 @@ def test_prefill_scale_sign(sa, oracle, synth, monkeypatch, scale, bf16, waves):
         cum = np.cumsum(v.astype(np.float64), axis=2) / np.arange(1, L + 1)[:, None]
         assert np.abs(out[:, ::2] - cum).max() <= (2e-2 if bf16 else 1e-5)
 
+
+
+def test_prefill_head_dim_limits(sa, synth):
+    """fp32 prefill takes head_dim 16 .. 128, bf16 64 and 128; others are
+    refused before any launch (out keeps its contents)."""
+    for D, bf16 in [(8, False), (256, False), (32, True), (16, True), (96, False)]:
+        q = torch.zeros(1, 2, 10, D, device="cuda")
+        t = (lambda a: a.to(torch.bfloat16)) if bf16 else (lambda a: a)
+        out = torch.full((1, 2, 10, D), 3.0, device="cuda")
+        with pytest.raises(sa.SaError) as e:
+            sa.prefill_causal(t(q), t(q), t(q), 0.1, out=out)
+        assert e.value.status == sa.SA_EINVAL
+        assert bool((out == 3.0).all())

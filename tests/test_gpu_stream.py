@@ -75,7 +75,7 @@ def test_long_context(sa, oracle, T):
         assert rel_l2(out, f64) <= max(2 * rel_l2(want, f64), 2e-6)
 
 
-@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("d", [8, 16, 32, 64, 128, 256])
 def test_ragged_lengths(sa, oracle, synth, d):
     for T in (1, 2, 15, 16, 17, 63, 64, 65, 255, 257, 1000, 4097):
         Q, K, V = synth.stream_inputs(T, d, seed=100 + T)
@@ -102,7 +102,7 @@ def test_chunk_override_matches(sa, oracle, monkeypatch):
 
 
 @pytest.mark.parametrize("Hq,Hkv", [(16, 8), (8, 8), (16, 4), (8, 1)])
-@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("D", [8, 16, 32, 64, 128, 256])
 def test_dense_gqa_decode(sa, oracle, synth, Hq, Hkv, D):
     B = 3
     for T in (1, 100, 3000):
