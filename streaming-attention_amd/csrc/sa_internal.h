@@ -77,6 +77,13 @@ __device__ __forceinline__ float swz_xor(float v) {
 __device__ __forceinline__ float swz_xor16(float v) { return swz_xor<16>(v); }
 __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
 
+// Workgroup barrier that orders LDS accesses only.  __syncthreads() also
+// waits for every outstanding global access of the wave (s_waitcnt
+// vmcnt(0)), which drains loads issued ahead of their use; here they stay in
+// flight and the compiler waits for each where its value is used.  For
+// kernels whose waves exchange data through LDS only.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 struct OpSum { __device__ static float apply(float a, float b) { return a + b; } };
 struct OpMax { __device__ static float apply(float a, float b) { return fmaxf(a, b); } };
 
