@@ -192,19 +192,21 @@ gemm_xwt_kernel(const float* __restrict__ X, int M, int K, const uint16_t* __res
     const uint16_t* Wl = W + (size_t)(n0 + r16) * K + k_begin + 8 * g;
     auto load_w = [&](int j) { return *reinterpret_cast<const bf16x8_t*>(Wl + j * kGK); };
     // X block of step j: thread t converts X[m0 + t / 4][k + 8 (t % 4) .. + 7].
+    // Rows past M load row M - 1 and are zeroed when converted.  Every load of
+    // the loop below is issued unconditionally (steps past the last clamp to
+    // it): a load behind a branch leaves the compiler unable to count the
+    // loads in flight, and it then waits for all of them (vmcnt(0)) before
+    // the first use of any, which drains the prefetch rings every step.
     const int xr = tid >> 2, xc = 8 * (tid & 3);
     const bool x_on = xr < Mt;
-    const float* Xl = X + (size_t)(m0 + xr) * K + k_begin + xc;
+    const float* Xl = X + (size_t)(m0 + min(xr, Mt - 1)) * K + k_begin + xc;
     auto load_x = [&](int j, f32x4_t& a, f32x4_t& b) {
-        if (x_on) {
-            a = *reinterpret_cast<const f32x4_t*>(Xl + j * kGK);
-            b = *reinterpret_cast<const f32x4_t*>(Xl + j * kGK + 4);
-        } else {
-            a = f32x4_t{};
-            b = f32x4_t{};
-        }
+        a = *reinterpret_cast<const f32x4_t*>(Xl + j * kGK);
+        b = *reinterpret_cast<const f32x4_t*>(Xl + j * kGK + 4);
     };
     auto store_x = [&](int buf, f32x4_t a, f32x4_t b) {
+        a = x_on ? a : f32x4_t{};
+        b = x_on ? b : f32x4_t{};
         f32x2_t v[4] = {{a[0], a[1]}, {a[2], a[3]}, {b[0], b[1]}, {b[2], b[3]}};
 #pragma unroll
         for (int t = 0; t < kGemmTerms; ++t) {
@@ -220,17 +222,20 @@ gemm_xwt_kernel(const float* __restrict__ X, int M, int K, const uint16_t* __res
         }
     };
 
+    const int last = nsteps - 1;
     bf16x8_t ring[kGemmRing];
 #pragma unroll
-    for (int u = 0; u < kGemmRing; ++u)
-        if (u < nsteps) ring[u] = load_w(u);
-    // acc[mt]: element i is row m0 + 16 mt + r16, column n0 + 4 g + i
+    for (int u = 0; u < kGemmRing; ++u) ring[u] = load_w(min(u, last));
+    // acc[mt]: element i is row m0 + 16 mt + r16, column n0 + 4 g + i.  Term
+    // by term, the four row blocks in turn: consecutive MFMAs write
+    // different accumulators (each accumulator still adds its terms in
+    // order 0, 1, 2).
     f32x4_t acc[kMaxRows / 16] = {};
     auto mfma_step = [&](const bf16x8_t& wf, int buf) {
 #pragma unroll
-        for (int mt = 0; mt < kMaxRows / 16; ++mt)
+        for (int t = 0; t < kGemmTerms; ++t)
 #pragma unroll
-            for (int t = 0; t < kGemmTerms; ++t) {
+            for (int mt = 0; mt < kMaxRows / 16; ++mt) {
                 const bf16x8_t xf = *reinterpret_cast<const bf16x8_t*>(&Xb[buf][t][16 * mt + r16][8 * g]);
                 acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf, xf, acc[mt], 0, 0, 0);
             }
@@ -239,29 +244,36 @@ gemm_xwt_kernel(const float* __restrict__ X, int M, int K, const uint16_t* __res
     // xr_a/xr_b[i]: the X block of the step s with s % kGemmXRing == i.
     f32x4_t xr_a[kGemmXRing], xr_b[kGemmXRing];
 #pragma unroll
-    for (int i = 0; i < kGemmXRing; ++i)
-        if (i < nsteps) load_x(i, xr_a[i], xr_b[i]);
+    for (int i = 0; i < kGemmXRing; ++i) load_x(min(i, last), xr_a[i], xr_b[i]);
     store_x(0, xr_a[0], xr_b[0]);
     __syncthreads();
 
-    for (int j0 = 0; j0 < nsteps; j0 += kGemmRing) {
+    // Step j = j0 + u, with u = j % kGemmRing known at compile time.
+    auto step = [&](int j, int u) {
+        const int buf = u & 1;       // kGemmRing is even, so j & 1 == u & 1
+        const bf16x8_t wf = ring[u];
+        ring[u] = load_w(min(j + kGemmRing, last));
+        mfma_step(wf, buf);
+        // the other buffer was last read before the previous barrier
+        const int nx = (u + 1) % kGemmXRing;
+        if (j + 1 < nsteps) store_x(buf ^ 1, xr_a[nx], xr_b[nx]);
+        // slot u % kGemmXRing held step j, stored one step ago
+        const int cx = u % kGemmXRing;
+        load_x(min(j + kGemmXRing, last), xr_a[cx], xr_b[cx]);
+        lds_barrier();
+    };
+    // Whole groups of kGemmRing steps with no exit inside (an exit after each
+    // step made the compiler wait there for the loads its epilogue's
+    // registers were still receiving), then the last partial group.
+    const int full = nsteps / kGemmRing * kGemmRing;
+    for (int j0 = 0; j0 < full; j0 += kGemmRing) {
 #pragma unroll
-        for (int u = 0; u < kGemmRing; ++u) {
-            const int j = j0 + u;
-            if (j < nsteps) {
-                const int buf = u & 1;   // kGemmRing is even, so j & 1 == u & 1
-                const bf16x8_t wf = ring[u];
-                if (j + kGemmRing < nsteps) ring[u] = load_w(j + kGemmRing);
-                mfma_step(wf, buf);
-                // the other buffer was last read before the previous barrier
-                const int nx = (u + 1) % kGemmXRing;
-                if (j + 1 < nsteps) store_x(buf ^ 1, xr_a[nx], xr_b[nx]);
-                // slot u % kGemmXRing held step j, stored one step ago
-                const int cx = u % kGemmXRing;
-                if (j + kGemmXRing < nsteps) load_x(j + kGemmXRing, xr_a[cx], xr_b[cx]);
-                lds_barrier();
-            }
-        }
+        for (int u = 0; u < kGemmRing; ++u) step(j0 + u, u);
+    }
+#pragma unroll
+    for (int u = 0; u < kGemmRing; ++u) {
+        if (full + u >= nsteps) break;
+        step(full + u, u);
     }
     float* out = P + (size_t)blockIdx.y * M * N + (size_t)m0 * N + n0 + 4 * g;
 #pragma unroll
