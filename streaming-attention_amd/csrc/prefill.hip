@@ -1082,7 +1082,14 @@ prefill_f32_kernel(PrefillArgs pa) {
 // feeding two MFMAs) measured 272-275 us at L = 8192 against 261-273 us for
 // the 8-wave ping-pong kernel on the same box: its dependency stalls fell
 // (28 % of wave cycles waiting against 43 %) but the single wave spent 45 %
-// of its cycles issuing VALU, AGPR reads of the scores included.
+// of its cycles issuing VALU, AGPR reads of the scores included.  With the
+// accumulators and scores in VGPRs instead (one wave per SIMD holding 32
+// queries of both heads of a KV group, the two heads' blocks pipelined so
+// that one head's softmax runs under the other's MFMAs, K and V^T fragments
+// read right before each MFMA): bit-exact with the ping-pong kernel, but
+// 372 us at L = 8192 and 175 us at L = 4096 against 246 and 106 us.  The
+// O accumulators and q of two heads (192 registers) left no room to read
+// fragments ahead, so every MFMA waited for its own LDS read.
 constexpr int kBfQB = 1;
 constexpr int kBfW = 8;
 constexpr int kBfWSmall = 4;
