@@ -1063,6 +1063,167 @@ prefill_f32_kernel(PrefillArgs pa) {
     }
 }
 
+// fp32, short prompts: a workgroup serves 32 queries of one head, and its 4
+// waves split every staged 64-key tile, wave w taking keys 16 w .. 16 w + 15
+// (with 128-query workgroups a 512-token prompt of 16 heads fills 64 CUs,
+// and one wave's tile of 32 queries x 64 keys is ~7 us of fp32 MFMA work).
+// Each wave keeps its own (m, l, O) over its keys; a block a wave sees fully
+// masked leaves m at -inf, so the softmax subtracts 0 in its place.  At the
+// end waves 1-3 leave their partials in LDS and wave 0 merges them (O =
+// sum 2^(m_w - M) O_w, l likewise, M the largest m_w) and writes the output.
+template <int D>
+__global__ void __launch_bounds__(kFThreads)
+prefill_f32_split_kernel(PrefillArgs pa) {
+    using Lds = F32Lds<D>;
+    const int L = pa.L;
+    const float sl2 = pa.scale * kLog2eP;
+    constexpr int NDB = D / 16;
+    constexpr int QF = D / 4;
+    extern __shared__ __align__(16) unsigned char smem[];
+    float* stage_base = reinterpret_cast<float*>(smem);
+
+    const Work wk = map_work(pa, blockIdx.x);
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int g = lane >> 4;
+    const int c16 = lane & 15;
+
+    const float* Q = static_cast<const float*>(pa.q) + wk.b * pa.qs[0] + wk.h0 * pa.qs[1];
+    const float* K = static_cast<const float*>(pa.k) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
+    const float* V = static_cast<const float*>(pa.v) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
+    const long long q_row = pa.qs[2], kv_row = pa.kvs[2];
+
+    const int q0 = wk.qt * 32;
+    const int n_kt = (min(L, q0 + 32) - 1) / kKTile + 1;
+
+    F32Stage<D> next;
+    f32_load<D>(next, K, V, kv_row, 0, L);
+
+    float qf[2][QF];
+#pragma unroll
+    for (int gq = 0; gq < 2; ++gq) {
+        const int qi = min(q0 + gq * 16 + c16, L - 1);
+#pragma unroll
+        for (int s = 0; s < QF; ++s) qf[gq][s] = Q[qi * q_row + s * 4 + g];
+    }
+
+    f32x4_t acc[2][NDB];
+#pragma unroll
+    for (int gq = 0; gq < 2; ++gq)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) acc[gq][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float m_run[2] = {-INFINITY, -INFINITY};
+    float l_run[2] = {0.f, 0.f};
+
+    f32_store<D>(next, stage_base, stage_base + Lds::K_ELEMS);
+    __syncthreads();
+
+    for (int kt = 0; kt < n_kt; ++kt) {
+        const float* sK = stage_base + (kt & 1) * Lds::STAGE;
+        const float* sV = sK + Lds::K_ELEMS;
+        const bool more = kt + 1 < n_kt;
+        if (more) f32_load<D>(next, K, V, kv_row, (kt + 1) * kKTile, L);
+
+        const int kb0 = kt * kKTile + wave * 16;   // this wave's first key
+        if (kb0 <= q0 + 31) {                      // else above every query of the workgroup
+            const bool diag = kb0 + 15 > q0;
+#pragma unroll
+            for (int gq = 0; gq < 2; ++gq) {
+                const int qi = q0 + gq * 16 + c16;
+                f32x4_t s = {0.f, 0.f, 0.f, 0.f};
+                const float* krow = sK + (wave * 16 + c16) * Lds::K_STRIDE;
+#pragma unroll
+                for (int ks = 0; ks < QF; ++ks) s = __builtin_amdgcn_mfma_f32_16x16x4f32(krow[ks * 4 + g], qf[gq][ks], s, 0, 0, 0);
+                float mt = -INFINITY;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float sv = s[i] * sl2;
+                    if (diag && kb0 + g * 4 + i > qi) sv = -INFINITY;
+                    s[i] = sv;
+                    mt = fmaxf(mt, sv);
+                }
+                mt = xmax16_32(mt);
+                const float m_new = fmaxf(m_run[gq], mt);
+                const float m_use = m_new == -INFINITY ? 0.f : m_new;
+                const float alpha = __builtin_amdgcn_exp2f(m_run[gq] - m_use);
+                float rs = 0.f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float p = __builtin_amdgcn_exp2f(s[i] - m_use);
+                    s[i] = p;
+                    rs += p;
+                }
+                rs = xsum16_32(rs);
+                l_run[gq] = l_run[gq] * alpha + rs;
+                m_run[gq] = m_new;
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) acc[gq][db] *= alpha;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float* vrow = sV + (wave * 16 + g * 4 + i) * Lds::V_STRIDE;
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db)
+                        acc[gq][db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vrow[db * 16 + c16], s[i], acc[gq][db], 0, 0, 0);
+                }
+            }
+        }
+        if (more) {
+            // The other stage was last read before the previous iteration's barrier.
+            float* nK = stage_base + ((kt + 1) & 1) * Lds::STAGE;
+            f32_store<D>(next, nK, nK + Lds::K_ELEMS);
+        }
+        __syncthreads();
+    }
+
+    // Partials of waves 1-3 into LDS, [element][lane] per wave.
+    constexpr int NE = 2 * NDB * 4 + 4;
+    float* const part = stage_base;
+    if (wave > 0) {
+        float* p = part + (wave - 1) * NE * 64 + lane;
+#pragma unroll
+        for (int gq = 0; gq < 2; ++gq) {
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) p[((gq * NDB + db) * 4 + i) * 64] = acc[gq][db][i];
+            p[(NE - 4 + gq) * 64] = m_run[gq];
+            p[(NE - 2 + gq) * 64] = l_run[gq];
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    // Wave 0 always holds key 0, so its m is finite.
+#pragma unroll
+    for (int o = 0; o < 3; ++o) {
+        const float* p = part + o * NE * 64 + lane;
+#pragma unroll
+        for (int gq = 0; gq < 2; ++gq) {
+            const float mo = p[(NE - 4 + gq) * 64], lo = p[(NE - 2 + gq) * 64];
+            const float m = fmaxf(m_run[gq], mo);
+            const float a = __builtin_amdgcn_exp2f(m_run[gq] - m);
+            const float b = mo == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mo - m);
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    acc[gq][db][i] = acc[gq][db][i] * a + p[((gq * NDB + db) * 4 + i) * 64] * b;
+            l_run[gq] = l_run[gq] * a + lo * b;
+            m_run[gq] = m;
+        }
+    }
+#pragma unroll
+    for (int gq = 0; gq < 2; ++gq) {
+        const int qi = q0 + gq * 16 + c16;
+        if (qi >= L) continue;
+        const float inv = 1.0f / l_run[gq];
+        float* orow = pa.out + wk.b * pa.os[0] + wk.h0 * pa.os[1] + qi * pa.os[2];
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+            *reinterpret_cast<float4*>(orow + db * 16 + g * 4) =
+                make_float4(acc[gq][db][0] * inv, acc[gq][db][1] * inv, acc[gq][db][2] * inv, acc[gq][db][3] * inv);
+    }
+}
+
 // ===========================================================================
 // Launch
 // ===========================================================================
@@ -1143,6 +1304,13 @@ sa_status launch_f32(const PrefillArgs& pa, dim3 grid, hipStream_t st) {
     return s;
 }
 
+template <int D>
+sa_status launch_f32_split(const PrefillArgs& pa, dim3 grid, hipStream_t st) {
+    sa_status s = opt_in_lds<&prefill_f32_split_kernel<D>>(F32Lds<D>::BYTES);
+    if (s == SA_OK) hipLaunchKernelGGL(prefill_f32_split_kernel<D>, grid, dim3(kFThreads), F32Lds<D>::BYTES, st, pa);
+    return s;
+}
+
 // Workgroups of W waves serve gh = gcd(Hq / Hkv, W) query heads, W / gh
 // waves of 32 queries per head.
 long long bf16_grid(const PrefillArgs& pa, int B, int W) {
@@ -1178,6 +1346,31 @@ sa_status launch(PrefillArgs pa, int B, bool bf16, int D, hipStream_t st) {
         const long long n_wg = (long long)B * (pa.Hq / pa.gh) * pa.n_qt;
         if (n_wg > 0x7fffffffLL) return fail(SA_ERANGE, "prefill grid too large");
         const sa_status s = launch_bf16_split(pa, dim3(static_cast<unsigned>(n_wg)), st);
+        if (s != SA_OK) return s;
+        SA_CHECK_LAUNCH();
+        return SA_OK;
+    }
+    // fp32: 32-query workgroups whose waves split each tile's keys while
+    // 128-query ones would give fewer than two workgroups per CU.  Measured
+    // (16/8 heads, D = 128, graph-replayed calls): L = 128 / 512 / 1024 /
+    // 2048 take 17.2 / 38.3 / 78.8 / 266.6 us against 29.0 / 87.2 / 164.8 /
+    // 320.8 us with 128-query workgroups; L = 4096 978 against 680 us.
+    if (!bf16 && (fsplit ? std::atoi(fsplit) != 0
+                         : (long long)B * pa.Hq * ((pa.L + kFQTile - 1) / kFQTile) < 2LL * device_cu_count())) {
+        pa.gh = 1;
+        pa.n_qt = (pa.L + 31) / 32;
+        const int groups = B * pa.Hkv;
+        pa.xcd_groups = groups % 8 == 0 ? groups / 8 : 0;
+        const long long n_wg = (long long)B * pa.Hq * pa.n_qt;
+        if (n_wg > 0x7fffffffLL) return fail(SA_ERANGE, "prefill grid too large");
+        const dim3 grid(static_cast<unsigned>(n_wg));
+        sa_status s = SA_OK;
+        switch (D) {
+            case 16: s = launch_f32_split<16>(pa, grid, st); break;
+            case 32: s = launch_f32_split<32>(pa, grid, st); break;
+            case 64: s = launch_f32_split<64>(pa, grid, st); break;
+            default: s = launch_f32_split<128>(pa, grid, st); break;
+        }
         if (s != SA_OK) return s;
         SA_CHECK_LAUNCH();
         return SA_OK;

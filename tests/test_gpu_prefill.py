@@ -36,7 +36,9 @@ def inputs(synth, L, Hq=16, Hkv=8, D=128, seed=50):
             synth.normal(seed, 3, (1, Hkv, L, D)))
 
 
-def test_prefill_golden(sa):
+@pytest.mark.parametrize("kernel", ["split", "unsplit"])
+def test_prefill_golden(sa, monkeypatch, kernel):
+    f32_variant(monkeypatch, kernel)
     meta, g = gi.load("prefill")
     q, k, v = gi.prefill_inputs()
     rows = np.array(meta["rows"])
@@ -46,8 +48,22 @@ def test_prefill_golden(sa):
         assert rel_l2(out, g[key]) <= 1e-5
 
 
+def f32_variant(monkeypatch, v):
+    """The fp32 kernel a launch takes: "split" the one whose 32-query
+    workgroups split each key tile over their four waves, "unsplit" the
+    128-query one, "default" the launch's own choice (split while 128-query
+    workgroups would give fewer than two per CU)."""
+    monkeypatch.delenv("SA_PREFILL_WAVES", raising=False)
+    if v == "default":
+        monkeypatch.delenv("SA_PREFILL_SPLIT", raising=False)
+    else:
+        monkeypatch.setenv("SA_PREFILL_SPLIT", "1" if v == "split" else "0")
+
+
+@pytest.mark.parametrize("kernel", ["default", "split", "unsplit"])
 @pytest.mark.parametrize("L", [1, 17, 128, 200, 1024])
-def test_prefill_fp32(sa, oracle, synth, L):
+def test_prefill_fp32(sa, oracle, synth, monkeypatch, L, kernel):
+    f32_variant(monkeypatch, kernel)
     q, k, v = inputs(synth, L)
     sc = np.float32(1 / np.sqrt(128))
     out = host(sa.prefill_causal(dev(q), dev(k), dev(v), float(sc)))
@@ -105,9 +121,11 @@ def test_prefill_bf16(sa, oracle, synth, L, rope):
     assert rel_l2(out[:, :, rows], want) <= 2e-2
 
 
+@pytest.mark.parametrize("kernel", ["split", "unsplit"])
 @pytest.mark.parametrize("Hq,Hkv,D", [(4, 4, 128), (8, 2, 128), (16, 8, 64), (2, 1, 64), (4, 2, 32), (8, 2, 16),
                                      (4, 4, 16)])
-def test_prefill_shapes(sa, oracle, synth, Hq, Hkv, D):
+def test_prefill_shapes(sa, oracle, synth, monkeypatch, Hq, Hkv, D, kernel):
+    f32_variant(monkeypatch, kernel)
     L = 300
     q, k, v = inputs(synth, L, Hq, Hkv, D, seed=52)
     q2 = np.concatenate([q, synth.normal(53, 1, q.shape)], 0)     # batch 2
@@ -120,8 +138,10 @@ def test_prefill_shapes(sa, oracle, synth, Hq, Hkv, D):
     assert rel_l2(out, want) <= 1e-5
 
 
-def test_prefill_last_row_is_decode(sa, synth):
+@pytest.mark.parametrize("kernel", ["split", "unsplit"])
+def test_prefill_last_row_is_decode(sa, synth, monkeypatch, kernel):
     """Row L-1 of the prefill equals a decode step over all L keys."""
+    f32_variant(monkeypatch, kernel)
     L = 777
     q, k, v = inputs(synth, L, seed=54)
     sc = float(1 / np.sqrt(128))
