@@ -866,6 +866,7 @@ prefill_bf16_split_kernel(PrefillArgs pa) {
 // ===========================================================================
 constexpr int kFQTile = 128;    // queries per workgroup
 constexpr int kFThreads = 256;
+constexpr int kF32SplitW = 8;   // waves of the short-prompt fp32 kernel
 
 template <int D>
 struct F32Lds {
@@ -875,35 +876,37 @@ struct F32Lds {
     static constexpr int STAGE = K_ELEMS + kKTile * V_STRIDE;   // floats per stage
     static constexpr int BYTES = 2 * STAGE * 4;
     static constexpr int CPR = D / 4;                // 16-byte chunks per row
-    static constexpr int NK = kKTile * CPR / kFThreads;
 };
 
-template <int D>
+// Register staging of one K/V tile, spread over the NT threads of a workgroup.
+template <int D, int NT = kFThreads>
 struct F32Stage {
-    u32x4_t k[F32Lds<D>::NK];
-    u32x4_t v[F32Lds<D>::NK];
+    static constexpr int NK = kKTile * (D / 4) / NT;
+    static_assert(NK >= 1 && NK * NT == kKTile * (D / 4), "tile chunks per thread");
+    u32x4_t k[NK];
+    u32x4_t v[NK];
 };
 
-template <int D>
-__device__ __forceinline__ void f32_load(F32Stage<D>& st, const float* K, const float* V, long long kv_row,
+template <int D, int NT>
+__device__ __forceinline__ void f32_load(F32Stage<D, NT>& st, const float* K, const float* V, long long kv_row,
                                          int key0, int L) {
     using Lds = F32Lds<D>;
     const int rmax = L - 1 - key0;
 #pragma unroll
-    for (int i = 0; i < Lds::NK; ++i) {
-        const int idx = threadIdx.x + i * kFThreads;
+    for (int i = 0; i < F32Stage<D, NT>::NK; ++i) {
+        const int idx = threadIdx.x + i * NT;
         const long long off = min(idx / Lds::CPR, rmax) * kv_row + (idx % Lds::CPR) * 4;
         st.k[i] = *reinterpret_cast<const u32x4_t*>(K + key0 * kv_row + off);
         st.v[i] = *reinterpret_cast<const u32x4_t*>(V + key0 * kv_row + off);
     }
 }
 
-template <int D>
-__device__ __forceinline__ void f32_store(const F32Stage<D>& st, float* sK, float* sV) {
+template <int D, int NT>
+__device__ __forceinline__ void f32_store(const F32Stage<D, NT>& st, float* sK, float* sV) {
     using Lds = F32Lds<D>;
 #pragma unroll
-    for (int i = 0; i < Lds::NK; ++i) {
-        const int idx = threadIdx.x + i * kFThreads;
+    for (int i = 0; i < F32Stage<D, NT>::NK; ++i) {
+        const int idx = threadIdx.x + i * NT;
         const int r = idx / Lds::CPR, c = (idx % Lds::CPR) * 4;
         *reinterpret_cast<u32x4_t*>(sK + r * Lds::K_STRIDE + c) = st.k[i];
         *reinterpret_cast<u32x4_t*>(sV + r * Lds::V_STRIDE + c) = st.v[i];
@@ -1063,18 +1066,24 @@ prefill_f32_kernel(PrefillArgs pa) {
     }
 }
 
-// fp32, short prompts: a workgroup serves 32 queries of one head, and its 4
-// waves split every staged 64-key tile, wave w taking keys 16 w .. 16 w + 15
+// fp32, short prompts: a workgroup serves 32 queries of one head, and its
+// waves split every staged 64-key tile, each taking one 16-key block of it
 // (with 128-query workgroups a 512-token prompt of 16 heads fills 64 CUs,
 // and one wave's tile of 32 queries x 64 keys is ~7 us of fp32 MFMA work).
-// Each wave keeps its own (m, l, O) over its keys; a block a wave sees fully
-// masked leaves m at -inf, so the softmax subtracts 0 in its place.  At the
-// end waves 1-3 leave their partials in LDS and wave 0 merges them (O =
-// sum 2^(m_w - M) O_w, l likewise, M the largest m_w) and writes the output.
-template <int D>
-__global__ void __launch_bounds__(kFThreads)
+// With W = 8 waves, waves 0-3 serve queries 0-15 and waves 4-7 queries
+// 16-31 (two waves per SIMD); with W = 4 each wave serves all 32.  Each wave
+// keeps its own (m, l, O) over its keys; a block a wave sees fully masked
+// leaves m at -inf, so the softmax subtracts 0 in its place.  At the end the
+// waves of blocks 1-3 leave their partials in LDS and the wave of block 0
+// merges them (O = sum 2^(m_w - M) O_w, l likewise, M the largest m_w) and
+// writes the output.
+template <int D, int W>
+__global__ void __launch_bounds__(W * 64)
 prefill_f32_split_kernel(PrefillArgs pa) {
+    static_assert(W == 4 || W == 8, "4 or 8 waves");
     using Lds = F32Lds<D>;
+    constexpr int NT = W * 64;
+    constexpr int GW = 8 / W;               // 16-query groups per wave
     const int L = pa.L;
     const float sl2 = pa.scale * kLog2eP;
     constexpr int NDB = D / 16;
@@ -1085,6 +1094,8 @@ prefill_f32_split_kernel(PrefillArgs pa) {
     const Work wk = map_work(pa, blockIdx.x);
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
+    const int blk = wave & 3;               // 16-key block of each tile
+    const int qset = wave >> 2;             // which 16 queries (W = 8)
     const int g = lane >> 4;
     const int c16 = lane & 15;
 
@@ -1094,44 +1105,47 @@ prefill_f32_split_kernel(PrefillArgs pa) {
     const long long q_row = pa.qs[2], kv_row = pa.kvs[2];
 
     const int q0 = wk.qt * 32;
+    const int qw0 = q0 + qset * 16 * GW;    // this wave's first query
     const int n_kt = (min(L, q0 + 32) - 1) / kKTile + 1;
 
-    F32Stage<D> next;
-    f32_load<D>(next, K, V, kv_row, 0, L);
+    F32Stage<D, NT> next;
+    f32_load<D, NT>(next, K, V, kv_row, 0, L);
 
-    float qf[2][QF];
+    float qf[GW][QF];
 #pragma unroll
-    for (int gq = 0; gq < 2; ++gq) {
-        const int qi = min(q0 + gq * 16 + c16, L - 1);
+    for (int gq = 0; gq < GW; ++gq) {
+        const int qi = min(qw0 + gq * 16 + c16, L - 1);
 #pragma unroll
         for (int s = 0; s < QF; ++s) qf[gq][s] = Q[qi * q_row + s * 4 + g];
     }
 
-    f32x4_t acc[2][NDB];
+    f32x4_t acc[GW][NDB];
+    float m_run[GW], l_run[GW];
 #pragma unroll
-    for (int gq = 0; gq < 2; ++gq)
+    for (int gq = 0; gq < GW; ++gq) {
 #pragma unroll
         for (int db = 0; db < NDB; ++db) acc[gq][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    float m_run[2] = {-INFINITY, -INFINITY};
-    float l_run[2] = {0.f, 0.f};
+        m_run[gq] = -INFINITY;
+        l_run[gq] = 0.f;
+    }
 
-    f32_store<D>(next, stage_base, stage_base + Lds::K_ELEMS);
+    f32_store<D, NT>(next, stage_base, stage_base + Lds::K_ELEMS);
     __syncthreads();
 
     for (int kt = 0; kt < n_kt; ++kt) {
         const float* sK = stage_base + (kt & 1) * Lds::STAGE;
         const float* sV = sK + Lds::K_ELEMS;
         const bool more = kt + 1 < n_kt;
-        if (more) f32_load<D>(next, K, V, kv_row, (kt + 1) * kKTile, L);
+        if (more) f32_load<D, NT>(next, K, V, kv_row, (kt + 1) * kKTile, L);
 
-        const int kb0 = kt * kKTile + wave * 16;   // this wave's first key
-        if (kb0 <= q0 + 31) {                      // else above every query of the workgroup
-            const bool diag = kb0 + 15 > q0;
+        const int kb0 = kt * kKTile + blk * 16;   // this wave's first key
+        if (kb0 <= qw0 + 16 * GW - 1) {           // else above every query of the wave
+            const bool diag = kb0 + 15 > qw0;
 #pragma unroll
-            for (int gq = 0; gq < 2; ++gq) {
-                const int qi = q0 + gq * 16 + c16;
+            for (int gq = 0; gq < GW; ++gq) {
+                const int qi = qw0 + gq * 16 + c16;
                 f32x4_t s = {0.f, 0.f, 0.f, 0.f};
-                const float* krow = sK + (wave * 16 + c16) * Lds::K_STRIDE;
+                const float* krow = sK + (blk * 16 + c16) * Lds::K_STRIDE;
 #pragma unroll
                 for (int ks = 0; ks < QF; ++ks) s = __builtin_amdgcn_mfma_f32_16x16x4f32(krow[ks * 4 + g], qf[gq][ks], s, 0, 0, 0);
                 float mt = -INFINITY;
@@ -1160,7 +1174,7 @@ prefill_f32_split_kernel(PrefillArgs pa) {
                 for (int db = 0; db < NDB; ++db) acc[gq][db] *= alpha;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float* vrow = sV + (wave * 16 + g * 4 + i) * Lds::V_STRIDE;
+                    const float* vrow = sV + (blk * 16 + g * 4 + i) * Lds::V_STRIDE;
 #pragma unroll
                     for (int db = 0; db < NDB; ++db)
                         acc[gq][db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vrow[db * 16 + c16], s[i], acc[gq][db], 0, 0, 0);
@@ -1170,35 +1184,35 @@ prefill_f32_split_kernel(PrefillArgs pa) {
         if (more) {
             // The other stage was last read before the previous iteration's barrier.
             float* nK = stage_base + ((kt + 1) & 1) * Lds::STAGE;
-            f32_store<D>(next, nK, nK + Lds::K_ELEMS);
+            f32_store<D, NT>(next, nK, nK + Lds::K_ELEMS);
         }
         __syncthreads();
     }
 
-    // Partials of waves 1-3 into LDS, [element][lane] per wave.
-    constexpr int NE = 2 * NDB * 4 + 4;
+    // Partials of the waves of blocks 1-3 into LDS, [element][lane] per wave.
+    constexpr int NE = GW * (NDB * 4 + 2);
     float* const part = stage_base;
-    if (wave > 0) {
-        float* p = part + (wave - 1) * NE * 64 + lane;
+    if (blk > 0) {
+        float* p = part + (qset * 3 + blk - 1) * NE * 64 + lane;
 #pragma unroll
-        for (int gq = 0; gq < 2; ++gq) {
+        for (int gq = 0; gq < GW; ++gq) {
 #pragma unroll
             for (int db = 0; db < NDB; ++db)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) p[((gq * NDB + db) * 4 + i) * 64] = acc[gq][db][i];
-            p[(NE - 4 + gq) * 64] = m_run[gq];
-            p[(NE - 2 + gq) * 64] = l_run[gq];
+            p[(GW * NDB * 4 + gq) * 64] = m_run[gq];
+            p[(GW * NDB * 4 + GW + gq) * 64] = l_run[gq];
         }
     }
     __syncthreads();
-    if (wave != 0) return;
-    // Wave 0 always holds key 0, so its m is finite.
+    if (blk != 0) return;
+    // Block 0 holds key 0, so this wave's m is finite.
 #pragma unroll
     for (int o = 0; o < 3; ++o) {
-        const float* p = part + o * NE * 64 + lane;
+        const float* p = part + (qset * 3 + o) * NE * 64 + lane;
 #pragma unroll
-        for (int gq = 0; gq < 2; ++gq) {
-            const float mo = p[(NE - 4 + gq) * 64], lo = p[(NE - 2 + gq) * 64];
+        for (int gq = 0; gq < GW; ++gq) {
+            const float mo = p[(GW * NDB * 4 + gq) * 64], lo = p[(GW * NDB * 4 + GW + gq) * 64];
             const float m = fmaxf(m_run[gq], mo);
             const float a = __builtin_amdgcn_exp2f(m_run[gq] - m);
             const float b = mo == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mo - m);
@@ -1212,8 +1226,8 @@ prefill_f32_split_kernel(PrefillArgs pa) {
         }
     }
 #pragma unroll
-    for (int gq = 0; gq < 2; ++gq) {
-        const int qi = q0 + gq * 16 + c16;
+    for (int gq = 0; gq < GW; ++gq) {
+        const int qi = qw0 + gq * 16 + c16;
         if (qi >= L) continue;
         const float inv = 1.0f / l_run[gq];
         float* orow = pa.out + wk.b * pa.os[0] + wk.h0 * pa.os[1] + qi * pa.os[2];
@@ -1304,10 +1318,13 @@ sa_status launch_f32(const PrefillArgs& pa, dim3 grid, hipStream_t st) {
     return s;
 }
 
+// 8 waves (two per SIMD) where the tile's chunks cover 512 threads, else 4.
 template <int D>
 sa_status launch_f32_split(const PrefillArgs& pa, dim3 grid, hipStream_t st) {
-    sa_status s = opt_in_lds<&prefill_f32_split_kernel<D>>(F32Lds<D>::BYTES);
-    if (s == SA_OK) hipLaunchKernelGGL(prefill_f32_split_kernel<D>, grid, dim3(kFThreads), F32Lds<D>::BYTES, st, pa);
+    constexpr int W = D >= 32 ? kF32SplitW : 4;
+    sa_status s = opt_in_lds<&prefill_f32_split_kernel<D, W>>(F32Lds<D>::BYTES);
+    if (s == SA_OK)
+        hipLaunchKernelGGL((prefill_f32_split_kernel<D, W>), grid, dim3(W * 64), F32Lds<D>::BYTES, st, pa);
     return s;
 }
 
@@ -1353,8 +1370,10 @@ sa_status launch(PrefillArgs pa, int B, bool bf16, int D, hipStream_t st) {
     // fp32: 32-query workgroups whose waves split each tile's keys while
     // 128-query ones would give fewer than two workgroups per CU.  Measured
     // (16/8 heads, D = 128, graph-replayed calls): L = 128 / 512 / 1024 /
-    // 2048 take 17.2 / 38.3 / 78.8 / 266.6 us against 29.0 / 87.2 / 164.8 /
-    // 320.8 us with 128-query workgroups; L = 4096 978 against 680 us.
+    // 2048 take 16.0 / 35.3 / 72.4 / 245.7 us against 29.0 / 86.9 / 164.3 /
+    // 319.5 us with 128-query workgroups (4 waves per 32-query workgroup
+    // instead of 8: 17.3 / 38.3 / 78.4 / 266.6 us); L = 4096 896 against
+    // 681 us.
     if (!bf16 && (fsplit ? std::atoi(fsplit) != 0
                          : (long long)B * pa.Hq * ((pa.L + kFQTile - 1) / kFQTile) < 2LL * device_cu_count())) {
         pa.gh = 1;
