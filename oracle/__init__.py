@@ -57,6 +57,7 @@ _REF_SIGS = {
     "ref_rotary": (_I, [_P, _I, _I, _I, _I, _I, _F, _I, _P]),
     "ref_argmax": (C.c_long, [_P, _P, _I, _I, _I, _P, C.c_long, _P, _P]),
     "ref_cross_attention": (None, [_P, _P, _P, _I, _I, _I, _I, _I, _F, _P]),
+    "ref_self_attention_avx2": (None, [_P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _I, _P]),
     "ref_time_decode_layer": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
 }
 
@@ -337,6 +338,18 @@ class Reference:
         B, H, Sq, D = q.shape
         out = np.empty_like(q)
         self.lib.ref_cross_attention(_p(q), _p(k), _p(v), B, H, Sq, k.shape[2], D, float(scale), _p(out))
+        return out
+
+    def self_attention_avx2(self, q, k, v, scale, mask=None):
+        """ops::avx2::self_attention_avx2(q [B][H][Sq][D], k/v [B][H][Sk][D],
+        mask [mrows][Sk] (given as [1][1][mrows][Sk]) or nullptr, scale)."""
+        q, k, v = _f32(q), _f32(k), _f32(v)
+        B, H, Sq, D = q.shape
+        out = np.empty_like(q)
+        m = None if mask is None else _f32(mask)
+        mrows = 0 if m is None else m.shape[0]
+        self.lib.ref_self_attention_avx2(_p(q), _p(k), _p(v), B, H, Sq, k.shape[2], D, float(scale),
+                                         None if m is None else _p(m), mrows, _p(out))
         return out
 
     def set_threads(self, n):

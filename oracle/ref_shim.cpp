@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "attention.h"
+#include "tensor_cpp/attention_avx.h"
 #include "tensor_cpp/kv_cache.h"
 #include "tensor_cpp/ops.h"
 #include "tensor_cpp/qwen3_ops.h"
@@ -440,6 +441,22 @@ void ref_cross_attention(const float* q, const float* k, const float* v, int B, 
     Tensor tk(std::vector<float>(k, k + ks.total()), ks);
     Tensor tv(std::vector<float>(v, v + ks.total()), ks);
     put(tensor_cpp::ops::cross_attention(tq, tk, tv, nullptr, scale), out);
+}
+
+// ops::avx2::self_attention_avx2(q [B][H][Sq][D], k/v [B][H][Sk][D], mask
+// [1][1][mrows][Sk] or null, scale) (tensor_cpp/src/attention_avx.cpp:22-158).
+void ref_self_attention_avx2(const float* q, const float* k, const float* v, int B, int H, int Sq, int Sk, int D,
+                             float scale, const float* mask, int mrows, float* out) {
+    const Shape qs({(size_t)B, (size_t)H, (size_t)Sq, (size_t)D}), ks({(size_t)B, (size_t)H, (size_t)Sk, (size_t)D});
+    Tensor tq(std::vector<float>(q, q + qs.total()), qs);
+    Tensor tk(std::vector<float>(k, k + ks.total()), ks);
+    Tensor tv(std::vector<float>(v, v + ks.total()), ks);
+    Tensor tm;
+    if (mask) {
+        const Shape ms({1, 1, (size_t)mrows, (size_t)Sk});
+        tm = Tensor(std::vector<float>(mask, mask + ms.total()), ms);
+    }
+    put(tensor_cpp::ops::avx2::self_attention_avx2(tq, tk, tv, mask ? &tm : nullptr, scale), out);
 }
 
 }  // extern "C"

@@ -1,6 +1,7 @@
 // Attention operators of the reference's ops namespace on the GPU
 // (reference tensor_cpp/src/ops.cpp:514-738, 742-1017, 1027-1599).
 #include "tensor_cpp/ops.h"
+#include "tensor_cpp/attention_avx.h"
 
 #include <cmath>
 #include <limits>
@@ -117,6 +118,27 @@ MaskKind classify(const Tensor* mask, size_t Sq, size_t Sk) {
     return MaskKind::kOther;
 }
 
+// The -inf pattern of a self_attention_avx2 mask, read as the reference reads
+// it (tensor_cpp/src/attention_avx.cpp:95-117): a mask whose dimension 2 is 1
+// is one row for every query, any other is [Sq, Sk]; finite entries do not
+// count.
+MaskKind classify_ninf(const Tensor* mask, size_t Sq, size_t Sk) {
+    if (!mask) return MaskKind::kNone;
+    const float ninf = -std::numeric_limits<float>::infinity();
+    const bool row = mask->ndim() >= 3 && mask->shape()[2] == 1;
+    if (mask->size() < (row ? Sk : Sq * Sk)) throw std::invalid_argument("mask is smaller than the score matrix");
+    bool none = true, causal = !row && Sq == Sk;
+    for (size_t i = 0; i < (row ? 1 : Sq); ++i)
+        for (size_t j = 0; j < Sk; ++j) {
+            const bool masked = (*mask)[i * Sk + j] == ninf;
+            if (masked) none = false;
+            if (causal && masked != (j > i)) causal = false;
+        }
+    if (none) return MaskKind::kNone;
+    if (causal) return MaskKind::kCausal;
+    return MaskKind::kOther;
+}
+
 }  // namespace
 
 Tensor self_attention(const Tensor& query, const Tensor& key, const Tensor& value, const Tensor* mask,
@@ -176,5 +198,23 @@ Tensor self_attention_streaming_blockwise_avx2_cache_optimized(const Tensor& que
     return self_attention_streaming_blockwise(query, key, value, scale, q_block_size, kv_block_size);
 }
 
+namespace avx2 {
+
+Tensor self_attention_avx2(const Tensor& query, const Tensor& key, const Tensor& value, const Tensor* mask,
+                           float scale) {
+    const Dims d = check_qkv(query, key, value);
+    switch (classify_ninf(mask, d.Sq, d.Sk)) {
+        case MaskKind::kNone: return decode_rows(query, key, value, d, scale);
+        case MaskKind::kCausal: return causal_prefill(query, key, value, d, scale);
+        default:
+            throw std::invalid_argument("self_attention_avx2 supports a mask with no -inf entries or the causal one");
+    }
+}
+
+Tensor linear_avx2(const Tensor& input, const Tensor& weight, const Tensor* bias) {
+    return ops::linear(input, weight, bias);
+}
+
+}  // namespace avx2
 }  // namespace ops
 }  // namespace tensor_cpp

@@ -10,6 +10,7 @@
 #include <string>
 #include <vector>
 
+#include "tensor_cpp/attention_avx.h"
 #include "tensor_cpp/kv_cache.h"
 #include "tensor_cpp/ops.h"
 #include "tensor_cpp/qwen3_loader.h"
@@ -306,6 +307,39 @@ int drv_cross_attention(const float* q, const float* k, const float* v, int B, i
         Tensor tm;
         if (mask) tm = make(mask, {(size_t)Sq, (size_t)Sk});
         const Tensor y = tensor_cpp::ops::cross_attention(tq, tk, tv, mask ? &tm : nullptr, scale);
+        std::memcpy(out, y.data(), y.size() * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) {
+        return failed_kind(e);
+    }
+}
+
+// ops::avx2::self_attention_avx2(q [B][Hq][Sq][D], k/v [B][Hkv][Sk][D], mask,
+// scale); mask [1][1][mrows][Sk] (mrows 1 or Sq) or null.
+int drv_self_attention_avx2(const float* q, const float* k, const float* v, int B, int Hq, int Hkv, int Sq, int Sk,
+                            int D, float scale, const float* mask, int mrows, float* out) {
+    try {
+        const Tensor tq = make(q, {(size_t)B, (size_t)Hq, (size_t)Sq, (size_t)D});
+        const Tensor tk = make(k, {(size_t)B, (size_t)Hkv, (size_t)Sk, (size_t)D});
+        const Tensor tv = make(v, {(size_t)B, (size_t)Hkv, (size_t)Sk, (size_t)D});
+        Tensor tm;
+        if (mask) tm = make(mask, {1, 1, (size_t)mrows, (size_t)Sk});
+        const Tensor y = tensor_cpp::ops::avx2::self_attention_avx2(tq, tk, tv, mask ? &tm : nullptr, scale);
+        std::memcpy(out, y.data(), y.size() * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) {
+        return failed_kind(e);
+    }
+}
+
+// ops::avx2::linear_avx2(x [M][K], w [N][K], bias [N] or null).
+int drv_linear_avx2(const float* x, const float* w, const float* bias, int M, int K, int N, float* out) {
+    try {
+        const Tensor tx = make(x, {(size_t)M, (size_t)K});
+        const Tensor tw = make(w, {(size_t)N, (size_t)K});
+        Tensor tb;
+        if (bias) tb = make(bias, {(size_t)N});
+        const Tensor y = tensor_cpp::ops::avx2::linear_avx2(tx, tw, bias ? &tb : nullptr);
         std::memcpy(out, y.data(), y.size() * sizeof(float));
         return 0;
     } catch (const std::exception& e) {

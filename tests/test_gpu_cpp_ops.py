@@ -1,5 +1,6 @@
-"""GPU: the C++ mirror's ops::RotaryEmbedding, ops::cross_attention and
-qwen3::test_qwen3_forward (include/tensor_cpp/ops.h, qwen3_loader.h).
+"""GPU: the C++ mirror's ops::RotaryEmbedding, ops::cross_attention,
+ops::avx2::self_attention_avx2 / linear_avx2 and qwen3::test_qwen3_forward
+(include/tensor_cpp/ops.h, attention_avx.h, qwen3_loader.h).
 
 - RotaryEmbedding against the mathematics it states (element i paired with
   i + dim/2, rotated by t * theta^(-i/dim) at sequence index t, zeros past
@@ -9,6 +10,10 @@ qwen3::test_qwen3_forward (include/tensor_cpp/ops.h, qwen3_loader.h).
   sequence index misses the 1e-5 bar by orders of magnitude.
 - cross_attention against the oracle's decode (every query row sees every
   key) and the reference's function; a mask changes nothing, as there.
+- self_attention_avx2 against the oracle (decode rows with no -inf in the
+  mask, causal prefill with the causal -inf pattern; finite mask values are
+  ignored, as in the reference) and the reference's function; linear_avx2
+  against float64.
 - test_qwen3_forward on a checkpoint file: the final-norm hidden states equal
   the oracle decoder's with an identity lm_head.
 Bars: max-abs <= 1e-4 and relative L2 <= 1e-5 (fp32 on both sides) unless
@@ -38,7 +43,10 @@ def drv(sa):
     lib.drv_rotary.argtypes = [_P, _I, _I, _I, _I, _I, _F, _I, _P]
     lib.drv_cross_attention.argtypes = [_P, _P, _P] + [_I] * 6 + [_F, _P, _P]
     lib.drv_test_forward.argtypes = [C.c_char_p, _P, _I, _I, _P, C.c_int64]
-    for f in (lib.drv_rotary, lib.drv_cross_attention, lib.drv_test_forward):
+    lib.drv_self_attention_avx2.argtypes = [_P, _P, _P] + [_I] * 6 + [_F, _P, _I, _P]
+    lib.drv_linear_avx2.argtypes = [_P, _P, _P, _I, _I, _I, _P]
+    for f in (lib.drv_rotary, lib.drv_cross_attention, lib.drv_test_forward, lib.drv_self_attention_avx2,
+              lib.drv_linear_avx2):
         f.restype = _I
     return lib
 
@@ -114,6 +122,82 @@ def test_cross_attention(drv, oracle, ref_opt, synth, B, Hq, Hkv, Sq, Sk, D):
     assert np.array_equal(out, out_m)
     if ref_opt is not None and Hq == Hkv:
         close(out, ref_opt.cross_attention(q, k, v, scale), "reference")
+
+
+def run_sa_avx2(drv, q, k, v, scale, mask=None):
+    """mask [mrows][Sk], passed as [1][1][mrows][Sk], or None."""
+    B, Hq, Sq, D = q.shape
+    Hkv, Sk = k.shape[1], k.shape[2]
+    out = np.full_like(q, np.nan)
+    m = None if mask is None else np.ascontiguousarray(mask, np.float32)
+    rc = drv.drv_self_attention_avx2(_p(q), _p(k), _p(v), B, Hq, Hkv, Sq, Sk, D, scale,
+                                     None if m is None else _p(m), 0 if m is None else m.shape[0], _p(out))
+    return rc, out
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Sq,Sk,D", [(2, 4, 4, 1, 300, 128), (1, 16, 8, 3, 77, 64), (2, 4, 4, 5, 5, 128)])
+def test_self_attention_avx2_rows(drv, oracle, ref_opt, synth, B, Hq, Hkv, Sq, Sk, D):
+    """No -inf in the mask: every query row attends to every key."""
+    q = synth.normal(76, Sq, (B, Hq, Sq, D))
+    k = synth.normal(77, Sk, (B, Hkv, Sk, D))
+    v = synth.normal(78, Sk, (B, Hkv, Sk, D))
+    scale = float(1 / np.sqrt(D))
+    rc, out = run_sa_avx2(drv, q, k, v, scale)
+    assert rc == 0, drv.drv_last_error()
+    want = np.stack([oracle.decode_gqa(np.ascontiguousarray(q[:, :, i]), k, v, np.float32(scale))
+                     for i in range(Sq)], axis=2)
+    close(out, want, "oracle")
+    # finite mask entries are ignored, row mask [1][1][1][Sk] or full [Sq][Sk]
+    for mask in (np.zeros((1, Sk)), synth.normal(79, 1, (1, Sk)), synth.normal(79, 2, (Sq, Sk))):
+        rc, out_m = run_sa_avx2(drv, q, k, v, scale, mask)
+        assert rc == 0, drv.drv_last_error()
+        assert np.array_equal(out, out_m)
+    if ref_opt is not None and Hq == Hkv:
+        close(out, ref_opt.self_attention_avx2(q, k, v, scale), "reference")
+        close(out, ref_opt.self_attention_avx2(q, k, v, scale, synth.normal(79, 2, (Sq, Sk))), "reference, mask")
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,L,D", [(1, 4, 4, 70, 128), (2, 8, 2, 33, 64), (1, 2, 2, 1, 128)])
+def test_self_attention_avx2_causal(drv, oracle, ref_opt, synth, B, Hq, Hkv, L, D):
+    """The causal -inf pattern (finite values elsewhere) runs the causal prefill."""
+    q = synth.normal(80, L, (B, Hq, L, D))
+    k = synth.normal(81, L, (B, Hkv, L, D))
+    v = synth.normal(82, L, (B, Hkv, L, D))
+    scale = float(1 / np.sqrt(D))
+    mask = synth.normal(83, L, (L, L))
+    mask[np.triu_indices(L, 1)] = -np.inf
+    rc, out = run_sa_avx2(drv, q, k, v, scale, mask)
+    assert rc == 0, drv.drv_last_error()
+    close(out, oracle.prefill_blockwise(q, k, v, np.float32(scale), 64), "oracle")
+    if ref_opt is not None and Hq == Hkv:
+        close(out, ref_opt.self_attention_avx2(q, k, v, scale, mask), "reference")
+
+
+def test_self_attention_avx2_refusals(drv, synth):
+    q = synth.normal(84, 1, (1, 2, 4, 64))
+    k = synth.normal(84, 2, (1, 2, 6, 64))
+    mask = np.zeros((4, 6), np.float32)
+    mask[1, 3] = -np.inf                                          # not the causal pattern
+    assert run_sa_avx2(drv, q, k, k, 0.125, mask)[0] == -1
+    assert drv.drv_last_error().startswith(b"I:")
+    row = np.zeros((1, 6), np.float32)
+    row[0, 2] = -np.inf                                           # a key masked for every row
+    assert run_sa_avx2(drv, q, k, k, 0.125, row)[0] == -1
+    assert run_sa_avx2(drv, q, synth.normal(84, 3, (1, 3, 6, 64)), synth.normal(84, 3, (1, 3, 6, 64)),
+                       0.125)[0] == -1                            # 2 query heads over 3 key heads
+
+
+@pytest.mark.parametrize("M,K,N,bias", [(5, 33, 70, True), (64, 256, 64, False)])
+def test_linear_avx2(drv, synth, M, K, N, bias):
+    x = synth.normal(85, M * 7 + K, (M, K))
+    w = synth.normal(86, N * 3 + K, (N, K), 0.05)
+    b = synth.normal(87, N, (N,)) if bias else None
+    out = np.empty((M, N), np.float32)
+    assert drv.drv_linear_avx2(_p(x), _p(w), None if b is None else _p(b), M, K, N, _p(out)) == 0, \
+        drv.drv_last_error()
+    want = x.astype(np.float64) @ w.astype(np.float64).T + (b if bias else 0.0)
+    scale = max(1.0, float(np.abs(want).max()))
+    assert float(np.abs(out - want).max()) <= 1e-5 * scale
 
 
 def test_test_qwen3_forward_hidden_states(drv, oracle, synth, tmp_path):
