@@ -569,14 +569,15 @@ split_kv_decode_kernel(DecodeArgs a) {
 // O = sum_c e^{m_c-M} O_c / sum_c e^{m_c-M} l_c.  A separate launch: the
 // kernel boundary publishes the partials, where an in-kernel hand-off would
 // need a device-scope fence per workgroup (measured at ~57 ns each,
-// serialised across the device).  MT threads read the partials as float4
-// columns, PARTS chunks at a time, so one round trip covers up to MT/(D/4)
-// chunks.
-template <int D, bool PAGED, int MT, bool FUSED = false>
+// serialised across the device).  A row's DS workgroups each take D/DS of
+// its columns; MT threads read the partials as float4 columns, PARTS chunks
+// at a time, so one round trip covers up to MT/(D/4/DS) chunks.
+template <int D, bool PAGED, int MT, bool FUSED = false, int DS = 1>
 __global__ void __launch_bounds__(MT)
 lse_merge_kernel(DecodeArgs a) {
-    constexpr int V4 = D / 4;
+    constexpr int V4 = D / 4 / DS;    // float4 columns of this workgroup: slice blockIdx.y of DS
     constexpr int PARTS = MT / V4;
+    static_assert(PARTS >= 1 && PARTS * V4 == MT, "threads per column");
     const int bh = blockIdx.x;
     const int seq = bh / a.n_q;
     int len;
@@ -594,7 +595,7 @@ lse_merge_kernel(DecodeArgs a) {
     __shared__ float4 sh_red[PARTS][V4];
     __shared__ float sh_scr[MT / kWave];
     const float* ml = a.part_ml + (size_t)bh * a.n_split * 2;
-    const float4* po = reinterpret_cast<const float4*>(a.part_o + (size_t)bh * a.n_split * D);
+    const float4* po = reinterpret_cast<const float4*>(a.part_o + (size_t)bh * a.n_split * D) + blockIdx.y * V4;
     const int j = threadIdx.x % V4;
     const int part = threadIdx.x / V4;
     // The first NPRE partial rows of this thread are loaded before the
@@ -604,7 +605,7 @@ lse_merge_kernel(DecodeArgs a) {
 #pragma unroll
     for (int k = 0; k < NPRE; ++k) {
         const int c = part + k * PARTS;
-        pre[k] = c < n_active ? po[(size_t)c * V4 + j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        pre[k] = c < n_active ? po[(size_t)c * (D / 4) + j] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     float mx = -INFINITY;
     for (int c = threadIdx.x; c < n_active; c += MT) mx = fmaxf(mx, ml[2 * c]);
@@ -628,7 +629,7 @@ lse_merge_kernel(DecodeArgs a) {
     }
 #pragma unroll 4
     for (int c = part + NPRE * PARTS; c < n_active; c += PARTS) {
-        const float4 x = po[(size_t)c * V4 + j];
+        const float4 x = po[(size_t)c * (D / 4) + j];
         const float w = sh_w[c];
         acc.x = fmaf(w, x.x, acc.x); acc.y = fmaf(w, x.y, acc.y);
         acc.z = fmaf(w, x.z, acc.z); acc.w = fmaf(w, x.w, acc.w);
@@ -643,7 +644,7 @@ lse_merge_kernel(DecodeArgs a) {
             t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
         }
         const float inv = 1.0f / ls;
-        reinterpret_cast<float4*>(a.out + (size_t)bh * D)[j] =
+        reinterpret_cast<float4*>(a.out + (size_t)bh * D)[blockIdx.y * V4 + j] =
             make_float4(t.x * inv, t.y * inv, t.z * inv, t.w * inv);
     }
 }
@@ -740,9 +741,19 @@ sa_status launch_decode(const DecodeArgs& a, int n_seq, hipStream_t st) {
     SA_CHECK_LAUNCH();
     if (a.n_split > 1) {
         const dim3 mgrid(n_seq * a.n_q);
-        if (a.n_split >= 64)
-            hipLaunchKernelGGL((lse_merge_kernel<D, PAGED, 1024, FUSED>), mgrid, dim3(1024), 0, st, a);
-        else
+        // Rows with many chunks: four 256-thread workgroups per row, each
+        // merging a quarter of head_dim (their block reductions span 4
+        // waves).  Measured on the T = 262144 single-query call (256 chunks,
+        // same box, interleaved): 44.7 us per call against 45.9 us with one
+        // 1024-thread workgroup per row; 2 or 8 slices, or 128 threads,
+        // 45.2-45.5 us.
+        if (a.n_split >= 64) {
+            if constexpr (D % 16 == 0)
+                hipLaunchKernelGGL((lse_merge_kernel<D, PAGED, 256, FUSED, 4>), dim3(n_seq * a.n_q, 4), dim3(256), 0,
+                                   st, a);
+            else
+                hipLaunchKernelGGL((lse_merge_kernel<D, PAGED, 1024, FUSED>), mgrid, dim3(1024), 0, st, a);
+        } else
             hipLaunchKernelGGL((lse_merge_kernel<D, PAGED, 256, FUSED>), mgrid, dim3(256), 0, st, a);
         SA_CHECK_LAUNCH();
     }
