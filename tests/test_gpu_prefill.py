@@ -72,6 +72,34 @@ def test_prefill_fp32(sa, oracle, synth, monkeypatch, L, kernel):
     assert rel_l2(out, want) <= 1e-5
 
 
+@pytest.mark.parametrize("kernel", ["split", "unsplit"])
+@pytest.mark.parametrize("L", [128, 1024])
+def test_prefill_fp32_roped(sa, oracle, synth, monkeypatch, L, kernel):
+    """The prompt-length workload as specified: N(0,1) q and k rotated by RoPE
+    (theta 1e6) at positions 0 .. L-1, every row against the oracle."""
+    f32_variant(monkeypatch, kernel)
+    q, k, v = inputs(synth, L, seed=55)
+    q, k = roped(oracle, q), roped(oracle, k)
+    sc = np.float32(1 / np.sqrt(128))
+    out = host(sa.prefill_causal(dev(q), dev(k), dev(v), float(sc)))
+    want = oracle.prefill_blockwise(q, k, v, sc, 64)
+    assert np.abs(out - want).max() <= 1e-4
+    assert rel_l2(out, want) <= 1e-5
+
+
+def test_prefill_fp32_8192_roped_rows(sa, oracle, synth):
+    L = 8192
+    q, k, v = inputs(synth, L, seed=56)
+    q, k = roped(oracle, q), roped(oracle, k)
+    sc = np.float32(1 / np.sqrt(128))
+    out = host(sa.prefill_causal(dev(q), dev(k), dev(v), float(sc)))
+    rows = np.array([0, 63, 64, 2047, 5000, 8191])
+    want = oracle.prefill_blockwise(q, k, v, sc, 64, rows=rows)[:, :, rows]
+    got = out[:, :, rows]
+    assert np.abs(got - want).max() <= 1e-4
+    assert rel_l2(got, want) <= 1e-5
+
+
 def test_prefill_fp32_8192_rows(sa, oracle, synth):
     L = 8192
     q, k, v = inputs(synth, L)
@@ -106,8 +134,8 @@ def roped(oracle, x):
     return oracle.apply_rope(x.reshape(-1, D), pos, cos, sin).reshape(x.shape)
 
 
-@pytest.mark.parametrize("L,rope", [(128, False), (1000, False), (1024, False), (1024, True), (8192, False),
-                                    (8192, True)])
+@pytest.mark.parametrize("L,rope", [(128, False), (128, True), (1000, False), (1024, False), (1024, True),
+                                    (8192, False), (8192, True)])
 def test_prefill_bf16(sa, oracle, synth, L, rope):
     q, k, v = inputs(synth, L, seed=51)
     if rope:
