@@ -176,21 +176,23 @@ constexpr int kGemmRing = 8;      // W fragments in flight per wave (k steps)
 constexpr int kGemmXRing = 4;     // X blocks in flight per thread (k steps); divides kGemmRing
 constexpr int kGemmXStride = kGK + 8;   // bf16 per LDS row of X: conflict-free fragment reads
 
+template <int CW>
 __global__ void __launch_bounds__(256)
 gemm_xwt_kernel(const float* __restrict__ X, int M, int K, const uint16_t* __restrict__ W, int N, int split,
                 float* __restrict__ P) {
     __shared__ __align__(16) uint16_t Xb[2][kGemmTerms][kMaxRows][kGemmXStride];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r16 = lane & 15, g = lane >> 4;
-    const int n0 = blockIdx.x * kGN + 16 * wave;
+    const int n0 = blockIdx.x * kGN * CW + 16 * CW * wave;
     const int k_begin = blockIdx.y * split;
     const int m0 = blockIdx.z * kMaxRows;
     const int Mt = min(M - m0, kMaxRows);
     const int nsteps = split / kGK;
 
-    // W fragment of step j (A operand): lane (r16, g) holds W[n0 + r16][k + 8 g .. + 7].
+    // W fragment c of step j (A operand): lane (r16, g) holds
+    // W[n0 + 16 c + r16][k + 8 g .. + 7].
     const uint16_t* Wl = W + (size_t)(n0 + r16) * K + k_begin + 8 * g;
-    auto load_w = [&](int j) { return *reinterpret_cast<const bf16x8_t*>(Wl + j * kGK); };
+    auto load_w = [&](int j, int c) { return *reinterpret_cast<const bf16x8_t*>(Wl + (size_t)c * 16 * K + j * kGK); };
     // X block of step j: thread t converts X[m0 + t / 4][k + 8 (t % 4) .. + 7].
     // Rows past M load row M - 1 and are zeroed when converted.  Every load of
     // the loop below is issued unconditionally (steps past the last clamp to
@@ -223,21 +225,25 @@ gemm_xwt_kernel(const float* __restrict__ X, int M, int K, const uint16_t* __res
     };
 
     const int last = nsteps - 1;
-    bf16x8_t ring[kGemmRing];
+    bf16x8_t ring[kGemmRing][CW];
 #pragma unroll
-    for (int u = 0; u < kGemmRing; ++u) ring[u] = load_w(min(u, last));
+    for (int u = 0; u < kGemmRing; ++u)
+#pragma unroll
+        for (int c = 0; c < CW; ++c) ring[u][c] = load_w(min(u, last), c);
     // acc[mt]: element i is row m0 + 16 mt + r16, column n0 + 4 g + i.  Term
     // by term, the four row blocks in turn: consecutive MFMAs write
     // different accumulators (each accumulator still adds its terms in
     // order 0, 1, 2).
-    f32x4_t acc[kMaxRows / 16] = {};
-    auto mfma_step = [&](const bf16x8_t& wf, int buf) {
+    f32x4_t acc[kMaxRows / 16][CW] = {};
+    auto mfma_step = [&](const bf16x8_t (&wf)[CW], int buf) {
 #pragma unroll
         for (int t = 0; t < kGemmTerms; ++t)
 #pragma unroll
             for (int mt = 0; mt < kMaxRows / 16; ++mt) {
                 const bf16x8_t xf = *reinterpret_cast<const bf16x8_t*>(&Xb[buf][t][16 * mt + r16][8 * g]);
-                acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf, xf, acc[mt], 0, 0, 0);
+#pragma unroll
+                for (int c = 0; c < CW; ++c)
+                    acc[mt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[c], xf, acc[mt][c], 0, 0, 0);
             }
     };
     static_assert(kGemmRing % kGemmXRing == 0, "the X ring index follows the unrolled W ring index");
@@ -251,8 +257,12 @@ gemm_xwt_kernel(const float* __restrict__ X, int M, int K, const uint16_t* __res
     // Step j = j0 + u, with u = j % kGemmRing known at compile time.
     auto step = [&](int j, int u) {
         const int buf = u & 1;       // kGemmRing is even, so j & 1 == u & 1
-        const bf16x8_t wf = ring[u];
-        ring[u] = load_w(min(j + kGemmRing, last));
+        bf16x8_t wf[CW];
+#pragma unroll
+        for (int c = 0; c < CW; ++c) {
+            wf[c] = ring[u][c];
+            ring[u][c] = load_w(min(j + kGemmRing, last), c);
+        }
         mfma_step(wf, buf);
         // the other buffer was last read before the previous barrier
         const int nx = (u + 1) % kGemmXRing;
@@ -279,7 +289,10 @@ gemm_xwt_kernel(const float* __restrict__ X, int M, int K, const uint16_t* __res
 #pragma unroll
     for (int mt = 0; mt < kMaxRows / 16; ++mt) {
         const int m = 16 * mt + r16;
-        if (m < Mt) *reinterpret_cast<f32x4_t*>(out + (size_t)m * N) = acc[mt];
+        if (m < Mt) {
+#pragma unroll
+            for (int c = 0; c < CW; ++c) *reinterpret_cast<f32x4_t*>(out + (size_t)m * N + 16 * c) = acc[mt][c];
+        }
     }
 }
 
@@ -426,8 +439,9 @@ __global__ void prompt_pos_kernel(int32_t* pos, long long n_rows, int heads, int
 // Split-K count for an M-row projection: doubled while the grid has fewer
 // than two workgroups per CU, each split keeping at least min_steps k-steps
 // and the partials at most max_cols * M floats (the partial buffer).
-int pick_split(int N, int K, int cus, int M = kMaxRows, int min_steps = 2, long long max_cols = 1LL << 30) {
-    const int nb = N / kGN, chunks = K / kGK, mt = (M + kMaxRows - 1) / kMaxRows;
+int pick_split(int N, int K, int cus, int M = kMaxRows, int min_steps = 2, long long max_cols = 1LL << 30,
+               int cw = 1) {
+    const int nb = N / (kGN * cw), chunks = K / kGK, mt = (M + kMaxRows - 1) / kMaxRows;
     int s = 1;
     while (s * 2 <= 32 && (long long)nb * s * mt < 2LL * cus && chunks % (s * 2) == 0 &&
            chunks / (s * 2) >= min_steps && (long long)N * s * 2 <= max_cols)
@@ -435,11 +449,15 @@ int pick_split(int N, int K, int cus, int M = kMaxRows, int min_steps = 2, long 
     return s;
 }
 
-struct Gemm { int N, K, S; };
+// cw: 16-column W fragments per wave (1, or 2 for 128-column workgroups).
+struct Gemm { int N, K, S, cw = 1; };
 
 sa_status gemm(const float* X, int M, const uint16_t* W, const Gemm& g, float* P, hipStream_t st) {
-    hipLaunchKernelGGL(gemm_xwt_kernel, dim3(g.N / kGN, g.S, (M + kMaxRows - 1) / kMaxRows), dim3(256), 0, st, X, M,
-                       g.K, W, g.N, g.K / g.S, P);
+    const dim3 grid(g.N / (kGN * g.cw), g.S, (M + kMaxRows - 1) / kMaxRows);
+    if (g.cw == 2)
+        hipLaunchKernelGGL(gemm_xwt_kernel<2>, grid, dim3(256), 0, st, X, M, g.K, W, g.N, g.K / g.S, P);
+    else
+        hipLaunchKernelGGL(gemm_xwt_kernel<1>, grid, dim3(256), 0, st, X, M, g.K, W, g.N, g.K / g.S, P);
     SA_CHECK_LAUNCH();
     return SA_OK;
 }
@@ -663,10 +681,22 @@ extern "C" sa_status sa_qwen3_prefill(sa_qwen3* m, sa_kvcache* cache, const int3
     const int cus = device_cu_count();
     const long long part_cols = std::max({s.Nqkv, 2 * s.I, s.H});
     const int m_rows = (int)std::min<long long>(M, 0x7fffffff);
-    const Gemm g_qkv{s.Nqkv, s.H, pick_split(s.Nqkv, s.H, cus, m_rows, 8, part_cols)};
-    const Gemm g_o{s.H, s.Nq, pick_split(s.H, s.Nq, cus, m_rows, 8, part_cols)};
-    const Gemm g_gu{2 * s.I, s.H, pick_split(2 * s.I, s.H, cus, m_rows, 8, part_cols)};
-    const Gemm g_down{s.H, s.I, pick_split(s.H, s.I, cus, m_rows, 8, part_cols)};
+    // 128-column workgroups (each X fragment read from LDS feeds two MFMAs)
+    // for prompts of more than four 64-row blocks, 64 columns below.
+    // Measured at the Qwen3-0.6B shape through benchmark_qwen3 (tok/s, same
+    // box, interleaved; 64 / 128 columns): 128 tokens 42,100 / 35,900, 256:
+    // 73,200 / 67,200, 384: 88,000 / 89,700, 512: 107,800 / 111,500, 1024:
+    // 128,100 / 141,100, 2048: 118,800 / 133,300.  Shorter prompts give
+    // 128-column grids too few workgroups once split-K keeps its minimum
+    // k-steps per split.
+    auto shape = [&](int N, int K) {
+        const int cw = m_rows > 4 * kMaxRows && N % (2 * kGN) == 0 ? 2 : 1;
+        return Gemm{N, K, pick_split(N, K, cus, m_rows, 8, part_cols, cw), cw};
+    };
+    const Gemm g_qkv = shape(s.Nqkv, s.H);
+    const Gemm g_o = shape(s.H, s.Nq);
+    const Gemm g_gu = shape(2 * s.I, s.H);
+    const Gemm g_down = shape(s.H, s.I);
 
     // activations of the M token rows, carved from one grow-only buffer
     const size_t f_x = M * s.H, f_q = M * s.Nq, f_k = M * s.Nk, f_act = M * s.I;
