@@ -108,6 +108,7 @@ sa_status refused(const Verdict& v) { return fail(v.status, v.msg); }
 struct AppendArgs {
     const float* q; const float* k; const float* v;
     float* q_out;
+    float* k_out;              // optional: K normed and rotated, as q_out
     const float* wq; const float* wk;
     const float* cos_t; const float* sin_t;
     RowList rows;              // cache row of each sequence of this launch
@@ -163,6 +164,7 @@ qknorm_rope_append_kernel(AppendArgs a) {
         r.store(a.q_out + src, lane);
         return;
     }
+    if (a.k_out) r.store(a.k_out + src, lane);
     const float* lo = r.lo;
     const float* hi = r.hi;
     // Append K (normed, rotated) and V (as given) at pos.  The host has
@@ -416,13 +418,12 @@ extern "C" sa_status sa_rope_table_init(float* d_cos, float* d_sin, int max_pos,
     return SA_OK;
 }
 
-extern "C" sa_status sa_qknorm_rope_append(sa_kvcache* c, int layer, const float* q, const float* k,
-                                           const float* v, int n_seq, int S, const int32_t* seq_ids,
-                                           int n_q_heads, const float* q_norm_w,
-                                           const float* k_norm_w, float eps, const float* rope_cos,
-                                           const float* rope_sin, int rope_max_pos, float* q_out,
-                                           sa_stream_t stream) {
-    clear_error();
+namespace sa {
+
+sa_status qknorm_rope_append(sa_kvcache* c, int layer, const float* q, const float* k, const float* v, int n_seq,
+                             int S, const int32_t* seq_ids, int n_q_heads, const float* q_norm_w,
+                             const float* k_norm_w, float eps, const float* rope_cos, const float* rope_sin,
+                             int rope_max_pos, float* q_out, float* k_out, hipStream_t st) {
     if (!valid_cache(c)) return fail(SA_EINVAL, "invalid cache");
     if (layer < 0 || layer >= c->desc.num_layers) return fail(SA_ERANGE, "Layer index out of range");
     if (!k || !v) return fail(SA_EINVAL, "null k or v");
@@ -441,7 +442,6 @@ extern "C" sa_status sa_qknorm_rope_append(sa_kvcache* c, int layer, const float
     a.max_pages = c->desc.max_pages_per_seq; a.rope_max_pos = rope_max_pos; a.eps = eps;
     const int rows = a.n_q + a.n_kv;
     const int D = c->desc.head_dim;
-    hipStream_t st = as_stream(stream);
     const bool bf = c->desc.kv_dtype == SA_DTYPE_BF16;
     // Up to kRowsPerLaunch sequences per launch, their cache rows by value.
     for (int i0 = 0; i0 < n_seq; i0 += kRowsPerLaunch) {
@@ -450,6 +450,7 @@ extern "C" sa_status sa_qknorm_rope_append(sa_kvcache* c, int layer, const float
         a.q = q ? q + (size_t)i0 * S * n_q_heads * D : nullptr;
         a.q_out = q ? q_out + (size_t)i0 * S * n_q_heads * D : nullptr;
         a.k = k + (size_t)i0 * S * a.n_kv * D;
+        a.k_out = k_out ? k_out + (size_t)i0 * S * a.n_kv * D : nullptr;
         a.v = v + (size_t)i0 * S * a.n_kv * D;
         dim3 grid((rows + 3) / 4, S, m);
         switch (D) {
@@ -470,6 +471,19 @@ extern "C" sa_status sa_qknorm_rope_append(sa_kvcache* c, int layer, const float
         SA_CHECK_LAUNCH();
     }
     return SA_OK;
+}
+
+}  // namespace sa
+
+extern "C" sa_status sa_qknorm_rope_append(sa_kvcache* c, int layer, const float* q, const float* k,
+                                           const float* v, int n_seq, int S, const int32_t* seq_ids,
+                                           int n_q_heads, const float* q_norm_w,
+                                           const float* k_norm_w, float eps, const float* rope_cos,
+                                           const float* rope_sin, int rope_max_pos, float* q_out,
+                                           sa_stream_t stream) {
+    clear_error();
+    return qknorm_rope_append(c, layer, q, k, v, n_seq, S, seq_ids, n_q_heads, q_norm_w, k_norm_w, eps, rope_cos,
+                              rope_sin, rope_max_pos, q_out, nullptr, as_stream(stream));
 }
 
 extern "C" size_t sa_paged_decode_ws_bytes(const sa_kvcache* c, int n_seq, int n_q_heads) {

@@ -427,12 +427,6 @@ __global__ void argmax_final_kernel(const float* pv, const int32_t* pi, int nb, 
     out[m] = idx == 0x7fffffff ? 0 : idx;
 }
 
-// pos[r] = position of row r of a token-major [B][L][heads] layout: (r / heads) % L.
-__global__ void prompt_pos_kernel(int32_t* pos, long long n_rows, int heads, int L) {
-    const long long r = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (r < n_rows) pos[r] = (int32_t)((r / heads) % L);
-}
-
 // ---------------------------------------------------------------------------
 // Host helpers
 // ---------------------------------------------------------------------------
@@ -701,9 +695,8 @@ extern "C" sa_status sa_qwen3_prefill(sa_qwen3* m, sa_kvcache* cache, const int3
     // activations of the M token rows, carved from one grow-only buffer
     const size_t f_x = M * s.H, f_q = M * s.Nq, f_k = M * s.Nk, f_act = M * s.I;
     const size_t f_part = M * part_cols;
-    const size_t n_pos = M * s.Hq + M * s.Hkv;
     const size_t floats = 2 * f_x + 2 * f_q + 2 * f_k + f_act + f_part + (size_t)batch * s.H;
-    const size_t need = floats * sizeof(float) + n_pos * sizeof(int32_t);
+    const size_t need = floats * sizeof(float);
     if (need > m->pf_bytes) {
         if (m->pf) SA_HIP_TRY(hipFree(m->pf));
         m->pf = nullptr;
@@ -720,15 +713,10 @@ extern "C" sa_status sa_qwen3_prefill(sa_qwen3* m, sa_kvcache* cache, const int3
     float* act = v + f_k;
     float* part = act + f_act;
     float* h_last = part + f_part;
-    int32_t* pos_q = reinterpret_cast<int32_t*>(h_last + (size_t)batch * s.H);
-    int32_t* pos_k = pos_q + M * s.Hq;
     const float eps = d.rms_eps;
     const float scale = 1.0f / sqrtf((float)d.head_dim);
     float* out_logits = logits ? logits : m->logits;
 
-    hipLaunchKernelGGL(prompt_pos_kernel, dim3((M * s.Hq + 255) / 256), dim3(256), 0, st, pos_q, M * s.Hq, s.Hq, L);
-    hipLaunchKernelGGL(prompt_pos_kernel, dim3((M * s.Hkv + 255) / 256), dim3(256), 0, st, pos_k, M * s.Hkv, s.Hkv,
-                       L);
     hipLaunchKernelGGL(embed_norm_kernel, dim3((unsigned)M), dim3(256), 0, st, m->embed, tokens, s.V, s.H,
                        m->layers[0].in_norm, eps, x, h);
     SA_CHECK_LAUNCH();
@@ -742,13 +730,10 @@ extern "C" sa_status sa_qwen3_prefill(sa_qwen3* m, sa_kvcache* cache, const int3
         hipLaunchKernelGGL(qkv_split_kernel, dim3((unsigned)M, (s.Nqkv + 1023) / 1024), dim3(256), 0, st, part,
                            g_qkv.S, (int)M, s.Nq, s.Nk, q, k, v);
         SA_CHECK_LAUNCH();
-        SA_TRY(sa_qk_norm_rope(q, (int)(M * s.Hq), s.D, pos_q, Ly.q_norm, eps, m->rope_cos, m->rope_sin, d.max_pos,
-                               q, stream));
-        SA_TRY(sa_qk_norm_rope(k, (int)(M * s.Hkv), s.D, pos_k, Ly.k_norm, eps, m->rope_cos, m->rope_sin,
-                               d.max_pos, k, stream));
-        // k is normed and rotated already: append it (and v) as they are
-        SA_TRY(sa_qknorm_rope_append(cache, l, nullptr, k, v, batch, L, nullptr, s.Hq, nullptr, nullptr, eps,
-                                     nullptr, nullptr, 0, nullptr, stream));
+        // q and k normed and rotated in place (positions 0 .. L-1: the cache
+        // is empty), K and V appended to the cache, in one launch.
+        SA_TRY(qknorm_rope_append(cache, l, q, k, v, batch, L, nullptr, s.Hq, Ly.q_norm, Ly.k_norm, eps, m->rope_cos,
+                                  m->rope_sin, d.max_pos, q, k, st));
         SA_TRY(sa_prefill_causal_strided(q, k, v, SA_DTYPE_F32, batch, s.Hq, s.Hkv, L, s.D, q_str, kv_str, q_str,
                                          scale, attn, stream));
         SA_TRY(gemm(attn, (int)M, Ly.o, g_o, part, st));

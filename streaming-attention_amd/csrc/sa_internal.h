@@ -223,6 +223,13 @@ struct PagedView {
     bool bf16;
 };
 
+// sa_qknorm_rope_append with an optional k_out: K normed and rotated, as
+// q_out receives q (either may alias its input).
+sa_status qknorm_rope_append(sa_kvcache* c, int layer, const float* q, const float* k, const float* v, int n_seq,
+                             int S, const int32_t* seq_ids, int n_q_heads, const float* q_norm_w,
+                             const float* k_norm_w, float eps, const float* rope_cos, const float* rope_sin,
+                             int rope_max_pos, float* q_out, float* k_out, hipStream_t st);
+
 size_t paged_ws(int n_seq, int n_q, int n_kv, int d, int max_pages);
 // seq_ids: host array of cache rows (NULL: 0 .. n_seq-1), already checked.
 sa_status decode_paged(const PagedView& c, const float* q, int n_seq, const int32_t* seq_ids,
