@@ -109,6 +109,12 @@ struct AppendArgs {
     const float* q; const float* k; const float* v;
     float* q_out;
     float* k_out;              // optional: K normed and rotated, as q_out
+    // Optional: q, k and v are the sum of part_S split-K partials of rows
+    // [part_row0 + i_seq * S + s] of a [part_M][(n_q + 2 n_kv) * D] projection;
+    // v also goes to v_out.
+    const float* part;
+    int part_S, part_M, part_row0;
+    float* v_out;
     const float* wq; const float* wk;
     const float* cos_t; const float* sin_t;
     RowList rows;              // cache row of each sequence of this launch
@@ -146,7 +152,7 @@ qknorm_rope_append_kernel(AppendArgs a) {
     const int n_rows = a.n_q + a.n_kv;
     if (row_id >= n_rows) return;
     const bool is_q = row_id < a.n_q;
-    if (is_q && !a.q) return;
+    if (is_q && !a.q && !a.part) return;
     const int head = is_q ? row_id : row_id - a.n_q;
     const int cache_row = a.rows.row[i_seq];
     const int pos = a.seq_lens[cache_row] + s;
@@ -156,8 +162,12 @@ qknorm_rope_append_kernel(AppendArgs a) {
     const float* x = (is_q ? a.q : a.k) + src;
     const float* w = is_q ? a.wq : a.wk;
 
+    const int part_cols = (a.n_q + 2 * a.n_kv) * D;
+    const size_t part_row = (size_t)(a.part_row0 + i_seq * a.S + s) * part_cols;
+    const size_t part_split = (size_t)a.part_M * part_cols;
     RowPairs<D> r;
-    r.load(x, lane);
+    if (a.part) r.load_sum(a.part + part_row + (is_q ? head : a.n_q + head) * D, part_split, a.part_S, lane);
+    else r.load(x, lane);
     if (w) r.rms_norm(w, a.eps, lane);
     if (a.cos_t && pos < a.rope_max_pos) r.rope(a.cos_t, a.sin_t, pos, lane);
     if (is_q) {
@@ -167,6 +177,14 @@ qknorm_rope_append_kernel(AppendArgs a) {
     if (a.k_out) r.store(a.k_out + src, lane);
     const float* lo = r.lo;
     const float* hi = r.hi;
+    // V as given, or summed from the partials (and written to v_out).
+    RowPairs<D> vr;
+    if (a.part) {
+        vr.load_sum(a.part + part_row + (a.n_q + a.n_kv + head) * D, part_split, a.part_S, lane);
+        if (a.v_out) vr.store(a.v_out + src, lane);
+    } else {
+        vr.load(a.v + src, lane);
+    }
     // Append K (normed, rotated) and V (as given) at pos.  The host has
     // checked that every row has a page there; these tests only keep a
     // device length that disagrees with the host from writing out of bounds.
@@ -174,7 +192,6 @@ qknorm_rope_append_kernel(AppendArgs a) {
     const int page = a.table[(size_t)cache_row * a.max_pages + (pos >> 6)];
     if (page < 0) return;
     const size_t row = (((size_t)page * a.n_kv + head) * 64 + (pos & 63)) * D;
-    const float* vx = a.v + src;
 #pragma unroll
     for (int c = 0; c < NP; ++c) {
         const int i = lane + c * kWave;
@@ -184,15 +201,15 @@ qknorm_rope_append_kernel(AppendArgs a) {
                 uint16_t* vd = reinterpret_cast<uint16_t*>(a.v_pool) + row;
                 kd[i] = f32_to_bf16_rne(lo[c]);
                 kd[i + H] = f32_to_bf16_rne(hi[c]);
-                vd[i] = f32_to_bf16_rne(vx[i]);
-                vd[i + H] = f32_to_bf16_rne(vx[i + H]);
+                vd[i] = f32_to_bf16_rne(vr.lo[c]);
+                vd[i + H] = f32_to_bf16_rne(vr.hi[c]);
             } else {
                 float* kd = reinterpret_cast<float*>(a.k_pool) + row;
                 float* vd = reinterpret_cast<float*>(a.v_pool) + row;
                 kd[i] = lo[c];
                 kd[i + H] = hi[c];
-                vd[i] = vx[i];
-                vd[i + H] = vx[i + H];
+                vd[i] = vr.lo[c];
+                vd[i + H] = vr.hi[c];
             }
         }
     }
@@ -420,14 +437,18 @@ extern "C" sa_status sa_rope_table_init(float* d_cos, float* d_sin, int max_pos,
 
 namespace sa {
 
-sa_status qknorm_rope_append(sa_kvcache* c, int layer, const float* q, const float* k, const float* v, int n_seq,
-                             int S, const int32_t* seq_ids, int n_q_heads, const float* q_norm_w,
-                             const float* k_norm_w, float eps, const float* rope_cos, const float* rope_sin,
-                             int rope_max_pos, float* q_out, float* k_out, hipStream_t st) {
+namespace {
+
+// Shared by the entry points below: q/k/v given (part == NULL), or summed from
+// the n_part split-K partials of the projection at part (q, k, v NULL).
+sa_status append_impl(sa_kvcache* c, int layer, const float* q, const float* k, const float* v, const float* part,
+                      int n_part, int n_seq, int S, const int32_t* seq_ids, int n_q_heads, const float* q_norm_w,
+                      const float* k_norm_w, float eps, const float* rope_cos, const float* rope_sin,
+                      int rope_max_pos, float* q_out, float* k_out, float* v_out, hipStream_t st) {
     if (!valid_cache(c)) return fail(SA_EINVAL, "invalid cache");
     if (layer < 0 || layer >= c->desc.num_layers) return fail(SA_ERANGE, "Layer index out of range");
-    if (!k || !v) return fail(SA_EINVAL, "null k or v");
-    if (q && (!q_out || n_q_heads <= 0)) return fail(SA_EINVAL, "q needs q_out and n_q_heads > 0");
+    if (part ? n_part <= 0 : (!k || !v)) return fail(SA_EINVAL, "null k or v");
+    if ((q || part) && (!q_out || n_q_heads <= 0)) return fail(SA_EINVAL, "q needs q_out and n_q_heads > 0");
     if (n_seq <= 0 || S <= 0) return fail(SA_EINVAL, "n_seq and S must be positive");
     if ((rope_cos == nullptr) != (rope_sin == nullptr)) return fail(SA_EINVAL, "cos and sin go together");
     if (rope_cos && rope_max_pos <= 0) return fail(SA_EINVAL, "RoPE table needs rope_max_pos > 0");
@@ -435,10 +456,11 @@ sa_status qknorm_rope_append(sa_kvcache* c, int layer, const float* q, const flo
     if (!vd.ok()) return refused(vd);
     AppendArgs a{};
     a.q_out = q_out;
+    a.part = part; a.part_S = n_part; a.part_M = n_seq * S;
     a.wq = q_norm_w; a.wk = k_norm_w; a.cos_t = rope_cos; a.sin_t = rope_sin;
     a.seq_lens = c->d_lens; a.table = c->d_table;
     a.k_pool = k_pool_of(c, layer); a.v_pool = v_pool_of(c, layer);
-    a.n_q = q ? n_q_heads : 0; a.n_kv = c->desc.num_kv_heads; a.S = S;
+    a.n_q = q || part ? n_q_heads : 0; a.n_kv = c->desc.num_kv_heads; a.S = S;
     a.max_pages = c->desc.max_pages_per_seq; a.rope_max_pos = rope_max_pos; a.eps = eps;
     const int rows = a.n_q + a.n_kv;
     const int D = c->desc.head_dim;
@@ -448,10 +470,12 @@ sa_status qknorm_rope_append(sa_kvcache* c, int layer, const float* q, const flo
         const int m = std::min(kRowsPerLaunch, n_seq - i0);
         for (int i = 0; i < m; ++i) a.rows.row[i] = seq_ids ? seq_ids[i0 + i] : i0 + i;
         a.q = q ? q + (size_t)i0 * S * n_q_heads * D : nullptr;
-        a.q_out = q ? q_out + (size_t)i0 * S * n_q_heads * D : nullptr;
-        a.k = k + (size_t)i0 * S * a.n_kv * D;
+        a.q_out = a.n_q ? q_out + (size_t)i0 * S * n_q_heads * D : nullptr;
+        a.k = k ? k + (size_t)i0 * S * a.n_kv * D : nullptr;
         a.k_out = k_out ? k_out + (size_t)i0 * S * a.n_kv * D : nullptr;
-        a.v = v + (size_t)i0 * S * a.n_kv * D;
+        a.v = v ? v + (size_t)i0 * S * a.n_kv * D : nullptr;
+        a.v_out = v_out ? v_out + (size_t)i0 * S * a.n_kv * D : nullptr;
+        a.part_row0 = i0 * S;
         dim3 grid((rows + 3) / 4, S, m);
         switch (D) {
 #define SA_APPEND_CASE(DD)                                                                        \
@@ -471,6 +495,25 @@ sa_status qknorm_rope_append(sa_kvcache* c, int layer, const float* q, const flo
         SA_CHECK_LAUNCH();
     }
     return SA_OK;
+}
+
+}  // namespace
+
+sa_status qknorm_rope_append(sa_kvcache* c, int layer, const float* q, const float* k, const float* v, int n_seq,
+                             int S, const int32_t* seq_ids, int n_q_heads, const float* q_norm_w,
+                             const float* k_norm_w, float eps, const float* rope_cos, const float* rope_sin,
+                             int rope_max_pos, float* q_out, float* k_out, hipStream_t st) {
+    return append_impl(c, layer, q, k, v, nullptr, 0, n_seq, S, seq_ids, n_q_heads, q_norm_w, k_norm_w, eps, rope_cos,
+                       rope_sin, rope_max_pos, q_out, k_out, nullptr, st);
+}
+
+sa_status qknorm_rope_append_partials(sa_kvcache* c, int layer, const float* part, int n_part, int n_seq, int S,
+                                      int n_q_heads, const float* q_norm_w, const float* k_norm_w, float eps,
+                                      const float* rope_cos, const float* rope_sin, int rope_max_pos, float* q_out,
+                                      float* k_out, float* v_out, hipStream_t st) {
+    if (!part) return fail(SA_EINVAL, "null partials");
+    return append_impl(c, layer, nullptr, nullptr, nullptr, part, n_part, n_seq, S, nullptr, n_q_heads, q_norm_w,
+                       k_norm_w, eps, rope_cos, rope_sin, rope_max_pos, q_out, k_out, v_out, st);
 }
 
 }  // namespace sa

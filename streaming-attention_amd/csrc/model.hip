@@ -727,13 +727,11 @@ extern "C" sa_status sa_qwen3_prefill(sa_qwen3* m, sa_kvcache* cache, const int3
         const sa_qwen3::Layer& Ly = m->layers[l];
         // ---- attention block ----
         SA_TRY(gemm(h, (int)M, Ly.qkv, g_qkv, part, st));
-        hipLaunchKernelGGL(qkv_split_kernel, dim3((unsigned)M, (s.Nqkv + 1023) / 1024), dim3(256), 0, st, part,
-                           g_qkv.S, (int)M, s.Nq, s.Nk, q, k, v);
-        SA_CHECK_LAUNCH();
-        // q and k normed and rotated in place (positions 0 .. L-1: the cache
-        // is empty), K and V appended to the cache, in one launch.
-        SA_TRY(qknorm_rope_append(cache, l, q, k, v, batch, L, nullptr, s.Hq, Ly.q_norm, Ly.k_norm, eps, m->rope_cos,
-                                  m->rope_sin, d.max_pos, q, k, st));
+        // q, k, v summed from the projection's split-K partials, q and k
+        // normed and rotated (positions 0 .. L-1: the cache is empty), K and V
+        // appended to the cache, q, k, v written for the attention: one launch.
+        SA_TRY(qknorm_rope_append_partials(cache, l, part, g_qkv.S, batch, L, s.Hq, Ly.q_norm, Ly.k_norm, eps,
+                                           m->rope_cos, m->rope_sin, d.max_pos, q, k, v, st));
         SA_TRY(sa_prefill_causal_strided(q, k, v, SA_DTYPE_F32, batch, s.Hq, s.Hkv, L, s.D, q_str, kv_str, q_str,
                                          scale, attn, stream));
         SA_TRY(gemm(attn, (int)M, Ly.o, g_o, part, st));

@@ -133,6 +133,23 @@ struct RowPairs {
             hi[c] = (i < H) ? x[i + H] : 0.f;
         }
     }
+    // The row as the sum, in split order, of S split-K partial rows
+    // x[s * split] .. (s = 0 .. S-1).
+    __device__ __forceinline__ void load_sum(const float* x, size_t split, int S, int lane) {
+#pragma unroll
+        for (int c = 0; c < NP; ++c) {
+            const int i = lane + c * kWave;
+            float a = 0.f, b = 0.f;
+            if (i < H) {
+                for (int t = 0; t < S; ++t) {
+                    a += x[t * split + i];
+                    b += x[t * split + i + H];
+                }
+            }
+            lo[c] = a;
+            hi[c] = b;
+        }
+    }
     // y = (x / sqrt(mean(x^2) + eps)) * w, eps inside the sqrt (reference
     // tensor_cpp/src/qwen3_ops.cpp:716-717), or with eps_outside
     // y = (x / (sqrt(mean(x^2)) + eps)) * w, as the reference's AVX2 layer
@@ -229,6 +246,14 @@ sa_status qknorm_rope_append(sa_kvcache* c, int layer, const float* q, const flo
                              int S, const int32_t* seq_ids, int n_q_heads, const float* q_norm_w,
                              const float* k_norm_w, float eps, const float* rope_cos, const float* rope_sin,
                              int rope_max_pos, float* q_out, float* k_out, hipStream_t st);
+
+// The same with q, k and v read as the sum of n_part split-K partials of a
+// [n_seq * S][(n_q_heads + 2 n_kv) * D] projection (q columns, then k, then
+// v; partial t at part + t * rows * cols), and v written to v_out as well.
+sa_status qknorm_rope_append_partials(sa_kvcache* c, int layer, const float* part, int n_part, int n_seq, int S,
+                                      int n_q_heads, const float* q_norm_w, const float* k_norm_w, float eps,
+                                      const float* rope_cos, const float* rope_sin, int rope_max_pos, float* q_out,
+                                      float* k_out, float* v_out, hipStream_t st);
 
 size_t paged_ws(int n_seq, int n_q, int n_kv, int d, int max_pages);
 // seq_ids: host array of cache rows (NULL: 0 .. n_seq-1), already checked.
