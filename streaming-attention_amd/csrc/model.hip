@@ -477,10 +477,13 @@ Shapes shapes_of(const sa_qwen3_desc& d, int cus) {
     s.H = d.hidden; s.I = d.intermediate; s.V = d.vocab;
     s.Hq = d.n_q_heads; s.Hkv = d.n_kv_heads; s.D = d.head_dim;
     s.Nq = s.Hq * s.D; s.Nk = s.Hkv * s.D; s.Nqkv = s.Nq + 2 * s.Nk;
-    s.qkv = {s.Nqkv, s.H, pick_split(s.Nqkv, s.H, cus)};
-    s.o = {s.H, s.Nq, pick_split(s.H, s.Nq, cus)};
-    s.gate_up = {2 * s.I, s.H, pick_split(2 * s.I, s.H, cus)};
-    s.down = {s.H, s.I, pick_split(s.H, s.I, cus)};
+    // Decode-step projections (up to 64 rows): splits of at least 8 k-steps.
+    // Measured on the 28-layer B = 64 step: 20.79 ms against 20.98 ms with
+    // 2-step splits (the partials' traffic outweighed the extra workgroups).
+    s.qkv = {s.Nqkv, s.H, pick_split(s.Nqkv, s.H, cus, kMaxRows, 8)};
+    s.o = {s.H, s.Nq, pick_split(s.H, s.Nq, cus, kMaxRows, 8)};
+    s.gate_up = {2 * s.I, s.H, pick_split(2 * s.I, s.H, cus, kMaxRows, 8)};
+    s.down = {s.H, s.I, pick_split(s.H, s.I, cus, kMaxRows, 8)};
     s.lm = {s.V, s.H, 1};
     return s;
 }
