@@ -88,6 +88,13 @@ struct DecodeArgs {
     const float* sin_t;
     float* q_out;            // [n_seq][n_q_heads][D] or NULL
     int32_t* lens_out;       // the cache's device lengths, written on commit
+    // Or q, k_new and v_new as the sum of part_S split-K partials: row seq of
+    // an [.][part_N] projection (q columns, then k, then v), partial t at
+    // part + t * part_split.
+    const float* part;
+    size_t part_split;
+    int part_S;
+    int part_N;
     RowList pos;
     float eps;
     int rope_max_pos;
@@ -333,15 +340,28 @@ split_kv_decode_kernel(DecodeArgs a) {
         const bool rope_on = a.cos_t && pos < a.rope_max_pos;
         RP qr[QPW], kr;
         float vl[NP], vh[NP], wql[NP], wqh[NP], wkl[NP], wkh[NP], cs[NP], sn[NP];
+        const float* prow = a.part ? a.part + (size_t)seq * a.part_N : nullptr;   // uniform
 #pragma unroll
         for (int j = 0; j < QPW; ++j) {
             const int h = wave + j * W;
-            if (h < NREP) qr[j].load(a.q + ((size_t)seq * a.n_q + g * NREP + h) * D, lane);
+            if (h < NREP) {
+                if (prow) qr[j].load_sum(prow + (g * NREP + h) * D, a.part_split, a.part_S, lane);
+                else qr[j].load(a.q + ((size_t)seq * a.n_q + g * NREP + h) * D, lane);
+            }
         }
         const size_t kv_src = ((size_t)seq * a.n_kv + g) * D;
         if (writer) {
-            kr.load(a.k_new + kv_src, lane);
-            RP::load_pairs(a.v_new + kv_src, lane, vl, vh);
+            if (prow) {
+                const float* kp = prow + (a.n_q + g) * D;
+                RP vr;
+                kr.load_sum(kp, a.part_split, a.part_S, lane);
+                vr.load_sum(kp + a.n_kv * D, a.part_split, a.part_S, lane);
+#pragma unroll
+                for (int c = 0; c < NP; ++c) { vl[c] = vr.lo[c]; vh[c] = vr.hi[c]; }
+            } else {
+                kr.load(a.k_new + kv_src, lane);
+                RP::load_pairs(a.v_new + kv_src, lane, vl, vh);
+            }
             if (a.wk) RP::load_pairs(a.wk, lane, wkl, wkh);
         }
         if (a.wq) RP::load_pairs(a.wq, lane, wql, wqh);
@@ -886,12 +906,16 @@ sa_status decode_paged(const PagedView& c, const float* q, int n_seq, const int3
 sa_status decode_paged_fused(const PagedView& c, const float* q, int n_seq, const int32_t* seq_ids, int n_q,
                              const FusedAppend& f, int max_len, long long total_len, float scale, float* out,
                              void* ws, size_t ws_bytes, hipStream_t st) {
-    if (!q || !out || !f.k || !f.v || !f.pos || !f.lens) return fail(SA_EINVAL, "null pointer");
+    if (!out || !f.pos || !f.lens || (!f.part && (!q || !f.k || !f.v))) return fail(SA_EINVAL, "null pointer");
+    if (f.part && (f.part_S <= 0 || f.part_M < n_seq)) return fail(SA_EINVAL, "bad projection partials");
     if (n_seq <= 0 || n_q <= 0 || n_q % c.n_kv) return fail(SA_EINVAL, "bad head counts");
     if (!aligned16(q) || !aligned16(out)) return fail(SA_EINVAL, "q and out must be 16-byte aligned");
     if (max_len <= 0) max_len = 1;
     DecodeArgs a{};
     a.k = c.k_pool; a.v = c.v_pool;
+    a.part_N = (n_q + 2 * c.n_kv) * c.d;
+    a.part_S = f.part_S;
+    a.part_split = (size_t)f.part_M * a.part_N;
     a.block_table = c.block_table; a.seq_lens = c.seq_lens;
     a.n_kv = c.n_kv; a.n_q = n_q; a.max_pages = c.max_pages; a.n_pending = 1;
     a.num_pages = c.num_pages;
@@ -914,11 +938,15 @@ sa_status decode_paged_fused(const PagedView& c, const float* q, int n_seq, cons
             a.rows.row[i] = seq_ids ? seq_ids[i0 + i] : i0 + i;
             a.pos.row[i] = f.pos[i0 + i];
         }
-        a.q = q + (size_t)i0 * n_q * c.d;
         a.out = out + (size_t)i0 * n_q * c.d;
         a.q_out = f.q_out ? f.q_out + (size_t)i0 * n_q * c.d : nullptr;
-        a.k_new = f.k + (size_t)i0 * c.n_kv * c.d;
-        a.v_new = f.v + (size_t)i0 * c.n_kv * c.d;
+        if (f.part) {
+            a.part = f.part + (size_t)i0 * a.part_N;
+        } else {
+            a.q = q + (size_t)i0 * n_q * c.d;
+            a.k_new = f.k + (size_t)i0 * c.n_kv * c.d;
+            a.v_new = f.v + (size_t)i0 * c.n_kv * c.d;
+        }
         if (c.bf16) {
             SA_TRY((dispatch_decode<true, true, true>(a, m, c.d, n_q / c.n_kv, st)));
         } else {

@@ -555,15 +555,19 @@ extern "C" sa_status sa_paged_decode(const sa_kvcache* c, int layer, const float
                         ws_bytes, as_stream(stream));
 }
 
-extern "C" sa_status sa_append_decode(sa_kvcache* c, int layer, const float* q, const float* k, const float* v,
-                                      int n_seq, const int32_t* seq_ids, int n_q_heads, const float* q_norm_w,
-                                      const float* k_norm_w, float eps, const float* rope_cos,
-                                      const float* rope_sin, int rope_max_pos, float scale, float* out,
-                                      float* q_out, void* ws, size_t ws_bytes, int commit, sa_stream_t stream) {
-    clear_error();
+namespace sa {
+namespace {
+
+// sa_append_decode; with part set, q, k and v come from the projection's
+// split-K partials instead (FusedAppend::part).
+sa_status append_decode_impl(sa_kvcache* c, int layer, const float* q, const float* k, const float* v,
+                             const float* part, int n_part, int n_seq, const int32_t* seq_ids, int n_q_heads,
+                             const float* q_norm_w, const float* k_norm_w, float eps, const float* rope_cos,
+                             const float* rope_sin, int rope_max_pos, float scale, float* out, float* q_out,
+                             void* ws, size_t ws_bytes, int commit, hipStream_t stream) {
     if (!valid_cache(c)) return fail(SA_EINVAL, "invalid cache");
     if (layer < 0 || layer >= c->desc.num_layers) return fail(SA_ERANGE, "Layer index out of range");
-    if (!q || !k || !v || !out) return fail(SA_EINVAL, "null q, k, v or out");
+    if (!out || (part ? n_part <= 0 : (!q || !k || !v))) return fail(SA_EINVAL, "null q, k, v or out");
     if (n_seq <= 0) return fail(SA_EINVAL, "n_seq must be positive");
     if (n_q_heads <= 0 || n_q_heads % c->desc.num_kv_heads) return fail(SA_EINVAL, "bad head counts");
     if ((rope_cos == nullptr) != (rope_sin == nullptr)) return fail(SA_EINVAL, "cos and sin go together");
@@ -587,13 +591,40 @@ extern "C" sa_status sa_append_decode(sa_kvcache* c, int layer, const float* q, 
     f.k = k; f.v = v; f.wq = q_norm_w; f.wk = k_norm_w; f.eps = eps;
     f.cos_t = rope_cos; f.sin_t = rope_sin; f.rope_max_pos = rope_max_pos;
     f.q_out = q_out; f.lens = c->d_lens; f.pos = pos.data(); f.commit = commit != 0;
+    f.part = part; f.part_S = n_part; f.part_M = n_seq;
     SA_TRY(decode_paged_fused(pv, q, n_seq, seq_ids, n_q_heads, f, max_len, total, scale, out, ws, ws_bytes,
-                              as_stream(stream)));
+                              stream));
     if (commit) {
         vd = c->pt.commit(seq_ids, n_seq, 1);   // checked above: cannot be refused
         if (!vd.ok()) return refused(vd);
     }
     return SA_OK;
+}
+
+}  // namespace
+
+sa_status append_decode_partials(sa_kvcache* c, int layer, const float* part, int n_part, int n_seq,
+                                 int n_q_heads, const float* q_norm_w, const float* k_norm_w, float eps,
+                                 const float* rope_cos, const float* rope_sin, int rope_max_pos, float scale,
+                                 float* out, void* ws, size_t ws_bytes, int commit, hipStream_t st) {
+    if (!part) return fail(SA_EINVAL, "null projection partials");
+    return append_decode_impl(c, layer, nullptr, nullptr, nullptr, part, n_part, n_seq, nullptr, n_q_heads,
+                              q_norm_w, k_norm_w, eps, rope_cos, rope_sin, rope_max_pos, scale, out, nullptr, ws,
+                              ws_bytes, commit, st);
+}
+
+}  // namespace sa
+
+extern "C" sa_status sa_append_decode(sa_kvcache* c, int layer, const float* q, const float* k, const float* v,
+                                      int n_seq, const int32_t* seq_ids, int n_q_heads, const float* q_norm_w,
+                                      const float* k_norm_w, float eps, const float* rope_cos,
+                                      const float* rope_sin, int rope_max_pos, float scale, float* out,
+                                      float* q_out, void* ws, size_t ws_bytes, int commit, sa_stream_t stream) {
+    clear_error();
+    if (!q || !k || !v) return fail(SA_EINVAL, "null q, k, v or out");
+    return append_decode_impl(c, layer, q, k, v, nullptr, 0, n_seq, seq_ids, n_q_heads, q_norm_w, k_norm_w, eps,
+                              rope_cos, rope_sin, rope_max_pos, scale, out, q_out, ws, ws_bytes, commit,
+                              as_stream(stream));
 }
 
 extern "C" sa_status sa_kvcache_gather(const sa_kvcache* c, int layer, int seq, int len, float* k_out,

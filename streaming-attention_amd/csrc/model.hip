@@ -3,16 +3,17 @@
 // Reference: qwen3_forward_with_cache and qwen3_decoder_layer_with_cache
 // (tensor_cpp/src/qwen3_ops.cpp:620-1014), qwen3_mlp (:265-296), and the ops
 // they call: embedding (tensor_cpp/src/ops.cpp:278-313), linear (:315-372),
-// rms_norm (:375-417).  The attention block itself runs on
-// sa_append_decode (decode step) and sa_qknorm_rope_append + the causal
-// prefill kernel (prompt).
+// rms_norm (:375-417).  The attention block itself runs on the fused
+// append + paged decode launch of sa_append_decode (decode step) and on
+// sa_qknorm_rope_append + the causal prefill kernel (prompt), both reading
+// q, k and v straight from the qkv projection's split-K partials.
 //
 // Layout: the batch of B <= 64 token rows stays fp32 in a residual stream
 // x[B][hidden]; every projection is one GEMM Y = X W^T with bf16 weights in
 // nn.Linear layout [out][in] and fp32 accumulation, split over K into
 // fixed-order partial sums when the output is narrow, so results do not
 // depend on scheduling.  Epilogue kernels fold the partial sums into the next
-// step: the q | k | v split, residual add + RMSNorm, SwiGLU.
+// step: the attention launches (q | k | v), residual add + RMSNorm, SwiGLU.
 #include <math.h>
 
 #include <algorithm>
@@ -315,20 +316,6 @@ __device__ __forceinline__ float4 psum4(const float* P, int S, int M, int N, int
         s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
     }
     return s;
-}
-
-// q | k | v columns of the fused projection into three token-major buffers.
-// Grid (M, N / 1024): a workgroup sums 1024 columns of one row.
-__global__ void __launch_bounds__(256)
-qkv_split_kernel(const float* P, int S, int M, int Nq, int Nk, float* q, float* k, float* v) {
-    const int m = blockIdx.x, N = Nq + 2 * Nk;
-    const int n = (blockIdx.y * 256 + threadIdx.x) * 4;
-    if (n >= N) return;
-    const float4 y = psum4(P, S, M, N, m, n);
-    // Nq and Nk are multiples of 64, so a group of 4 columns never straddles two outputs
-    float* dst = n < Nq ? q + (size_t)m * Nq + n
-                        : n < Nq + Nk ? k + (size_t)m * Nk + n - Nq : v + (size_t)m * Nk + n - Nq - Nk;
-    *reinterpret_cast<float4*>(dst) = y;
 }
 
 // x[m] += projection output; h[m] = rms_norm(x[m]) * w (the next block's norm).
@@ -804,15 +791,13 @@ extern "C" sa_status sa_qwen3_decode_step(sa_qwen3* m, sa_kvcache* cache, const 
         const sa_qwen3::Layer& L = m->layers[l];
         // ---- attention block ----
         SA_TRY(gemm(m->h, M, L.qkv, s.qkv, m->part, st));
-        hipLaunchKernelGGL(qkv_split_kernel, dim3(M, (s.Nqkv + 1023) / 1024), dim3(256), 0, st, m->part, s.qkv.S,
-                           M, s.Nq, s.Nk, m->q, m->k, m->v);
-        SA_CHECK_LAUNCH();
-        // q/k norm + RoPE, the K/V append and the paged decode in one launch
-        // per 64 sequences (plus the LSE merge of multi-chunk sequences); the
-        // last layer's call also commits the token.
-        SA_TRY(sa_append_decode(cache, l, m->q, m->k, m->v, M, nullptr, s.Hq, L.q_norm, L.k_norm, eps, m->rope_cos,
-                                m->rope_sin, d.max_pos, scale, m->attn, nullptr, m->ws, m->ws_bytes,
-                                l + 1 == d.num_layers ? 1 : 0, stream));
+        // The split-K sum of the projection, q/k norm + RoPE, the K/V append
+        // and the paged decode in one launch per 64 sequences (plus the LSE
+        // merge of multi-chunk sequences); the last layer's call also commits
+        // the token.  (A separate split kernel cost 4.7 us per layer.)
+        SA_TRY(sa::append_decode_partials(cache, l, m->part, s.qkv.S, M, s.Hq, L.q_norm, L.k_norm, eps,
+                                          m->rope_cos, m->rope_sin, d.max_pos, scale, m->attn, m->ws, m->ws_bytes,
+                                          l + 1 == d.num_layers ? 1 : 0, st));
         SA_TRY(gemm(m->attn, M, L.o, s.o, m->part, st));
         hipLaunchKernelGGL(residual_norm_kernel, dim3(M), dim3(256), 0, st, m->part, s.o.S, M, s.H, m->x,
                            L.post_norm, eps, m->h);

@@ -255,6 +255,12 @@ sa_status qknorm_rope_append_partials(sa_kvcache* c, int layer, const float* par
                                       const float* rope_cos, const float* rope_sin, int rope_max_pos, float* q_out,
                                       float* k_out, float* v_out, hipStream_t st);
 
+// sa_append_decode with q, k and v read from split-K partials (FusedAppend).
+sa_status append_decode_partials(sa_kvcache* c, int layer, const float* part, int n_part, int n_seq,
+                                 int n_q_heads, const float* q_norm_w, const float* k_norm_w, float eps,
+                                 const float* rope_cos, const float* rope_sin, int rope_max_pos, float scale,
+                                 float* out, void* ws, size_t ws_bytes, int commit, hipStream_t st);
+
 size_t paged_ws(int n_seq, int n_q, int n_kv, int d, int max_pages);
 // seq_ids: host array of cache rows (NULL: 0 .. n_seq-1), already checked.
 sa_status decode_paged(const PagedView& c, const float* q, int n_seq, const int32_t* seq_ids,
@@ -279,6 +285,12 @@ struct FusedAppend {
     int32_t* lens;             // the cache's device lengths (written on commit)
     const int32_t* pos;        // host, [n_seq]
     bool commit;
+    // Optional: q, k and v (then unused) read as the sum of part_S split-K
+    // partials of an [part_M][(n_q + 2 n_kv) * D] projection (q columns, then
+    // k, then v; partial t at part + t * part_M * cols), row i for sequence i.
+    const float* part = nullptr;
+    int part_S = 0;
+    int part_M = 0;
 };
 
 // decode_paged with the step's append folded in: one launch per
