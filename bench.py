@@ -118,7 +118,7 @@ def time_batch(torch, fn, steps: int, warmup: int, warm_s: float = 0.0):
 # ---------------------------------------------------------------- headline
 
 def bench_stream(torch, sa, synth, T: int, steps: int, warmup: int, min_footprint: float = 1.1e9,
-                 calls_per_step: int = 1):
+                 calls_per_step: int = 1, graph: bool = False):
     log(f"[bench] single-head streaming attention T={T} d=128 fp32: generating inputs")
     Q, K, V = synth.stream_inputs(T, 128, seed=2, scale=0.5, outlier_frac=0.01)
     per_rep = K.nbytes + V.nbytes
@@ -144,8 +144,26 @@ def bench_stream(torch, sa, synth, T: int, steps: int, warmup: int, min_footprin
 
     n_calls = steps * calls_per_step
     kern_ms, wall = time_batch(torch, one_call, n_calls, warmup * calls_per_step, warm_s=0.5)
-    bytes_per = (2 * T * 128 + 2 * 128) * 4
+    bytes_per = bytes_per_call(T)
     got = out.cpu().numpy()
+    graph_res = {}
+    if graph:
+        # A short call's kernels finish before the ctypes call that launches
+        # them returns; one call per replica replayed from a HIP graph gives
+        # the device-side time per call (every replica once per replay, so the
+        # footprint stays above the caches).
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            cap = torch.cuda.current_stream().cuda_stream
+            for b in bound:
+                sa.check(call(*b[:-1], cap))
+        g.replay()
+        torch.cuda.synchronize()
+        g_per, _ = time_launches(torch, lambda i: g.replay(), 20, 2)
+        g_ms = statistics.mean(g_per) / n_rep
+        del g
+        graph_res = {"graph_kernel_ms": g_ms, "graph_gbs": bytes_per_call(T) / (g_ms * 1e-3) / 1e9,
+                     "graph_equals_eager": bool(np.array_equal(out.cpu().numpy(), got))}
     from oracle import Oracle
     want = Oracle().streaming_serial(Q, K, V, 128)
     err = float(np.abs(got - want).max())
@@ -155,7 +173,19 @@ def bench_stream(torch, sa, synth, T: int, steps: int, warmup: int, min_footprin
     return {"T": T, "bytes_per_launch": bytes_per, "kernel_ms": kern_ms, "wall_ms_per_call": wall,
             "wall_ms_per_step": wall * calls_per_step, "calls_per_step": calls_per_step,
             "gbs": bytes_per / (kern_ms * 1e-3) / 1e9, "wall_gbs": bytes_per / (wall * 1e-3) / 1e9,
-            "replicas": n_rep, "max_abs_err": err, "rel_l2_err": rl2, "gpu_out": got}, (Q, K, V)
+            "replicas": n_rep, "max_abs_err": err, "rel_l2_err": rl2, "gpu_out": got, **graph_res}, (Q, K, V)
+
+
+def bytes_per_call(T: int) -> int:
+    """Bytes one single-query call must move: K and V, q in, out."""
+    return (2 * T * 128 + 2 * 128) * 4
+
+
+def graph_fields(c: dict) -> dict:
+    """The graph-replayed timing of a bench_stream result, rounded."""
+    return {"graph_kernel_ms": round(c["graph_kernel_ms"], 5), "graph_gbs": round(c["graph_gbs"], 1),
+            "graph_hbm_frac": round(c["graph_gbs"] / HBM_PEAK_GBS, 4),
+            "graph_equals_eager": c["graph_equals_eager"]}
 
 
 def fp64_errors(Q, K, V, gpu_out):
@@ -625,16 +655,17 @@ def main() -> int:
     run = (lambda name: True) if args.only == "all" else (lambda name: name == args.only)
     if run("single"):
         log("[bench] single-head T=1024")
-        c1, _ = bench_stream(torch, sa, synth, 1024, 200, 20, min_footprint=1.1e9)
+        c1, _ = bench_stream(torch, sa, synth, 1024, 200, 20, min_footprint=1.1e9, graph=True)
         extra["single_head_T1024"] = {k: c1[k] for k in ("kernel_ms", "gbs", "max_abs_err", "rel_l2_err")}
         extra["single_head_T1024"]["hbm_frac"] = round(c1["gbs"] / HBM_PEAK_GBS, 5)
+        extra["single_head_T1024"].update(graph_fields(c1))
         for T in (8192, 65536):
             log(f"[bench] single-head T={T}")
-            c2, (q2, k2, v2) = bench_stream(torch, sa, synth, T, 200, 5)
+            c2, (q2, k2, v2) = bench_stream(torch, sa, synth, T, 200, 5, graph=True)
             extra[f"single_head_T{T}"] = {"kernel_ms": c2["kernel_ms"], "gbs": round(c2["gbs"], 1),
                                           "hbm_frac": round(c2["gbs"] / HBM_PEAK_GBS, 4),
                                           "rel_l2_err": c2["rel_l2_err"], "max_abs_err": c2["max_abs_err"],
-                                          **fp64_errors(q2, k2, v2, c2["gpu_out"])}
+                                          **graph_fields(c2), **fp64_errors(q2, k2, v2, c2["gpu_out"])}
     from oracle import Reference
     cpu_extra = args.cpu_budget >= 1.0 and Reference.available()
     if run("layer"):
