@@ -838,7 +838,14 @@ sa_status decode_dense(const float* q, const float* k, const float* v, int batch
     DecodeArgs a{};
     a.q = q; a.k = k; a.v = v; a.out = out;
     a.n_kv = n_kv; a.n_q = n_q; a.T = T; a.scale = scale;
-    a.chunk = pick_chunk((long long)batch * n_kv * T, T);
+    const long long rows = (long long)batch * n_kv * T;
+    a.chunk = pick_chunk(rows, T);
+    // Dense launches of at most 64 rows per CU (one head of up to 16,384
+    // tokens on 256 CUs) take the smallest chunk: one tile per wave, still
+    // one round of workgroups.  Measured per single-head call: T = 1024
+    // 8.0-8.4 against 9.9 us, T = 8192 9.4-9.7 against 10.8-11.0 us; at
+    // T = 65536 it would mean two rounds (17.6 against 16.5 us).
+    if (env_int("SA_DECODE_CHUNK", 0) <= 0 && rows <= 64LL * device_cu_count()) a.chunk = kMinChunk;
     a.n_split = (T + a.chunk - 1) / a.chunk;
     const long long bh = (long long)batch * n_q;
     const size_t need = ws_bytes_for(bh, a.n_split, d);
