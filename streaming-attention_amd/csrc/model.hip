@@ -464,13 +464,17 @@ Shapes shapes_of(const sa_qwen3_desc& d, int cus) {
     s.H = d.hidden; s.I = d.intermediate; s.V = d.vocab;
     s.Hq = d.n_q_heads; s.Hkv = d.n_kv_heads; s.D = d.head_dim;
     s.Nq = s.Hq * s.D; s.Nk = s.Hkv * s.D; s.Nqkv = s.Nq + 2 * s.Nk;
-    // Decode-step projections (up to 64 rows): splits of at least 8 k-steps.
-    // Measured on the 28-layer B = 64 step: 20.79 ms against 20.98 ms with
-    // 2-step splits (the partials' traffic outweighed the extra workgroups).
+    // Decode-step projections (up to 64 rows): splits of at least 8 k-steps,
+    // 4 for the 1024-column o and down projections (16 column blocks: 256
+    // workgroups instead of 128).  Measured on the 28-layer B = 64 step:
+    // 20.79 ms against 20.98 ms with 2-step splits everywhere (the partials'
+    // traffic outweighed the extra workgroups); o/down at 4 / 8 / 16 steps
+    // 20.76 / 20.78 / 21.00 ms on one box.
     s.qkv = {s.Nqkv, s.H, pick_split(s.Nqkv, s.H, cus, kMaxRows, 8)};
-    s.o = {s.H, s.Nq, pick_split(s.H, s.Nq, cus, kMaxRows, 8)};
+    const int od_steps = 4;
+    s.o = {s.H, s.Nq, pick_split(s.H, s.Nq, cus, kMaxRows, od_steps)};
     s.gate_up = {2 * s.I, s.H, pick_split(2 * s.I, s.H, cus, kMaxRows, 8)};
-    s.down = {s.H, s.I, pick_split(s.H, s.I, cus, kMaxRows, 8)};
+    s.down = {s.H, s.I, pick_split(s.H, s.I, cus, kMaxRows, od_steps)};
     // lm_head: 128-column workgroups halve the activation re-reads; at
     // vocab 151936, 64 rows: 93.7 us against 111 us per call.
     s.lm = {s.V, s.H, 1, s.V % (2 * kGN) == 0 ? 2 : 1};
