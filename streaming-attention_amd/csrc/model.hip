@@ -469,7 +469,9 @@ Shapes shapes_of(const sa_qwen3_desc& d, int cus) {
     // workgroups instead of 128).  Measured on the 28-layer B = 64 step:
     // 20.79 ms against 20.98 ms with 2-step splits everywhere (the partials'
     // traffic outweighed the extra workgroups); o/down at 4 / 8 / 16 steps
-    // 20.76 / 20.78 / 21.00 ms on one box.
+    // 20.76 / 20.78 / 21.00 ms on one box.  128-column workgroups for qkv
+    // and gate_up measured slower (20.72 ms, 20.79 with 4-step splits,
+    // against 20.67 ms on another box).
     s.qkv = {s.Nqkv, s.H, pick_split(s.Nqkv, s.H, cus, kMaxRows, 8)};
     const int od_steps = 4;
     s.o = {s.H, s.Nq, pick_split(s.H, s.Nq, cus, kMaxRows, od_steps)};
