@@ -713,6 +713,12 @@ int pick_chunk(long long total_rows, long long max_len, long long max_chunk = 1L
         c = std::min<long long>(std::max<long long>((total_rows + target - 1) / target, kChunkLo), kChunkHi);
         c = std::max<long long>(c, (max_len + kSplitTarget - 1) / kSplitTarget);
         c = (c + kChunkAlign - 1) / kChunkAlign * kChunkAlign;
+        // Above 1024 tokens, the nearest multiple of 512 (still within the
+        // split caps below).  B = 64 paged bf16 (979-31,078 tokens), same
+        // box: 2048-token chunks 0.680 ms per call and 20.47 ms per 28-layer
+        // model step, against 0.689 / 20.71 at the 2176 of 128-alignment,
+        // 0.685 / 20.69 at 1792 and 0.683 / 20.64 at 2304.
+        if (c > 1024) c = (c + 256) / 512 * 512;
     }
     return (int)std::max<long long>(std::min<long long>(c, max_chunk), cap_floor);
 }

@@ -2,7 +2,7 @@
 benchmark measures: B = 64 sequences of U[512, 32768] tokens (seeded: 979 to
 31,078), 16 query / 8 KV heads, D = 128, bf16 KV in 64-token pages assigned
 from a seeded shuffle of the pool.  At this size the default launch picks
-2,176-token chunks (34 pages each), so chunks span many pages and page
+2,048-token chunks (32 pages each), so chunks span many pages and page
 switches fall inside a wave's tiles.
 
 Each checked sequence is compared with the oracle's STANDARD decode
