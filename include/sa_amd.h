@@ -268,6 +268,19 @@ sa_status sa_append_decode(sa_kvcache* cache, int layer, const float* q, const f
                            float scale, float* out, float* q_out, void* ws, size_t ws_bytes,
                            int commit, sa_stream_t stream);
 
+/* sa_append_decode with q, k and v given as the sum of n_part split-K partial
+ * products of the layer's fused qkv projection, summed in order 0 .. n_part-1
+ * from zero: part [n_part][n_seq][(n_q_heads + 2 n_kv_heads) D] fp32, each row
+ * its q columns, then k, then v (the q/k/v split of qwen3_ops.cpp:652-688).
+ * The device decoder's step calls this form; a caller whose projection ends
+ * in split-K partials saves the pass that sums them. */
+sa_status sa_append_decode_partials(sa_kvcache* cache, int layer, const float* part, int n_part,
+                                    int n_seq, const int32_t* seq_ids, int n_q_heads,
+                                    const float* q_norm_w, const float* k_norm_w, float eps,
+                                    const float* rope_cos, const float* rope_sin, int rope_max_pos,
+                                    float scale, float* out, float* q_out, void* ws, size_t ws_bytes,
+                                    int commit, sa_stream_t stream);
+
 /* Dense copy of a sequence's first len tokens: k_out, v_out [n_kv_heads][len][D]
  * fp32 (serves KVCache::get_cached_keys / get_cached_values, kv_cache.h:161-237). */
 sa_status sa_kvcache_gather(const sa_kvcache* cache, int layer, int seq, int len,

@@ -93,6 +93,8 @@ SIGNATURES = {
     "sa_axpby_f32": (_I, [_P, _F, _P, _F, _SZ, _P, _P]),
     "sa_paged_decode_ws_bytes": (_SZ, [_P, _I, _I]),
     "sa_paged_decode": (_I, [_P, _I, _P, _I, _P, _I, _I, _F, _P, _P, _SZ, _P]),
+    "sa_append_decode_partials": (_I, [_P, _I, _P, _I, _I, _P, _I, _P, _P, _F, _P, _P, _I, _F, _P, _P, _P,
+                                       _SZ, _I, _P]),
     "sa_kvcache_gather": (_I, [_P, _I, _I, _I, _P, _P, _P]),
     "sa_append_decode": (_I, [_P, _I, _P, _P, _P, _I, _P, _I, _P, _P, _F, _P, _P, _I, _F, _P, _P, _P, _SZ,
                               _I, _P]),
@@ -308,6 +310,26 @@ class KVCache:
             _rows(seq_ids, n_seq), Hq, _ptr(_f32(q_norm_w, "q_norm_w")), _ptr(_f32(k_norm_w, "k_norm_w")), eps,
             _ptr(cos), _ptr(sin), max_pos, scale, _ptr(out), _ptr(q_out), _ptr(ws), ws.numel(), int(bool(commit)),
             _stream(stream)))
+        return out
+
+    def append_decode_partials(self, layer: int, part, n_q_heads: int, scale: float, q_norm_w=None,
+                               k_norm_w=None, eps: float = 1e-6, rope=None, out=None, q_out=None, ws=None,
+                               commit: bool = False, seq_ids=None, stream=None):
+        """append_decode with q, k and v of the new token given as split-K
+        partials: part [n_part, n_seq, (Hq + 2 Hkv) D], summed in order."""
+        import torch
+        n_part, n_seq, _ = part.shape
+        D = self.desc.head_dim
+        out = torch.empty(n_seq, n_q_heads, D, dtype=torch.float32, device=part.device) if out is None else out
+        if ws is None:
+            need = self.decode_ws_bytes(n_seq, n_q_heads)
+            ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=part.device)
+        cos, sin = (None, None) if rope is None else rope
+        max_pos = 0 if rope is None else cos.shape[0]
+        check(lib().sa_append_decode_partials(
+            self.handle, layer, _ptr(_f32(part, "part")), n_part, n_seq, _rows(seq_ids, n_seq), n_q_heads,
+            _ptr(_f32(q_norm_w, "q_norm_w")), _ptr(_f32(k_norm_w, "k_norm_w")), eps, _ptr(cos), _ptr(sin), max_pos,
+            scale, _ptr(out), _ptr(q_out), _ptr(ws), ws.numel(), int(bool(commit)), _stream(stream)))
         return out
 
     def gather(self, layer: int, seq: int, length: int, stream=None):

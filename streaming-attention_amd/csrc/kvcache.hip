@@ -590,11 +590,17 @@ sa_status append_decode_impl(sa_kvcache* c, int layer, const float* q, const flo
     FusedAppend f{};
     f.k = k; f.v = v; f.wq = q_norm_w; f.wk = k_norm_w; f.eps = eps;
     f.cos_t = rope_cos; f.sin_t = rope_sin; f.rope_max_pos = rope_max_pos;
-    f.q_out = q_out; f.lens = c->d_lens; f.pos = pos.data(); f.commit = commit != 0;
+    // One launch (up to kRowsPerLaunch rows) commits inside the kernel.  A
+    // call of more rows takes several launches; their lengths are published
+    // by one pass after the last launch is enqueued, so a launch that fails
+    // leaves every device length as it was.
+    const bool in_kernel_commit = commit && n_seq <= kRowsPerLaunch;
+    f.q_out = q_out; f.lens = c->d_lens; f.pos = pos.data(); f.commit = in_kernel_commit;
     f.part = part; f.part_S = n_part; f.part_M = n_seq;
     SA_TRY(decode_paged_fused(pv, q, n_seq, seq_ids, n_q_heads, f, max_len, total, scale, out, ws, ws_bytes,
                               stream));
     if (commit) {
+        if (!in_kernel_commit) SA_TRY(publish_lens(c, seq_ids, n_seq, 1, 1, stream));
         vd = c->pt.commit(seq_ids, n_seq, 1);   // checked above: cannot be refused
         if (!vd.ok()) return refused(vd);
     }
@@ -604,12 +610,13 @@ sa_status append_decode_impl(sa_kvcache* c, int layer, const float* q, const flo
 }  // namespace
 
 sa_status append_decode_partials(sa_kvcache* c, int layer, const float* part, int n_part, int n_seq,
-                                 int n_q_heads, const float* q_norm_w, const float* k_norm_w, float eps,
-                                 const float* rope_cos, const float* rope_sin, int rope_max_pos, float scale,
-                                 float* out, void* ws, size_t ws_bytes, int commit, hipStream_t st) {
+                                 const int32_t* seq_ids, int n_q_heads, const float* q_norm_w,
+                                 const float* k_norm_w, float eps, const float* rope_cos, const float* rope_sin,
+                                 int rope_max_pos, float scale, float* out, float* q_out, void* ws,
+                                 size_t ws_bytes, int commit, hipStream_t st) {
     if (!part) return fail(SA_EINVAL, "null projection partials");
-    return append_decode_impl(c, layer, nullptr, nullptr, nullptr, part, n_part, n_seq, nullptr, n_q_heads,
-                              q_norm_w, k_norm_w, eps, rope_cos, rope_sin, rope_max_pos, scale, out, nullptr, ws,
+    return append_decode_impl(c, layer, nullptr, nullptr, nullptr, part, n_part, n_seq, seq_ids, n_q_heads,
+                              q_norm_w, k_norm_w, eps, rope_cos, rope_sin, rope_max_pos, scale, out, q_out, ws,
                               ws_bytes, commit, st);
 }
 
@@ -625,6 +632,18 @@ extern "C" sa_status sa_append_decode(sa_kvcache* c, int layer, const float* q, 
     return append_decode_impl(c, layer, q, k, v, nullptr, 0, n_seq, seq_ids, n_q_heads, q_norm_w, k_norm_w, eps,
                               rope_cos, rope_sin, rope_max_pos, scale, out, q_out, ws, ws_bytes, commit,
                               as_stream(stream));
+}
+
+extern "C" sa_status sa_append_decode_partials(sa_kvcache* c, int layer, const float* part, int n_part,
+                                               int n_seq, const int32_t* seq_ids, int n_q_heads,
+                                               const float* q_norm_w, const float* k_norm_w, float eps,
+                                               const float* rope_cos, const float* rope_sin, int rope_max_pos,
+                                               float scale, float* out, float* q_out, void* ws, size_t ws_bytes,
+                                               int commit, sa_stream_t stream) {
+    clear_error();
+    return append_decode_partials(c, layer, part, n_part, n_seq, seq_ids, n_q_heads, q_norm_w, k_norm_w, eps,
+                                  rope_cos, rope_sin, rope_max_pos, scale, out, q_out, ws, ws_bytes, commit,
+                                  as_stream(stream));
 }
 
 extern "C" sa_status sa_kvcache_gather(const sa_kvcache* c, int layer, int seq, int len, float* k_out,

@@ -803,9 +803,9 @@ extern "C" sa_status sa_qwen3_decode_step(sa_qwen3* m, sa_kvcache* cache, const 
         // and the paged decode in one launch per 64 sequences (plus the LSE
         // merge of multi-chunk sequences); the last layer's call also commits
         // the token.  (A separate split kernel cost 4.7 us per layer.)
-        SA_TRY(sa::append_decode_partials(cache, l, m->part, s.qkv.S, M, s.Hq, L.q_norm, L.k_norm, eps,
-                                          m->rope_cos, m->rope_sin, d.max_pos, scale, m->attn, m->ws, m->ws_bytes,
-                                          l + 1 == d.num_layers ? 1 : 0, st));
+        SA_TRY(sa::append_decode_partials(cache, l, m->part, s.qkv.S, M, nullptr, s.Hq, L.q_norm, L.k_norm, eps,
+                                          m->rope_cos, m->rope_sin, d.max_pos, scale, m->attn, nullptr, m->ws,
+                                          m->ws_bytes, l + 1 == d.num_layers ? 1 : 0, st));
         SA_TRY(gemm(m->attn, M, L.o, s.o, m->part, st));
         hipLaunchKernelGGL(residual_norm_kernel, dim3(M), dim3(256), 0, st, m->part, s.o.S, M, s.H, m->x,
                            L.post_norm, eps, m->h);

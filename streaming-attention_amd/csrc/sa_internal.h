@@ -18,6 +18,12 @@ sa_status fail(sa_status st, const std::string& msg);
 sa_status hip_fail(hipError_t e, const char* what);
 int device_cu_count();
 
+// Process-wide tile settings (sa_set_attention_blocks); 0 = the launch's own
+// choice.  q: query rows per prefill workgroup and head; kv: tokens per
+// split-KV chunk of decode attention.
+int attn_q_block();
+int attn_kv_block();
+
 #define SA_HIP_TRY(expr)                                   \
     do {                                                   \
         hipError_t _e = (expr);                            \
@@ -257,9 +263,10 @@ sa_status qknorm_rope_append_partials(sa_kvcache* c, int layer, const float* par
 
 // sa_append_decode with q, k and v read from split-K partials (FusedAppend).
 sa_status append_decode_partials(sa_kvcache* c, int layer, const float* part, int n_part, int n_seq,
-                                 int n_q_heads, const float* q_norm_w, const float* k_norm_w, float eps,
-                                 const float* rope_cos, const float* rope_sin, int rope_max_pos, float scale,
-                                 float* out, void* ws, size_t ws_bytes, int commit, hipStream_t st);
+                                 const int32_t* seq_ids, int n_q_heads, const float* q_norm_w,
+                                 const float* k_norm_w, float eps, const float* rope_cos, const float* rope_sin,
+                                 int rope_max_pos, float scale, float* out, float* q_out, void* ws,
+                                 size_t ws_bytes, int commit, hipStream_t st);
 
 size_t paged_ws(int n_seq, int n_q, int n_kv, int d, int max_pages);
 // seq_ids: host array of cache rows (NULL: 0 .. n_seq-1), already checked.

@@ -14,36 +14,14 @@ import numpy as np
 import pytest
 import torch
 
+from model_parity import SubsetChecker, host_weights, rel_l2
+
 pytestmark = pytest.mark.gpu
 
 SMALL = dict(num_layers=2, hidden=256, intermediate=512, vocab=1024, n_q_heads=4, n_kv_heads=2,
              head_dim=64, rms_eps=1e-6, rope_theta=1e6)
 SHAPE_KEYS = ("num_layers", "hidden", "intermediate", "vocab", "n_q_heads", "n_kv_heads", "head_dim",
               "rms_eps", "rope_theta")
-
-
-def rel_l2(a, b):
-    a = np.asarray(a, np.float64)
-    b = np.asarray(b, np.float64)
-    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
-
-
-def host_weights(sa, model, cfg):
-    """The model's weights as the oracle's fp32 dict (exact: bf16 widens exactly)."""
-    from oracle.qwen3_model import TENSORS
-    H, I, V = cfg["hidden"], cfg["intermediate"], cfg["vocab"]
-    Hq, Hkv, D = cfg["n_q_heads"], cfg["n_kv_heads"], cfg["head_dim"]
-    shapes = {sa.QW_EMBED: (V, H), sa.QW_LM_HEAD: (V, H), sa.QW_FINAL_NORM: (H,), sa.QW_IN_NORM: (H,),
-              sa.QW_QKV: ((Hq + 2 * Hkv) * D, H), sa.QW_Q_NORM: (D,), sa.QW_K_NORM: (D,),
-              sa.QW_O: (H, Hq * D), sa.QW_POST_NORM: (H,), sa.QW_GATE_UP: (2 * I, H), sa.QW_DOWN: (H, I)}
-
-    def get(which, layer=0):
-        return model.tensor(which, layer).float().cpu().numpy().reshape(shapes[which])
-
-    ids = dict(zip(TENSORS, (sa.QW_IN_NORM, sa.QW_QKV, sa.QW_Q_NORM, sa.QW_K_NORM, sa.QW_O, sa.QW_POST_NORM,
-                             sa.QW_GATE_UP, sa.QW_DOWN)))
-    return {"embed": get(sa.QW_EMBED), "final_norm": get(sa.QW_FINAL_NORM), "lm_head": get(sa.QW_LM_HEAD),
-            "layers": [{t: get(ids[t], l) for t in TENSORS} for l in range(cfg["num_layers"])]}
 
 
 def make_cache(sa, synth, cfg, lens, steps, kv_dtype, seed):
@@ -178,4 +156,40 @@ def test_model_rejects_bad_calls(sa):
     assert sa.lib().sa_qwen3_create(C.byref(d), 1, C.byref(h)) == sa.SA_EINVAL
     cache.close()
     good.close()
+    model.close()
+
+
+def test_model_decode_b64_workload_rows(sa, oracle, synth):
+    """The 64-sequence workload of the decode benchmark as it runs: the
+    Qwen3-0.6B shape (weights N(0, 0.02), seed 71), context lengths
+    U[512, 32768] (seed 70), 64-token pages from a seeded shuffle, bf16 KV
+    N(0,1).  Its launches are the 4-wave fused step on 8 x 16 x 64
+    workgroups.  Two greedy steps; the longest sequence, the shortest and
+    two of at least three 2,048-token chunks against the oracle on the
+    device's weights and the gathered cache: each row's logits within
+    relative L2 2e-2, greedy tokens identical."""
+    cfg = dict(sa.QWEN3_0_6B)
+    B, steps = 64, 2
+    lens = synth.batch_lengths(B, 512, 32768, 70)
+    order = np.argsort(lens)
+    multi = [int(s) for s in synth.permutation(70, 3, B) if lens[s] > 3 * 2048 and s != order[-1]][:2]
+    seqs = [int(order[-1]), int(order[0])] + multi
+    model = sa.Qwen3(B, max(lens) + steps + 1)
+    model.init_random(71, 0.02)
+    cache = make_cache(sa, synth, cfg, lens, steps, sa.SA_DTYPE_BF16, 71)
+    chk = SubsetChecker(sa, oracle, model, cache, cfg, seqs, steps, True)
+    tokens = torch.tensor([int(x * cfg["vocab"]) % cfg["vocab"] for x in synth.uniform(71, 3, B)],
+                          dtype=torch.int32, device="cuda")
+    logits = torch.empty(B, cfg["vocab"], dtype=torch.float32, device="cuda")
+    for t in range(steps):
+        want = chk.want(tokens.cpu().numpy())
+        nxt = model.decode_step(cache, tokens, logits=logits)
+        res = chk.compare(want, logits.cpu().numpy(), nxt.cpu().numpy())
+        print(f"step {t} rows {seqs} (lens {[lens[s] for s in seqs]}): worst row rel-L2 "
+              f"{res['worst_row_rel_l2']:.2e}, max-abs {res['max_abs_err']:.2e}")
+        assert res["worst_row_rel_l2"] <= 2e-2, (t, res["row_rel_l2"])
+        assert res["tokens_identical"], t
+        tokens = nxt
+    assert [cache.length(s) for s in range(B)] == [L + steps for L in lens]
+    cache.close()
     model.close()
