@@ -309,6 +309,31 @@ sa_status sa_prefill_causal_strided(const void* q, const void* k, const void* v,
                                     sa_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * Tile sizes of the attention kernels, for the whole process: the
+ * counterpart of the reference's tensor_cpp::g_q_block_size and
+ * g_kv_block_size (tensor_cpp/src/ops.cpp:1630-1631), which benchmark_qwen3
+ * sets from --q-block-size and --kv-block-size (benchmark_qwen3.cpp:1072-1073).
+ *
+ * q_block: query rows per prefill workgroup and head.  fp32: 32 (workgroups
+ * whose waves split each key tile), 64 or 128.  bf16: 32 (the split-key
+ * kernel; head_dim 128 and even GQA groups) or the workgroup width whose
+ * per-head tile it is (16/8 heads: 64 or 128); a bf16 shape with no kernel of
+ * that tile keeps the launch's own choice.  The key tile stays 64 rows.
+ * kv_block: tokens per split-KV chunk of decode attention (the range one
+ * workgroup streams before the log-sum-exp merge), a multiple of 64 in
+ * [64, 16384]; raised where a sequence would need more than 1,024 chunks.
+ * 0 selects the launch's own choice.  Other values return SA_EINVAL and
+ * change nothing.  Results agree across settings up to fp32 rounding.
+ * ------------------------------------------------------------------------ */
+sa_status sa_set_attention_blocks(int q_block, int kv_block);
+sa_status sa_get_attention_blocks(int* q_block, int* kv_block);
+
+/* The query rows per workgroup and head a prefill launch of this shape takes
+ * under the current settings, or a negative sa_status for a shape the
+ * prefill refuses. */
+int sa_prefill_query_tile(sa_dtype dtype, int batch, int n_q_heads, int n_kv_heads, int L, int D);
+
+/* ------------------------------------------------------------------------
  * Dense fp32 operators of the decoder layer (projections, norms, MLP,
  * residuals), for callers whose weights are fp32.  All pointers are device
  * pointers; rows are contiguous.

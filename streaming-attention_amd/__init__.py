@@ -100,6 +100,9 @@ SIGNATURES = {
                               _I, _P]),
     "sa_prefill_causal": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _P]),
     "sa_prefill_causal_strided": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _F, _P, _P]),
+    "sa_set_attention_blocks": (_I, [_I, _I]),
+    "sa_get_attention_blocks": (_I, [C.POINTER(_I), C.POINTER(_I)]),
+    "sa_prefill_query_tile": (_I, [_I, _I, _I, _I, _I, _I]),
     "sa_qwen3_create": (_I, [C.POINTER(Qwen3Desc), _I, C.POINTER(_P)]),
     "sa_qwen3_destroy": (_I, [_P]),
     "sa_qwen3_get_desc": (_I, [_P, C.POINTER(Qwen3Desc)]),
@@ -424,6 +427,26 @@ def axpby(x, a: float, y=None, b: float = 0.0, out=None, stream=None):
 
 
 # ---------------------------------------------------------------- prefill
+
+def set_attention_blocks(q_block: int = 0, kv_block: int = 0) -> None:
+    """Process-wide attention tiles (0 = the launch's own choice): prefill
+    query rows per workgroup and head, decode split-KV chunk tokens."""
+    check(lib().sa_set_attention_blocks(int(q_block), int(kv_block)))
+
+
+def get_attention_blocks() -> tuple[int, int]:
+    q, kv = C.c_int(), C.c_int()
+    check(lib().sa_get_attention_blocks(C.byref(q), C.byref(kv)))
+    return q.value, kv.value
+
+
+def prefill_query_tile(dtype: int, batch: int, n_q_heads: int, n_kv_heads: int, L: int, D: int) -> int:
+    """Query rows per workgroup and head of a prefill launch of this shape."""
+    r = lib().sa_prefill_query_tile(dtype, batch, n_q_heads, n_kv_heads, L, D)
+    if r < 0:
+        check(r)
+    return r
+
 
 def prefill_causal(q, k, v, scale: float, out=None, stream=None):
     """q [B, Hq, L, D], k/v [B, Hkv, L, D] (fp32 or bf16) -> out fp32 [B, Hq, L, D]."""

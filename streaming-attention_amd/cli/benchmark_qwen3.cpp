@@ -11,9 +11,13 @@
 //
 // Options the GPU path has no use for are accepted and reported: --mode,
 // --method, --parallel-strategy, --attention-algo and --attention all select
-// the same kernels (the online-softmax kernels are exact attention), --threads
-// sets nothing, and the kernels' tile sizes are fixed (--q-block-size and
-// --kv-block-size are printed, not applied).  --synthetic replaces --model
+// the same kernels (the online-softmax kernels are exact attention) and
+// --threads sets nothing.  --q-block-size and --kv-block-size set the
+// attention tiles, as the reference sets g_q_block_size / g_kv_block_size
+// from them (benchmark_qwen3.cpp:1072-1073): the prefill's query rows per
+// workgroup and head (32, 64 or 128) and the decode's split-KV chunk (a
+// multiple of 64 tokens); unset, each launch picks its own, and the header
+// prints the query tile the prefill launch takes.  --synthetic replaces --model
 // with seeded random weights of the Qwen3-0.6B shape; --synthetic-shape,
 // --seed and --std (not in the reference) pick another shape and draw, and
 // --logits-out writes --verify's logits, so the command line can be checked
@@ -57,7 +61,7 @@ struct Config {
     std::string mode = "omp", method = "baseline", parallel_strategy = "headwise";
     std::string attention_algo = "standard", attention = "standard";
     int batch_size = 1, prompt_len = 128, gen_len = 100, iters = 10, num_threads = 16, warmup = 2;
-    int q_block_size = 128, kv_block_size = 128;
+    int q_block_size = 0, kv_block_size = 0;     // 0: each launch picks its tile
     bool verbose = false, use_kv_cache = true, compare_kv_cache = false, verify_mode = false;
     bool kv_bf16 = false;
     std::vector<int> shape;                 // layers, hidden, intermediate, vocab, q heads, kv heads, head_dim
@@ -85,8 +89,10 @@ void usage(const char* prog) {
               << "  --synthetic-shape L,H,I,V,Hq,Hkv,D   shape of the synthetic model [28,1024,3072,151936,16,8,128]\n"
               << "  --seed N, --std X         synthetic draw: seed [42], N(0, X) matrices, 1 + N(0, X) norms [0.02]\n"
               << "  --logits-out PATH         --verify writes both paths' last logits there (fp32 [2][batch][vocab])\n"
+              << "  --q-block-size N          prefill query rows per workgroup and head: 32, 64, 128 [auto]\n"
+              << "  --kv-block-size N         decode split-KV chunk, tokens: multiple of 64 in [64, 16384] [auto]\n"
               << "  --mode, --method, --parallel-strategy, --attention-algo, --attention,\n"
-              << "  --threads, --q-block-size, --kv-block-size: accepted for compatibility\n"
+              << "  --threads: accepted for compatibility\n"
               << "  --verbose, --help\n";
 }
 
@@ -178,6 +184,12 @@ Config parse(int argc, char** argv) {
     }
     if (c.prompt_len < 1 || c.gen_len < 1 || c.iters < 1) {
         std::cerr << "error: --prompt-len, --gen-len and --iters must be at least 1\n";
+        std::exit(1);
+    }
+    // The tiles are process-wide settings of the library (host state only).
+    if (sa_set_attention_blocks(c.q_block_size, c.kv_block_size) != SA_OK) {
+        std::cerr << "error: --q-block-size " << c.q_block_size << " / --kv-block-size " << c.kv_block_size
+                  << ": " << sa_last_error() << "\n";
         std::exit(1);
     }
     return c;
@@ -319,6 +331,16 @@ double bench_decode_no_cache(Runner& r) {
     return ms_since(t0);
 }
 
+std::string block_name(int b) { return b ? std::to_string(b) : std::string("auto"); }
+
+// The query tile the model's prefill attention (fp32, token-major q/k/v)
+// takes for this benchmark's shape.
+int prefill_tile(const Config& c, const Runner& r) {
+    const int L = c.phase == "prefill" ? c.prompt_len : 16;
+    return sa_prefill_query_tile(SA_DTYPE_F32, c.batch_size, r.desc.n_q_heads, r.desc.n_kv_heads, L,
+                                 r.desc.head_dim);
+}
+
 void print_header(const Config& c, const Runner& r) {
     std::cout << "\n==================================================\n"
               << "         Qwen3 Performance Benchmark (MI355X)\n"
@@ -337,8 +359,11 @@ void print_header(const Config& c, const Runner& r) {
     std::cout << "batch size:      " << c.batch_size << "\n"
               << "iterations:      " << c.iters << "\n"
               << "KV cache dtype:  " << (c.kv_bf16 ? "bf16" : "fp32") << "\n"
-              << "block sizes:     q " << c.q_block_size << ", kv " << c.kv_block_size
-              << " (accepted; the GPU kernels use fixed tiles)\n"
+              << "block sizes:     q " << block_name(c.q_block_size) << ", kv " << block_name(c.kv_block_size) << "\n"
+              << "attention tiles: prefill " << prefill_tile(c, r) << " queries per workgroup and head, 64-key tiles; "
+              << "decode split-KV chunk "
+              << (c.kv_block_size ? std::to_string(c.kv_block_size) + " tokens" : std::string("per launch"))
+              << "\n"
               << "model config:    layers " << r.desc.num_layers << ", heads " << r.desc.n_q_heads << "/"
               << r.desc.n_kv_heads << " x " << r.desc.head_dim << ", hidden " << r.desc.hidden << ", vocab "
               << r.desc.vocab << "\n"
@@ -381,7 +406,8 @@ int verify(Runner& r) {
         const float m = std::max(std::fabs(a[i]), std::fabs(b[i]));
         max_rel = std::max(max_rel, m > 1e-6f ? d / m : d);
     }
-    std::cout << "verify: " << n << " tokens, batch " << B << "\n"
+    std::cout << "verify: " << n << " tokens, batch " << B << ", block sizes q " << block_name(r.cfg.q_block_size)
+              << ", kv " << block_name(r.cfg.kv_block_size) << "\n"
               << "  prefill of the whole sequence -> next token " << next_a << "\n"
               << "  prefill of 1 + " << n - 1 << " decode steps   -> next token " << next_b << "\n"
               << "  last-position logits: max abs diff " << max_diff << ", max rel diff " << max_rel * 100.f

@@ -1,6 +1,7 @@
 // Error state and device queries shared by the C ABI entry points.
 #include "sa_internal.h"
 
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -39,6 +40,33 @@ int device_cu_count() {
     return cache[dev];
 }
 
+namespace {
+std::atomic<int> g_q_block{0};
+std::atomic<int> g_kv_block{0};
+}  // namespace
+
+int attn_q_block() { return g_q_block.load(std::memory_order_relaxed); }
+int attn_kv_block() { return g_kv_block.load(std::memory_order_relaxed); }
+
 }  // namespace sa
 
 extern "C" const char* sa_last_error(void) { return sa::g_last_error.c_str(); }
+
+extern "C" sa_status sa_set_attention_blocks(int q_block, int kv_block) {
+    sa::clear_error();
+    if (q_block != 0 && q_block != 32 && q_block != 64 && q_block != 128)
+        return sa::fail(SA_EINVAL, "q_block_size must be 32, 64 or 128 (0: automatic)");
+    if (kv_block != 0 && (kv_block < 64 || kv_block > 16384 || kv_block % 64 != 0))
+        return sa::fail(SA_EINVAL, "kv_block_size must be a multiple of 64 in [64, 16384] (0: automatic)");
+    sa::g_q_block.store(q_block, std::memory_order_relaxed);
+    sa::g_kv_block.store(kv_block, std::memory_order_relaxed);
+    return SA_OK;
+}
+
+extern "C" sa_status sa_get_attention_blocks(int* q_block, int* kv_block) {
+    sa::clear_error();
+    if (!q_block || !kv_block) return sa::fail(SA_EINVAL, "null pointer");
+    *q_block = sa::attn_q_block();
+    *kv_block = sa::attn_kv_block();
+    return SA_OK;
+}

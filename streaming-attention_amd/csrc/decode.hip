@@ -702,12 +702,21 @@ constexpr int kChunkAlign = 128;
 // SA_DECODE_CHUNK overrides those rules (still at most kSplitCap chunks).
 // max_chunk bounds the result (paged chunks: kMaxChunkPages pages) unless
 // kSplitCap forbids it.
+// A chunk the caller fixed: sa_set_attention_blocks' kv block, else
+// SA_DECODE_CHUNK; 0 when neither is set.
+int forced_chunk() {
+    const int set = attn_kv_block();
+    return set > 0 ? set : env_int("SA_DECODE_CHUNK", 0);
+}
+
 int pick_chunk(long long total_rows, long long max_len, long long max_chunk = 1LL << 30) {
     const long long cap_floor = round64((max_len + kSplitCap - 1) / kSplitCap);
-    const int forced = env_int("SA_DECODE_CHUNK", 0);
+    const int forced = forced_chunk();
     long long c;
     if (forced > 0) {
-        c = std::max<long long>(round64(forced), kMinChunk);
+        // A fixed chunk may be a single page: the waves past its tiles see
+        // none and contribute nothing to the chunk's merge.
+        c = std::max<long long>(round64(forced), 64);
     } else {
         const long long target = (long long)kGroupsPerCu * device_cu_count();
         c = std::min<long long>(std::max<long long>((total_rows + target - 1) / target, kChunkLo), kChunkHi);
@@ -725,7 +734,8 @@ int pick_chunk(long long total_rows, long long max_len, long long max_chunk = 1L
 
 // Upper bound of the split count any call may use for sequences up to max_len.
 long long max_splits_for(long long max_len) {
-    const long long c = std::max<long long>(kMinChunk, round64((max_len + kSplitCap - 1) / kSplitCap));
+    // Fixed chunks may be as short as one 64-token page.
+    const long long c = std::max<long long>(64, round64((max_len + kSplitCap - 1) / kSplitCap));
     return (max_len + c - 1) / c;
 }
 
@@ -851,7 +861,7 @@ sa_status decode_dense(const float* q, const float* k, const float* v, int batch
     // one round of workgroups.  Measured per single-head call: T = 1024
     // 8.0-8.4 against 9.9 us, T = 8192 9.4-9.7 against 10.8-11.0 us; at
     // T = 65536 it would mean two rounds (17.6 against 16.5 us).
-    if (env_int("SA_DECODE_CHUNK", 0) <= 0 && rows <= 64LL * device_cu_count()) a.chunk = kMinChunk;
+    if (forced_chunk() <= 0 && rows <= 64LL * device_cu_count()) a.chunk = kMinChunk;
     a.n_split = (T + a.chunk - 1) / a.chunk;
     const long long bh = (long long)batch * n_q;
     const size_t need = ws_bytes_for(bh, a.n_split, d);

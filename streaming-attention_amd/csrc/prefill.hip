@@ -864,7 +864,7 @@ prefill_bf16_split_kernel(PrefillArgs pa) {
 // ===========================================================================
 // fp32 kernel
 // ===========================================================================
-constexpr int kFQTile = 128;    // queries per workgroup
+constexpr int kFQTile = 128;    // queries per workgroup (4 waves of 32; 64 with 16 per wave)
 constexpr int kFThreads = 256;
 constexpr int kF32SplitW = 8;   // waves of the short-prompt fp32 kernel
 
@@ -924,10 +924,15 @@ __device__ __forceinline__ float xmax16_32(float v) {
     return v;
 }
 
-template <int D>
+// Four waves of GQ groups of 16 queries: a workgroup serves 64 GQ queries
+// of one head (GQ = 2: 128, GQ = 1: 64).
+template <int D, int GQ = 2>
 __global__ void __launch_bounds__(kFThreads)
 prefill_f32_kernel(PrefillArgs pa) {
     using Lds = F32Lds<D>;
+    constexpr int NT = kFThreads;
+    constexpr int QW = 16 * GQ;            // queries per wave
+    constexpr int QT = 4 * QW;             // queries per workgroup
     const int L = pa.L;
     const float sl2 = pa.scale * kLog2eP;
     constexpr int NDB = D / 16;            // 16-wide d blocks of the output
@@ -946,30 +951,32 @@ prefill_f32_kernel(PrefillArgs pa) {
     const float* V = static_cast<const float*>(pa.v) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
     const long long q_row = pa.qs[2], kv_row = pa.kvs[2];
 
-    const int q_wave0 = wk.qt * kFQTile + wave * 32;   // first query of this wave
-    const int n_kt = (min(L, (wk.qt + 1) * kFQTile) - 1) / kKTile + 1;
+    const int q_wave0 = wk.qt * QT + wave * QW;   // first query of this wave
+    const int n_kt = (min(L, (wk.qt + 1) * QT) - 1) / kKTile + 1;
 
-    F32Stage<D> next;
-    f32_load<D>(next, K, V, kv_row, 0, L);
+    F32Stage<D, NT> next;
+    f32_load<D, NT>(next, K, V, kv_row, 0, L);
 
     // Q^T fragments (B operand) per 16-query group.
-    float qf[2][QF];
+    float qf[GQ][QF];
 #pragma unroll
-    for (int gq = 0; gq < 2; ++gq) {
+    for (int gq = 0; gq < GQ; ++gq) {
         const int qi = min(q_wave0 + gq * 16 + c16, L - 1);
 #pragma unroll
         for (int s = 0; s < QF; ++s) qf[gq][s] = Q[qi * q_row + s * 4 + g];
     }
 
-    f32x4_t acc[2][NDB];
+    f32x4_t acc[GQ][NDB];
 #pragma unroll
-    for (int gq = 0; gq < 2; ++gq)
+    for (int gq = 0; gq < GQ; ++gq)
 #pragma unroll
         for (int db = 0; db < NDB; ++db) acc[gq][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    float m_run[2] = {-INFINITY, -INFINITY};
-    float l_run[2] = {0.f, 0.f};
+    float m_run[GQ];
+    float l_run[GQ];
+#pragma unroll
+    for (int gq = 0; gq < GQ; ++gq) { m_run[gq] = -INFINITY; l_run[gq] = 0.f; }
 
-    f32_store<D>(next, stage_base, stage_base + Lds::K_ELEMS);
+    f32_store<D, NT>(next, stage_base, stage_base + Lds::K_ELEMS);
     __syncthreads();
 
     for (int kt = 0; kt < n_kt; ++kt) {
@@ -977,12 +984,12 @@ prefill_f32_kernel(PrefillArgs pa) {
         const float* sK = stage_base + (kt & 1) * Lds::STAGE;
         const float* sV = sK + Lds::K_ELEMS;
         const bool more = kt + 1 < n_kt;
-        if (more) f32_load<D>(next, K, V, kv_row, key0 + kKTile, L);
+        if (more) f32_load<D, NT>(next, K, V, kv_row, key0 + kKTile, L);
 
-        if (key0 <= q_wave0 + 31 && q_wave0 < L) {   // else the whole wave is above the diagonal
+        if (key0 <= q_wave0 + QW - 1 && q_wave0 < L) {   // else the whole wave is above the diagonal
             const bool diag = key0 + kKTile - 1 > q_wave0;
 #pragma unroll
-            for (int gq = 0; gq < 2; ++gq) {
+            for (int gq = 0; gq < GQ; ++gq) {
                 const int qi = q_wave0 + gq * 16 + c16;
                 // ---- S^T = K Q^T for 4 blocks of 16 keys ----
                 f32x4_t st[4];
@@ -1045,14 +1052,14 @@ prefill_f32_kernel(PrefillArgs pa) {
             // The other stage was last read before the barrier that ended the
             // previous iteration.
             float* nK = stage_base + ((kt + 1) & 1) * Lds::STAGE;
-            f32_store<D>(next, nK, nK + Lds::K_ELEMS);
+            f32_store<D, NT>(next, nK, nK + Lds::K_ELEMS);
         }
         __syncthreads();
     }
 
     // ---- normalise and store: lane holds O^T[d = db*16 + 4g + i][q = c16] ----
 #pragma unroll
-    for (int gq = 0; gq < 2; ++gq) {
+    for (int gq = 0; gq < GQ; ++gq) {
         const int qi = q_wave0 + gq * 16 + c16;
         if (qi >= L) continue;
         const float inv = 1.0f / l_run[gq];
@@ -1311,10 +1318,11 @@ sa_status launch_bf16_split(const PrefillArgs& pa, dim3 grid, hipStream_t st) {
     return SA_OK;
 }
 
-template <int D>
+template <int D, int GQ = 2>
 sa_status launch_f32(const PrefillArgs& pa, dim3 grid, hipStream_t st) {
-    sa_status s = opt_in_lds<&prefill_f32_kernel<D>>(F32Lds<D>::BYTES);
-    if (s == SA_OK) hipLaunchKernelGGL(prefill_f32_kernel<D>, grid, dim3(kFThreads), F32Lds<D>::BYTES, st, pa);
+    sa_status s = opt_in_lds<&prefill_f32_kernel<D, GQ>>(F32Lds<D>::BYTES);
+    if (s == SA_OK)
+        hipLaunchKernelGGL((prefill_f32_kernel<D, GQ>), grid, dim3(kFThreads), F32Lds<D>::BYTES, st, pa);
     return s;
 }
 
@@ -1336,7 +1344,33 @@ long long bf16_grid(const PrefillArgs& pa, int B, int W) {
     return (long long)B * (pa.Hq / gh) * ((pa.L + q_tile - 1) / q_tile);
 }
 
-sa_status launch(PrefillArgs pa, int B, bool bf16, int D, hipStream_t st) {
+// The kernel a prefill launch takes and its query tile.
+enum class PfKind { BfSplit, Bf, F32Split, F32 };
+struct PfPlan {
+    PfKind kind;
+    int W;        // Bf: waves per workgroup (kBfWSmall or kBfW)
+    int gh;       // query heads per workgroup
+    int q_tile;   // query rows per workgroup and head
+};
+
+PfPlan plan_prefill(const PrefillArgs& pa, int B, bool bf16, int D) {
+    const int G = pa.Hq / pa.Hkv;
+    const bool split_shape = bf16 && D == 128 && G % kSplitGH == 0;
+    // A query tile set through sa_set_attention_blocks (the reference's
+    // g_q_block_size): fp32 32 (the split kernel), 64 or 128 (16 or 32
+    // queries per wave); bf16 32 (the split kernel, head_dim 128 and even
+    // GQA groups) or the unsplit workgroup width whose per-head tile it is
+    // (16/8 heads: 64 with 4 waves, 128 with 8).  A bf16 shape with no
+    // kernel of that tile takes the launch's own choice.
+    const int want = attn_q_block();
+    if (want > 0) {
+        if (!bf16) return {want == 32 ? PfKind::F32Split : PfKind::F32, 0, 1, want};
+        if (want == 32 && split_shape) return {PfKind::BfSplit, 0, kSplitGH, 32};
+        for (int W : {kBfWSmall, kBfW}) {
+            const int gh = std::gcd(G, W);
+            if ((W / gh) * kBfQB * 32 == want) return {PfKind::Bf, W, gh, want};
+        }
+    }
     // bf16: 8-wave workgroups while they give every CU two of them; below
     // that, 4-wave workgroups (one wave per SIMD) spread the same waves over
     // twice as many CUs.  Measured (16/8 heads, D = 128): 4 waves are faster
@@ -1352,21 +1386,9 @@ sa_status launch(PrefillArgs pa, int B, bool bf16, int D, hipStream_t st) {
     // with 4-wave workgroups; L = 128 8.3 us either way.
     // SA_PREFILL_SPLIT=1 / 0 forces it on (where the shape allows) / off.
     const char* fsplit = std::getenv("SA_PREFILL_SPLIT");
-    const bool split_shape = bf16 && D == 128 && (pa.Hq / pa.Hkv) % kSplitGH == 0;
     const bool split = split_shape && (fsplit ? std::atoi(fsplit) != 0
                                               : !forced && bf16_grid(pa, B, kBfWSmall) <= device_cu_count());
-    if (split) {
-        pa.gh = kSplitGH;
-        pa.n_qt = (pa.L + 31) / 32;
-        const int groups = B * pa.Hkv;
-        pa.xcd_groups = groups % 8 == 0 ? groups / 8 : 0;
-        const long long n_wg = (long long)B * (pa.Hq / pa.gh) * pa.n_qt;
-        if (n_wg > 0x7fffffffLL) return fail(SA_ERANGE, "prefill grid too large");
-        const sa_status s = launch_bf16_split(pa, dim3(static_cast<unsigned>(n_wg)), st);
-        if (s != SA_OK) return s;
-        SA_CHECK_LAUNCH();
-        return SA_OK;
-    }
+    if (split) return {PfKind::BfSplit, 0, kSplitGH, 32};
     // fp32: 32-query workgroups whose waves split each tile's keys while
     // 128-query ones would give fewer than two workgroups per CU.  Measured
     // (16/8 heads, D = 128, graph-replayed calls): L = 128 / 512 / 1024 /
@@ -1374,57 +1396,74 @@ sa_status launch(PrefillArgs pa, int B, bool bf16, int D, hipStream_t st) {
     // 319.5 us with 128-query workgroups (4 waves per 32-query workgroup
     // instead of 8: 17.3 / 38.3 / 78.4 / 266.6 us); L = 4096 896 against
     // 681 us.
-    if (!bf16 && (fsplit ? std::atoi(fsplit) != 0
-                         : (long long)B * pa.Hq * ((pa.L + kFQTile - 1) / kFQTile) < 2LL * device_cu_count())) {
-        pa.gh = 1;
-        pa.n_qt = (pa.L + 31) / 32;
-        const int groups = B * pa.Hkv;
-        pa.xcd_groups = groups % 8 == 0 ? groups / 8 : 0;
-        const long long n_wg = (long long)B * pa.Hq * pa.n_qt;
-        if (n_wg > 0x7fffffffLL) return fail(SA_ERANGE, "prefill grid too large");
-        const dim3 grid(static_cast<unsigned>(n_wg));
-        sa_status s = SA_OK;
-        switch (D) {
-            case 16: s = launch_f32_split<16>(pa, grid, st); break;
-            case 32: s = launch_f32_split<32>(pa, grid, st); break;
-            case 64: s = launch_f32_split<64>(pa, grid, st); break;
-            default: s = launch_f32_split<128>(pa, grid, st); break;
-        }
-        if (s != SA_OK) return s;
-        SA_CHECK_LAUNCH();
-        return SA_OK;
+    if (!bf16) {
+        const bool fsp = fsplit ? std::atoi(fsplit) != 0
+                                : (long long)B * pa.Hq * ((pa.L + kFQTile - 1) / kFQTile) < 2LL * device_cu_count();
+        return fsp ? PfPlan{PfKind::F32Split, 0, 1, 32} : PfPlan{PfKind::F32, 0, 1, kFQTile};
     }
     const int W = fw == kBfW || fw == kBfWSmall ? fw
-                  : bf16 && bf16_grid(pa, B, kBfW) < 2LL * device_cu_count() ? kBfWSmall : kBfW;
-    pa.gh = bf16 ? std::gcd(pa.Hq / pa.Hkv, W) : 1;
-    const int q_tile = bf16 ? (W / pa.gh) * kBfQB * 32 : kFQTile;
-    pa.n_qt = (pa.L + q_tile - 1) / q_tile;
+                  : bf16_grid(pa, B, kBfW) < 2LL * device_cu_count() ? kBfWSmall : kBfW;
+    const int gh = std::gcd(G, W);
+    return {PfKind::Bf, W, gh, (W / gh) * kBfQB * 32};
+}
+
+sa_status launch(PrefillArgs pa, int B, bool bf16, int D, hipStream_t st) {
+    const PfPlan plan = plan_prefill(pa, B, bf16, D);
+    pa.gh = plan.gh;
+    pa.n_qt = (pa.L + plan.q_tile - 1) / plan.q_tile;
     const int groups = B * pa.Hkv;
     pa.xcd_groups = groups % 8 == 0 ? groups / 8 : 0;
     const long long n_wg = (long long)B * (pa.Hq / pa.gh) * pa.n_qt;
     if (n_wg > 0x7fffffffLL) return fail(SA_ERANGE, "prefill grid too large");
     const dim3 grid(static_cast<unsigned>(n_wg));
-    // head_dim 128 in bf16 uses the load-unit kernel when a workgroup's
-    // queries end within the tiles its schedule keeps resident (two with 8
-    // waves, one with 4), so every wave's diagonal tile is still in LDS after
-    // the loop: GQA groups of 2 or more.  Measured against the register-staged
-    // kernel (16/8 heads): 1.04x at L = 8192, 1.08x .. 1.14x at L = 1024 .. 4096.
-    const bool dma = bf16 && D == 128 &&
-                     q_tile <= (W == kBfW ? 2 : 1) * kKTile;
     sa_status s = SA_OK;
-    if (dma) {
-        s = W == kBfW ? launch_bf16_dma<kBfW>(pa, grid, st) : launch_bf16_dma<kBfWSmall>(pa, grid, st);
-    } else if (bf16 && W == kBfW) {
-        s = D == 64 ? launch_bf16<64, kBfQB, kBfW>(pa, grid, st) : launch_bf16<128, kBfQB, kBfW>(pa, grid, st);
-    } else if (bf16) {
-        s = D == 64 ? launch_bf16<64, kBfQB, kBfWSmall>(pa, grid, st)
-                    : launch_bf16<128, kBfQB, kBfWSmall>(pa, grid, st);
-    } else {
-        switch (D) {
-            case 16: s = launch_f32<16>(pa, grid, st); break;
-            case 32: s = launch_f32<32>(pa, grid, st); break;
-            case 64: s = launch_f32<64>(pa, grid, st); break;
-            default: s = launch_f32<128>(pa, grid, st); break;
+    switch (plan.kind) {
+        case PfKind::BfSplit:
+            s = launch_bf16_split(pa, grid, st);
+            break;
+        case PfKind::F32Split:
+            switch (D) {
+                case 16: s = launch_f32_split<16>(pa, grid, st); break;
+                case 32: s = launch_f32_split<32>(pa, grid, st); break;
+                case 64: s = launch_f32_split<64>(pa, grid, st); break;
+                default: s = launch_f32_split<128>(pa, grid, st); break;
+            }
+            break;
+        case PfKind::F32:
+            if (plan.q_tile == 64) {
+                switch (D) {
+                    case 16: s = launch_f32<16, 1>(pa, grid, st); break;
+                    case 32: s = launch_f32<32, 1>(pa, grid, st); break;
+                    case 64: s = launch_f32<64, 1>(pa, grid, st); break;
+                    default: s = launch_f32<128, 1>(pa, grid, st); break;
+                }
+            } else {
+                switch (D) {
+                    case 16: s = launch_f32<16>(pa, grid, st); break;
+                    case 32: s = launch_f32<32>(pa, grid, st); break;
+                    case 64: s = launch_f32<64>(pa, grid, st); break;
+                    default: s = launch_f32<128>(pa, grid, st); break;
+                }
+            }
+            break;
+        case PfKind::Bf: {
+            // head_dim 128 in bf16 uses the load-unit kernel when a
+            // workgroup's queries end within the tiles its schedule keeps
+            // resident (two with 8 waves, one with 4), so every wave's
+            // diagonal tile is still in LDS after the loop: GQA groups of 2 or
+            // more.  Measured against the register-staged kernel (16/8 heads):
+            // 1.04x at L = 8192, 1.08x .. 1.14x at L = 1024 .. 4096.
+            const int W = plan.W;
+            const bool dma = D == 128 && plan.q_tile <= (W == kBfW ? 2 : 1) * kKTile;
+            if (dma) {
+                s = W == kBfW ? launch_bf16_dma<kBfW>(pa, grid, st) : launch_bf16_dma<kBfWSmall>(pa, grid, st);
+            } else if (W == kBfW) {
+                s = D == 64 ? launch_bf16<64, kBfQB, kBfW>(pa, grid, st) : launch_bf16<128, kBfQB, kBfW>(pa, grid, st);
+            } else {
+                s = D == 64 ? launch_bf16<64, kBfQB, kBfWSmall>(pa, grid, st)
+                            : launch_bf16<128, kBfQB, kBfWSmall>(pa, grid, st);
+            }
+            break;
         }
     }
     if (s != SA_OK) return s;
@@ -1468,6 +1507,18 @@ sa_status prefill(const void* q, const void* k, const void* v, sa_dtype dtype, i
 
 }  // namespace
 }  // namespace sa
+
+extern "C" int sa_prefill_query_tile(sa_dtype dtype, int batch, int n_q_heads, int n_kv_heads, int L, int D) {
+    sa::clear_error();
+    if (dtype != SA_DTYPE_F32 && dtype != SA_DTYPE_BF16) return sa::fail(SA_EINVAL, "dtype must be F32 or BF16");
+    if (batch <= 0 || n_q_heads <= 0 || n_kv_heads <= 0 || n_q_heads % n_kv_heads || L <= 0)
+        return sa::fail(SA_EINVAL, "bad prefill shape");
+    if (dtype == SA_DTYPE_BF16 ? D != 64 && D != 128 : D != 16 && D != 32 && D != 64 && D != 128)
+        return sa::fail(SA_EINVAL, "unsupported head_dim");
+    sa::PrefillArgs pa{};
+    pa.Hq = n_q_heads; pa.Hkv = n_kv_heads; pa.L = L;
+    return sa::plan_prefill(pa, batch, dtype == SA_DTYPE_BF16, D).q_tile;
+}
 
 extern "C" sa_status sa_prefill_causal(const void* q, const void* k, const void* v, sa_dtype dtype,
                                        int batch, int n_q_heads, int n_kv_heads, int L, int D,

@@ -43,6 +43,56 @@ def test_help_and_bad_options():
     assert r.returncode == 1
     r = run("--phase", "prefill")          # neither --model nor --synthetic
     assert r.returncode == 1
+    for opt, bad in (("--q-block-size", "48"), ("--q-block-size", "256"), ("--kv-block-size", "100"),
+                     ("--kv-block-size", "32768")):
+        r = run("--synthetic", opt, bad)
+        assert r.returncode == 1 and "error:" in r.stderr and "block" in r.stderr, (opt, bad, r.stderr)
+
+
+# q_block:kv_block pairs of the reference's block-size sweep
+# (tensor_cpp/scripts/exp6_block_size_tuning.sh:28-34), at its prompt lengths.
+EXP6_BLOCKS = ["32:64", "64:128", "64:64", "128:128", "128:256"]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seq_len", [128, 1024])
+def test_block_size_sweep_prefill(seq_len):
+    """The sweep's prefill runs: every setting prints the result lines and
+    the query tile it asked for."""
+    for cfg in EXP6_BLOCKS:
+        q, kv = cfg.split(":")
+        r = run("--synthetic", "--phase", "prefill", "--prompt-len", str(seq_len), "--q-block-size", q,
+                "--kv-block-size", kv, "--iters", "2", "--warmup", "1")
+        assert r.returncode == 0, (cfg, r.stderr)
+        assert field(r.stdout, "处理token数:") == 2 * seq_len
+        assert field(r.stdout, "吞吐量:") > 0
+        assert re.search(rf"attention tiles: prefill {q} queries per workgroup and head", r.stdout), r.stdout
+        assert f"decode split-KV chunk {kv} tokens" in r.stdout
+
+
+@pytest.mark.gpu
+def test_block_sizes_change_only_rounding(tmp_path):
+    """--verify (a 300-token prefill, and a one-token prefill followed by 299
+    decode steps) under each block setting of the sweep and the automatic
+    one: the last-position logits of both paths agree with the automatic
+    setting's to fp32 rounding (max-abs <= 1e-4 relative to the largest
+    logit, same greedy token), and each run's two paths MATCH."""
+    import numpy as np
+    toks = ",".join(str((7 * i * i + 3 * i + 11) % 151936) for i in range(300))
+    res = {}
+    for cfg in ["0:0"] + EXP6_BLOCKS:
+        q, kv = cfg.split(":")
+        out = tmp_path / f"logits_{q}_{kv}.bin"
+        r = run("--synthetic", "--synthetic-shape", "2,1024,3072,151936,16,8,128", "--q-block-size", q,
+                "--kv-block-size", kv, "--verify", toks, "--logits-out", str(out))
+        assert r.returncode == 0 and "MATCH" in r.stdout, (cfg, r.stdout, r.stderr)
+        res[cfg] = np.fromfile(out, np.float32).reshape(2, 1, -1)
+    base = res["0:0"]
+    scale = float(np.abs(base).max())
+    for cfg, got in res.items():
+        err = float(np.abs(got - base).max())
+        assert err <= 1e-4 * scale, (cfg, err, scale)
+        assert (got.argmax(-1) == base.argmax(-1)).all(), cfg
 
 
 @pytest.mark.gpu

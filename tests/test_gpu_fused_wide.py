@@ -19,8 +19,9 @@ seeded sequences are also held to the fp32 bar (max-abs 1e-4, relative L2
 tensor_cpp/src/ops.cpp:514-641) on the K/V the cache holds.
 
 Lengths span 0 .. 4,095 cached tokens (1 to 16 chunks of the default 256
-tokens; up to 32 forced chunks of 128), on shuffled pages, called in a
-shuffled row order.
+tokens; up to 32 forced chunks of 128 and 64 of 64, where bf16 workgroups
+have waves without a tile), on shuffled pages, called in a shuffled row
+order.
 """
 from __future__ import annotations
 
@@ -112,7 +113,7 @@ def compare(sa, oracle, synth, a, b, lens, order, out_a, qa, out_b, qb, commit, 
         assert err <= 1e-4 and rel <= 1e-5, (s, lens[s], err, rel)
 
 
-@pytest.mark.parametrize("chunk_env", [None, 128], indirect=True)
+@pytest.mark.parametrize("chunk_env", [None, 128, 64], indirect=True)
 @pytest.mark.parametrize("n_seq,commit", [(40, True), (72, True), (72, False)])
 @pytest.mark.parametrize("kv", ["f32", "bf16"])
 def test_fused_wide_grid_equals_three_calls(sa, oracle, synth, chunk_env, n_seq, commit, kv):
@@ -139,7 +140,7 @@ def test_fused_wide_grid_equals_three_calls(sa, oracle, synth, chunk_env, n_seq,
     b.close()
 
 
-@pytest.mark.parametrize("chunk_env", [None, 128], indirect=True)
+@pytest.mark.parametrize("chunk_env", [None, 128, 64], indirect=True)
 @pytest.mark.parametrize("n_seq,n_part", [(40, 8), (72, 3)])
 @pytest.mark.parametrize("kv", ["f32", "bf16"])
 def test_fused_partials_wide_grid_equals_three_calls(sa, oracle, synth, chunk_env, n_seq, n_part, kv):

@@ -72,6 +72,52 @@ def test_prefill_fp32(sa, oracle, synth, monkeypatch, L, kernel):
     assert rel_l2(out, want) <= 1e-5
 
 
+@pytest.fixture
+def blocks(sa):
+    """sa_set_attention_blocks, restored to the automatic choice afterwards."""
+    yield sa.set_attention_blocks
+    sa.set_attention_blocks(0, 0)
+
+
+@pytest.mark.parametrize("q_block", [32, 64, 128])
+@pytest.mark.parametrize("L,Hq,Hkv,D", [(1, 16, 8, 128), (17, 16, 8, 128), (200, 16, 8, 128), (1024, 16, 8, 128),
+                                        (300, 4, 2, 64), (300, 8, 2, 16), (129, 4, 4, 32)])
+def test_prefill_fp32_query_tiles(sa, oracle, synth, blocks, q_block, L, Hq, Hkv, D):
+    """The query tile set through sa_set_attention_blocks (the reference's
+    g_q_block_size): 32 (waves split each key tile), 64 (16 queries per
+    wave) and 128 (32 per wave) rows per workgroup, every row at the fp32
+    bar, and the launch reports the tile it takes."""
+    blocks(q_block, 0)
+    assert sa.get_attention_blocks() == (q_block, 0)
+    assert sa.prefill_query_tile(sa.SA_DTYPE_F32, 1, Hq, Hkv, L, D) == q_block
+    q, k, v = inputs(synth, L, Hq, Hkv, D, seed=58)
+    sc = np.float32(1 / np.sqrt(D))
+    out = host(sa.prefill_causal(dev(q), dev(k), dev(v), float(sc)))
+    want = oracle.prefill_blockwise(q, k, v, sc, 64)
+    assert np.abs(out - want).max() <= 1e-4
+    assert rel_l2(out, want) <= 1e-5
+
+
+@pytest.mark.parametrize("q_block,tile", [(32, 32), (64, 64), (128, 128)])
+def test_prefill_bf16_query_tiles(sa, oracle, synth, blocks, q_block, tile):
+    """bf16 at 16/8 heads: 32 runs the split-key kernel, 64 the 4-wave and 128
+    the 8-wave workgroups; bad values are refused and change nothing."""
+    blocks(q_block, 0)
+    L = 1000
+    assert sa.prefill_query_tile(sa.SA_DTYPE_BF16, 1, 16, 8, L, 128) == tile
+    q, k, v = (synth.bf16_round(x) for x in inputs(synth, L, seed=59))
+    sc = np.float32(1 / np.sqrt(128))
+    t = lambda a: dev(a).to(torch.bfloat16)
+    out = host(sa.prefill_causal(t(q), t(k), t(v), float(sc)))
+    want = oracle.prefill_blockwise(q, k, v, sc, 64)
+    assert rel_l2(out, want) <= 2e-2
+    for bad in ((48, 0), (0, 96), (256, 0), (0, 16448)):
+        with pytest.raises(sa.SaError) as e:
+            sa.set_attention_blocks(*bad)
+        assert e.value.status == sa.SA_EINVAL
+    assert sa.get_attention_blocks() == (q_block, 0)
+
+
 @pytest.mark.parametrize("kernel", ["split", "unsplit"])
 @pytest.mark.parametrize("L", [128, 1024])
 def test_prefill_fp32_roped(sa, oracle, synth, monkeypatch, L, kernel):
