@@ -513,13 +513,19 @@ struct FoldWave {
         return s;
     }
     // P = 2^s as the PV product's B operand, and this lane's sum of it.
+    // This lane's sum of the 16 bf16 P values: two independent chains of
+    // four dot products each (one chain of eight measured 1 % slower at
+    // L = 8192).
+    __device__ __forceinline__ static float psum(const bf16x8_t (&pb)[2]) {
+        return sum_bf16x8(pb[1], 0.f) + sum_bf16x8(pb[0], 0.f);
+    }
     __device__ __forceinline__ static float softmax(const f32x16_t& s, bf16x8_t (&pb)[2]) {
         float p[16];
 #pragma unroll
         for (int j = 0; j < 16; ++j) p[j] = __builtin_amdgcn_exp2f(s[j]);
         pb[0] = pack_bf16x8(p);
         pb[1] = pack_bf16x8(p + 8);
-        return sum_bf16x8(pb[1], sum_bf16x8(pb[0], 0.f));
+        return psum(pb);
     }
     // Raise m to the row max of this half when the sum left the cap (or m is
     // still -inf): O and the row sum are rescaled and P recomputed.
@@ -543,7 +549,7 @@ struct FoldWave {
         for (int j = 0; j < 16; ++j) p[j] = __builtin_amdgcn_exp2f(s[j] + delta);
         pb[0] = pack_bf16x8(p);
         pb[1] = pack_bf16x8(p + 8);
-        rs = sum_bf16x8(pb[1], sum_bf16x8(pb[0], 0.f));
+        rs = psum(pb);
         ms = m_new;
         cap = m_new == -INFINITY ? -1.f : kSumCap;
 #pragma unroll
@@ -693,6 +699,10 @@ prefill_bf16_fold_kernel(PrefillArgs pa) {
         // every wave is done with tile kt.
         static_assert(NS == 2 && NI == 2, "ping-pong schedule: two stages, two loads per tensor tile");
         const bool late = wave >= W / 2;
+        // The early waves' MFMAs go first when both waves of a SIMD have some
+        // ready, so the early wave's softmax starts sooner (L = 8192, same
+        // box: 1 % faster; the late waves first: 2 % slower).
+        if (!late) __builtin_amdgcn_s_setprio(1);
         bf16x8_t pv_v[NDB][2];
         bf16x8_t pv_p[2];
 #pragma unroll

@@ -107,7 +107,18 @@ def test_model_init_matches_generator(sa, synth):
     model.close()
 
 
-def test_model_decode_fp32_kv(sa, oracle, synth):
+@pytest.fixture(params=["auto", "interleaved"])
+def interleave(request, monkeypatch):
+    """The decode step as the launch chooses (one stream at these sizes), or
+    forced to run its two half-batches on two streams."""
+    if request.param == "interleaved":
+        monkeypatch.setenv("SA_DECODE_INTERLEAVE", "1")
+    else:
+        monkeypatch.delenv("SA_DECODE_INTERLEAVE", raising=False)
+    return request.param
+
+
+def test_model_decode_fp32_kv(sa, oracle, synth, interleave):
     """Small model, fp32 KV, three sequences of different lengths (one of a
     single token), 8 greedy steps at the fp32 bar."""
 
@@ -118,7 +129,7 @@ def test_model_decode_fp32_kv(sa, oracle, synth):
     run_parity(sa, oracle, synth, SMALL, 0.1, [70, 130, 1], 8, sa.SA_DTYPE_F32, 31, [5, 17, 900], check)
 
 
-def test_model_decode_qwen3_shape_bf16_kv(sa, oracle, synth):
+def test_model_decode_qwen3_shape_bf16_kv(sa, oracle, synth, interleave):
     """The Qwen3-0.6B shape (28 layers, 16/8 heads, vocab 151936), bf16 KV on
     shuffled pages, 4 sequences with lengths in [512, 2048], 32 greedy steps:
     identical tokens, logits within the bf16-KV tolerance."""
@@ -191,5 +202,43 @@ def test_model_decode_b64_workload_rows(sa, oracle, synth):
         assert res["tokens_identical"], t
         tokens = nxt
     assert [cache.length(s) for s in range(B)] == [L + steps for L in lens]
+    cache.close()
+    model.close()
+
+
+def test_model_decode_interleaved_graph_replay(sa, synth, monkeypatch):
+    """An interleaved decode step (two half-batches on two streams, attention
+    launches ordered by events) captured into a HIP graph: every replay, with
+    eager work between replays, reproduces the eager step's logits and
+    tokens bit for bit."""
+    monkeypatch.setenv("SA_DECODE_INTERLEAVE", "1")
+    lens = [300, 17, 129, 64, 1, 500]
+    model = sa.Qwen3(len(lens), 600, **{k: SMALL[k] for k in SHAPE_KEYS})
+    model.init_random(12, 0.1)
+    cache = make_cache(sa, synth, SMALL, lens, 2, sa.SA_DTYPE_BF16, 12)
+    tokens = torch.tensor([3, 5, 7, 11, 13, 17], dtype=torch.int32, device="cuda")
+    logits = torch.empty(len(lens), SMALL["vocab"], dtype=torch.float32, device="cuda")
+    nxt = torch.empty_like(tokens)
+    model.decode_step(cache, tokens, next_tokens=nxt, logits=logits)   # eager; also sizes the buffers
+    torch.cuda.synchronize()
+    want_l, want_t = logits.clone(), nxt.clone()
+    for s, L in enumerate(lens):
+        cache.set_len(s, L)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        model.decode_step(cache, tokens, next_tokens=nxt, logits=logits)
+    for rep in range(3):
+        logits.fill_(float("nan"))
+        nxt.fill_(-1)
+        (torch.randn(1 << 20, device="cuda") * 2).sum().item()
+        for s, L in enumerate(lens):
+            cache.set_len(s, L)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(logits, want_l), f"replay {rep}"
+        assert torch.equal(nxt, want_t), f"replay {rep}"
+    del graph
     cache.close()
     model.close()
