@@ -1083,6 +1083,277 @@ prefill_f32_kernel(PrefillArgs pa) {
     }
 }
 
+// ===========================================================================
+// fp32 on bf16 MFMA, head_dim 128: exact three-term splits
+// ===========================================================================
+// An fp32 value x is the exact sum of three bf16 terms, t0 = rne(x),
+// t1 = rne(x - t0), t2 = x - t0 - t1 (each difference is exact in fp32 and the
+// last fits bf16 exactly).  A product x y of two fp32 operands is taken as
+// the six products ti uj with i + j <= 2; the three left out are below
+// 2^-24 |x y|, the rounding of an fp32 product.  Every bf16 x bf16 product is
+// exact in fp32 and accumulates in fp32 (v_mfma_f32_16x16x32_bf16), so the
+// scores q.k and the output sum p.v come out at fp32 accuracy, at 6 bf16
+// MFMAs per fp32 product: 16/6 times the fp32 MFMA rate of
+// v_mfma_f32_16x16x4f32.
+//
+// A wave owns 16 queries of one head; a workgroup of W waves serves gh query
+// heads of one KV group, W / gh waves per head.  Key tiles of 32 rows are
+// loaded as fp32 into registers one tile ahead, split into their three terms
+// and stored to LDS (K terms and V terms, 48 KiB per stage, two stages).
+// Scores S^T = K Q^T (two 16-key blocks, K rows permuted so that a lane's
+// scores are the 8 consecutive keys the B operand of the PV product needs),
+// folded softmax as in the bf16 kernels (q pre-scaled by scale log2(e), the
+// score chain starting from -m, the running max raised lazily when a lane's
+// sum of p exceeds kSumCap), P split into three terms, O^T += V^T P^T with
+// the V^T operands read by ds_read_b64_tr_b16.
+constexpr int kX3KTile = 32;                          // keys per tile
+constexpr int kX3Row = 256;                           // bytes per LDS row: 128 bf16
+constexpr int kX3TermBytes = kX3KTile * kX3Row;       // one term of one tensor's tile
+constexpr int kX3StageBytes = 6 * kX3TermBytes;       // K terms 0-2, V terms 0-2
+// Term pairs (of the first and the second operand) of a product.
+constexpr int kX3Pairs = 6;
+__host__ __device__ constexpr int x3_pair_a(int pr) { return pr == 2 || pr == 4 ? 1 : pr == 5 ? 2 : 0; }
+__host__ __device__ constexpr int x3_pair_b(int pr) { return pr == 1 || pr == 4 ? 1 : pr == 3 ? 2 : 0; }
+
+// 16-byte chunk c of tile row r sits at chunk position c ^ x3_swz(r): the
+// rows one K-fragment read touches (8a + 4kb + b, a, b < 4) and the rows one
+// V^T read touches (8G + 4u + b) land on distinct positions.
+__device__ __forceinline__ int x3_swz(int r) { return ((r & 3) << 2) | ((r >> 3) & 3); }
+__device__ __forceinline__ int x3_off(int r, int c16) { return r * kX3Row + ((c16 ^ x3_swz(r)) << 4); }
+
+// x = t0 + t1 + t2 for a pair of fp32 values: three packed bf16 pairs.
+__device__ __forceinline__ void x3_split2(float a, float b, uint32_t& t0, uint32_t& t1, uint32_t& t2) {
+    t0 = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+    a -= bf16_lo(t0);
+    b -= bf16_hi(t0);
+    t1 = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+    a -= bf16_lo(t1);
+    b -= bf16_hi(t1);
+    t2 = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
+
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void x3_st(lds_u8_t* p, uint32_t a, uint32_t b) {
+    *reinterpret_cast<__attribute__((address_space(3))) u32x2_t*>(p) = u32x2_t{a, b};
+}
+
+// Eight fp32 values as three bf16x8 terms.
+__device__ __forceinline__ void x3_split8(const float* x, bf16x8_t (&t)[3]) {
+    uint32_t w[3][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x3_split2(x[2 * i], x[2 * i + 1], w[0][i], w[1][i], w[2][i]);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) t[k] = __builtin_bit_cast(bf16x8_t, u32x4_t{w[k][0], w[k][1], w[k][2], w[k][3]});
+}
+
+template <int W>
+__global__ void __launch_bounds__(W * 64)
+prefill_f32x3_kernel(PrefillArgs pa) {
+    constexpr int NT = W * 64;
+    constexpr int NC = kX3KTile * 32 / NT;   // 16-byte fp32 chunks per thread and tensor of a tile
+    static_assert(NC >= 1 && NC * NT == kX3KTile * 32, "tile chunks per thread");
+    extern __shared__ __align__(16) unsigned char smem[];
+    lds_u8_t* const lsm = (lds_u8_t*)smem;
+
+    const int L = pa.L;
+    const Work wk = map_work(pa, blockIdx.x);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r16 = lane & 15, g = lane >> 4;
+    const int wph = W / pa.gh;
+    const int qtile = wph * 16;
+    const int h = wk.h0 + wave / wph;
+    const float* Q = static_cast<const float*>(pa.q) + wk.b * pa.qs[0] + h * pa.qs[1];
+    const float* K = static_cast<const float*>(pa.k) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
+    const float* V = static_cast<const float*>(pa.v) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
+    const long long kv_row = pa.kvs[2];
+
+    const int q0 = wk.qt * qtile + (wave % wph) * 16;   // this wave's first query
+    const int n_kt = (min(L, (wk.qt + 1) * qtile) - 1) / kX3KTile + 1;
+    const int wave_kt = q0 < L ? min(q0 + 15, L - 1) / kX3KTile + 1 : 0;   // tiles this wave computes
+
+    // ---- tile staging: fp32 rows in registers, three bf16 terms in LDS ----
+    f32x4_t sk[NC], sv[NC];
+    auto load_tile = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            const int idx = threadIdx.x + i * NT;
+            const long long key = min(kt * kX3KTile + (idx >> 5), L - 1);
+            const long long e = key * kv_row + 4 * (idx & 31);
+            sk[i] = *reinterpret_cast<const f32x4_t*>(K + e);
+            sv[i] = *reinterpret_cast<const f32x4_t*>(V + e);
+        }
+    };
+    auto store_tile = [&](int stage) {
+        lds_u8_t* base = lsm + stage * kX3StageBytes;
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            const int idx = threadIdx.x + i * NT;
+            const int r = idx >> 5, c4 = idx & 31;
+            const int off = x3_off(r, c4 >> 1) + (c4 & 1) * 8;
+            uint32_t k0a, k1a, k2a, k0b, k1b, k2b, v0a, v1a, v2a, v0b, v1b, v2b;
+            x3_split2(sk[i][0], sk[i][1], k0a, k1a, k2a);
+            x3_split2(sk[i][2], sk[i][3], k0b, k1b, k2b);
+            x3_split2(sv[i][0], sv[i][1], v0a, v1a, v2a);
+            x3_split2(sv[i][2], sv[i][3], v0b, v1b, v2b);
+            x3_st(base + 0 * kX3TermBytes + off, k0a, k0b);
+            x3_st(base + 1 * kX3TermBytes + off, k1a, k1b);
+            x3_st(base + 2 * kX3TermBytes + off, k2a, k2b);
+            x3_st(base + 3 * kX3TermBytes + off, v0a, v0b);
+            x3_st(base + 4 * kX3TermBytes + off, v1a, v1b);
+            x3_st(base + 5 * kX3TermBytes + off, v2a, v2b);
+        }
+    };
+
+    // ---- this wave's queries: q' = q * scale * log2(e), three terms of the
+    // B operand per 32-wide d step (lane: query q0 + r16, d 32 ks + 8 g ..) ----
+    bf16x8_t qf[4][3];
+    {
+        const float sq = pa.scale * kLog2eP;
+        const float* qrow = Q + (long long)min(q0 + r16, L - 1) * pa.qs[2] + 8 * g;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const f32x4_t a = *reinterpret_cast<const f32x4_t*>(qrow + 32 * ks);
+            const f32x4_t b = *reinterpret_cast<const f32x4_t*>(qrow + 32 * ks + 4);
+            const float x[8] = {a[0] * sq, a[1] * sq, a[2] * sq, a[3] * sq, b[0] * sq, b[1] * sq, b[2] * sq, b[3] * sq};
+            x3_split8(x, qf[ks]);
+        }
+    }
+    // K fragment rows: block kb's row r16 is tile key 8 (r16 / 4) + 4 kb + r16 % 4,
+    // so score element e of block kb is key 8 g + 4 kb + e of the lane's query.
+    int k_off[2][4];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+        const int r = 8 * (r16 >> 2) + 4 * kb + (r16 & 3);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) k_off[kb][ks] = x3_off(r, 4 * ks + g);
+    }
+    // V^T reads (ds_read_b64_tr_b16, read u of d block db): source lane s of
+    // the lane's 16-group reads row 8 g + 4 u + s / 4, columns 16 db + 4 (s % 4) ..;
+    // output lane r16 then holds V[8 g + 4 u + e][16 db + r16], e < 4.
+    int v_off[2][8];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int r = 8 * g + 4 * u + (r16 >> 2);
+#pragma unroll
+        for (int db = 0; db < 8; ++db) {
+            const int col = 16 * db + 4 * (r16 & 3);
+            v_off[u][db] = 3 * kX3TermBytes + x3_off(r, col >> 3) + (col & 7) * 2;
+        }
+    }
+
+    f32x4_t acc[8];
+#pragma unroll
+    for (int db = 0; db < 8; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float ms = -INFINITY;      // running max of the lane's query (log2 domain) at the last raise
+    float b = 0.f;             // -ms once finite: the score chain's start
+    float lp = 0.f;            // the lane's part of the row sum
+    float cap = -1.f;          // kSumCap once ms is finite: the first tile always raises
+
+    auto compute = [&](int kt, const lds_u8_t* sb) {
+        // ---- scores, two independent chains ----
+        f32x4_t s[2] = {f32x4_t{b, b, b, b}, f32x4_t{b, b, b, b}};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            bf16x8_t kf[2][3];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int t = 0; t < 3; ++t)
+                    kf[kb][t] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(
+                        sb + t * kX3TermBytes + k_off[kb][ks]);
+#pragma unroll
+            for (int pr = 0; pr < kX3Pairs; ++pr)
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+                    s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kb][x3_pair_a(pr)], qf[ks][x3_pair_b(pr)],
+                                                                    s[kb], 0, 0, 0);
+        }
+        if (kt * kX3KTile + kX3KTile - 1 > q0) {   // the diagonal: keys past the query
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (kt * kX3KTile + 8 * g + 4 * kb + e > q0 + r16) s[kb][e] = -INFINITY;
+        }
+        // ---- P = 2^s, its sum; raise the max when the sum left the cap ----
+        float p[8];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) p[4 * kb + e] = __builtin_amdgcn_exp2f(s[kb][e]);
+        float rs = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+        if (__any(!(rs <= cap))) {
+            float mt = s[0][0];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) mt = fmaxf(mt, s[kb][e]);
+            mt = xmax16_32(mt);                       // the row: lanes r16, r16 + 16, + 32, + 48
+            const float mq = mt - b;                  // unbiased row max of this tile
+            const float m_new = fmaxf(ms, mq);
+            const float alpha = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - m_new);
+#pragma unroll
+            for (int db = 0; db < 8; ++db) acc[db] *= alpha;
+            lp *= alpha;
+            const float b_new = m_new == -INFINITY ? 0.f : -m_new;
+            const float delta = b_new - b;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) p[4 * kb + e] = __builtin_amdgcn_exp2f(s[kb][e] + delta);
+            rs = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+            ms = m_new;
+            b = b_new;
+            cap = m_new == -INFINITY ? -1.f : kSumCap;
+        }
+        lp += rs;
+        bf16x8_t pt[3];
+        x3_split8(p, pt);
+        // ---- O^T += V^T P^T, 8 blocks of 16 d ----
+#pragma unroll
+        for (int db = 0; db < 8; ++db) {
+            bf16x8_t vf[3];
+#pragma unroll
+            for (int t = 0; t < 3; ++t) {
+                const lds_u8_t* p0 = sb + t * kX3TermBytes + v_off[0][db];
+                const lds_u8_t* p1 = sb + t * kX3TermBytes + v_off[1][db];
+                const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p0);
+                const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p1);
+                vf[t] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+            }
+#pragma unroll
+            for (int pr = 0; pr < kX3Pairs; ++pr)
+                acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[x3_pair_a(pr)], pt[x3_pair_b(pr)], acc[db], 0, 0, 0);
+        }
+    };
+
+    load_tile(0);
+    store_tile(0);
+    if (n_kt > 1) load_tile(1);
+    __syncthreads();
+    for (int kt = 0; kt < n_kt; ++kt) {
+        if (kt < wave_kt) compute(kt, lsm + (kt & 1) * kX3StageBytes);
+        if (kt + 1 < n_kt) {
+            store_tile((kt + 1) & 1);
+            if (kt + 2 < n_kt) load_tile(kt + 2);
+        }
+        __syncthreads();
+    }
+
+    // ---- O / l for query q0 + r16: lane holds O[q][16 db + 4 g + e] ----
+    const float l = xsum16_32(lp);
+    const int qi = q0 + r16;
+    if (qi < L) {
+        const float inv = 1.0f / l;
+        float* orow = pa.out + wk.b * pa.os[0] + h * pa.os[1] + (long long)qi * pa.os[2] + 4 * g;
+#pragma unroll
+        for (int db = 0; db < 8; ++db)
+            *reinterpret_cast<float4*>(orow + 16 * db) =
+                make_float4(acc[db][0] * inv, acc[db][1] * inv, acc[db][2] * inv, acc[db][3] * inv);
+    }
+}
+
 // fp32, short prompts: a workgroup serves 32 queries of one head, and its
 // waves split every staged 64-key tile, each taking one 16-key block of it
 // (with 128-query workgroups a 512-token prompt of 16 heads fills 64 CUs,
@@ -1354,8 +1625,24 @@ long long bf16_grid(const PrefillArgs& pa, int B, int W) {
     return (long long)B * (pa.Hq / gh) * ((pa.L + q_tile - 1) / q_tile);
 }
 
+template <int W>
+sa_status launch_f32x3(const PrefillArgs& pa, dim3 grid, hipStream_t st) {
+    constexpr int bytes = 2 * kX3StageBytes;
+    sa_status s = opt_in_lds<&prefill_f32x3_kernel<W>>(bytes);
+    if (s == SA_OK) hipLaunchKernelGGL(prefill_f32x3_kernel<W>, grid, dim3(W * 64), bytes, st, pa);
+    return s;
+}
+
+// Workgroups of the three-term fp32 kernel: W waves of 16 queries serve
+// gcd(Hq / Hkv, W) query heads.
+long long x3_grid(const PrefillArgs& pa, int B, int W) {
+    const int gh = std::gcd(pa.Hq / pa.Hkv, W);
+    const int q_tile = (W / gh) * 16;
+    return (long long)B * (pa.Hq / gh) * ((pa.L + q_tile - 1) / q_tile);
+}
+
 // The kernel a prefill launch takes and its query tile.
-enum class PfKind { BfSplit, Bf, F32Split, F32 };
+enum class PfKind { BfSplit, Bf, F32Split, F32, F32x3 };
 struct PfPlan {
     PfKind kind;
     int W;        // Bf: waves per workgroup (kBfWSmall or kBfW)
@@ -1406,6 +1693,15 @@ PfPlan plan_prefill(const PrefillArgs& pa, int B, bool bf16, int D) {
     // 319.5 us with 128-query workgroups (4 waves per 32-query workgroup
     // instead of 8: 17.3 / 38.3 / 78.4 / 266.6 us); L = 4096 896 against
     // 681 us.
+    // fp32 at head_dim 128: the three-term kernel on bf16 MFMA, 8 waves
+    // while that grid fills the CUs, else 4.  SA_PREFILL_F32X3=0 (or a
+    // SA_PREFILL_SPLIT setting) selects the fp32-MFMA kernels below.
+    const char* fx3 = std::getenv("SA_PREFILL_F32X3");
+    if (!bf16 && D == 128 && !fsplit && (!fx3 || std::atoi(fx3) != 0)) {
+        const int W = x3_grid(pa, B, 8) >= device_cu_count() ? 8 : 4;
+        const int gh = std::gcd(G, W);
+        return {PfKind::F32x3, W, gh, (W / gh) * 16};
+    }
     if (!bf16) {
         const bool fsp = fsplit ? std::atoi(fsplit) != 0
                                 : (long long)B * pa.Hq * ((pa.L + kFQTile - 1) / kFQTile) < 2LL * device_cu_count();
@@ -1430,6 +1726,9 @@ sa_status launch(PrefillArgs pa, int B, bool bf16, int D, hipStream_t st) {
     switch (plan.kind) {
         case PfKind::BfSplit:
             s = launch_bf16_split(pa, grid, st);
+            break;
+        case PfKind::F32x3:
+            s = plan.W == 8 ? launch_f32x3<8>(pa, grid, st) : launch_f32x3<4>(pa, grid, st);
             break;
         case PfKind::F32Split:
             switch (D) {

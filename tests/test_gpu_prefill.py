@@ -36,7 +36,7 @@ def inputs(synth, L, Hq=16, Hkv=8, D=128, seed=50):
             synth.normal(seed, 3, (1, Hkv, L, D)))
 
 
-@pytest.mark.parametrize("kernel", ["split", "unsplit"])
+@pytest.mark.parametrize("kernel", ["default", "split", "unsplit"])
 def test_prefill_golden(sa, monkeypatch, kernel):
     f32_variant(monkeypatch, kernel)
     meta, g = gi.load("prefill")
@@ -49,11 +49,13 @@ def test_prefill_golden(sa, monkeypatch, kernel):
 
 
 def f32_variant(monkeypatch, v):
-    """The fp32 kernel a launch takes: "split" the one whose 32-query
-    workgroups split each key tile over their four waves, "unsplit" the
-    128-query one, "default" the launch's own choice (split while 128-query
+    """The fp32 kernel a launch takes: "split" the fp32-MFMA kernel whose
+    32-query workgroups split each key tile over their waves, "unsplit" the
+    128-query fp32-MFMA one, "default" the launch's own choice (head_dim 128:
+    the three-term kernel on bf16 MFMA; other sizes split while 128-query
     workgroups would give fewer than two per CU)."""
     monkeypatch.delenv("SA_PREFILL_WAVES", raising=False)
+    monkeypatch.delenv("SA_PREFILL_F32X3", raising=False)
     if v == "default":
         monkeypatch.delenv("SA_PREFILL_SPLIT", raising=False)
     else:
@@ -118,7 +120,7 @@ def test_prefill_bf16_query_tiles(sa, oracle, synth, blocks, q_block, tile):
     assert sa.get_attention_blocks() == (q_block, 0)
 
 
-@pytest.mark.parametrize("kernel", ["split", "unsplit"])
+@pytest.mark.parametrize("kernel", ["default", "split", "unsplit"])
 @pytest.mark.parametrize("L", [128, 1024])
 def test_prefill_fp32_roped(sa, oracle, synth, monkeypatch, L, kernel):
     """The prompt-length workload as specified: N(0,1) q and k rotated by RoPE
@@ -142,6 +144,29 @@ def test_prefill_fp32_8192_roped_rows(sa, oracle, synth):
     rows = np.array([0, 63, 64, 2047, 5000, 8191])
     want = oracle.prefill_blockwise(q, k, v, sc, 64, rows=rows)[:, :, rows]
     got = out[:, :, rows]
+    assert np.abs(got - want).max() <= 1e-4
+    assert rel_l2(got, want) <= 1e-5
+
+
+@pytest.mark.parametrize("L,Hq,Hkv", [(8192, 16, 8), (2048, 16, 8), (3001, 8, 8), (1500, 32, 8), (77, 16, 8)])
+def test_prefill_fp32_three_term_every_row_of_a_group(sa, oracle, synth, monkeypatch, L, Hq, Hkv):
+    """The fp32 kernel on bf16 MFMA (exact three-term splits of q, k, v and p):
+    every row of the query heads of KV group 1 at the fp32 bar (max-abs
+    1e-4, relative L2 1e-5) against the oracle on the same inputs, RoPE'd q
+    and k, at 8- and 4-wave workgroups (the larger prompts and the smaller),
+    GQA groups of 1, 2 and 4, and a prompt off the tile sizes."""
+    f32_variant(monkeypatch, "default")
+    q, k, v = inputs(synth, L, Hq, Hkv, seed=60 + L % 97)
+    q, k = roped(oracle, q), roped(oracle, k)
+    sc = np.float32(1 / np.sqrt(128))
+    assert sa.prefill_query_tile(sa.SA_DTYPE_F32, 1, Hq, Hkv, L, 128) in (16, 32, 64, 128)
+    out = host(sa.prefill_causal(dev(q), dev(k), dev(v), float(sc)))
+    G = Hq // Hkv
+    heads = slice(G, 2 * G)
+    got = out[:, heads]
+    want = oracle.prefill_blockwise(q[:, heads], k[:, 1:2], v[:, 1:2], sc, 64)
+    row = np.linalg.norm((got - want).astype(np.float64), axis=-1) / np.linalg.norm(want.astype(np.float64), axis=-1)
+    print(f"L={L} {Hq}/{Hkv}: max-abs {np.abs(got - want).max():.2e}, worst row rel-L2 {row.max():.2e}")
     assert np.abs(got - want).max() <= 1e-4
     assert rel_l2(got, want) <= 1e-5
 
@@ -219,7 +244,7 @@ def test_prefill_bf16_8192_every_row_of_a_group(sa, oracle, synth, rope):
     assert row.max() <= 2e-2, (h, r, float(row.max()))
 
 
-@pytest.mark.parametrize("kernel", ["split", "unsplit"])
+@pytest.mark.parametrize("kernel", ["default", "split", "unsplit"])
 @pytest.mark.parametrize("Hq,Hkv,D", [(4, 4, 128), (8, 2, 128), (16, 8, 64), (2, 1, 64), (4, 2, 32), (8, 2, 16),
                                      (4, 4, 16)])
 def test_prefill_shapes(sa, oracle, synth, monkeypatch, Hq, Hkv, D, kernel):
@@ -236,7 +261,7 @@ def test_prefill_shapes(sa, oracle, synth, monkeypatch, Hq, Hkv, D, kernel):
     assert rel_l2(out, want) <= 1e-5
 
 
-@pytest.mark.parametrize("kernel", ["split", "unsplit"])
+@pytest.mark.parametrize("kernel", ["default", "split", "unsplit"])
 def test_prefill_last_row_is_decode(sa, synth, monkeypatch, kernel):
     """Row L-1 of the prefill equals a decode step over all L keys."""
     f32_variant(monkeypatch, kernel)

@@ -140,3 +140,42 @@ def test_argument_errors(sa):
     with pytest.raises(sa.SaError) as e:
         sa.stream_attn(dev(Q), dev(K), dev(V), 64, ws=torch.empty(16, dtype=torch.uint8, device="cuda"))
     assert e.value.status == sa.SA_ENOMEM
+
+
+
+@pytest.mark.parametrize("T,chunk", [(65536, None), (262144, None), (8192, 64), (20000, 256)])
+def test_repeated_calls_bit_exact(sa, synth, monkeypatch, T, chunk):
+    """300 back-to-back calls on one workspace give the first call's output
+    bit for bit (chunking and merge order are fixed) and match the oracle."""
+    from oracle import Oracle
+    if chunk:
+        monkeypatch.setenv("SA_DECODE_CHUNK", str(chunk))
+    else:
+        monkeypatch.delenv("SA_DECODE_CHUNK", raising=False)
+    Q, K, V = synth.stream_inputs(T, 128, seed=8, scale=0.5, outlier_frac=0.01)
+    dQ, dK, dV = dev(Q), dev(K), dev(V)
+    ws = torch.zeros(max(sa.lib().sa_stream_attn_ws_bytes(T, 128), 1), dtype=torch.uint8, device="cuda")
+    outs = torch.empty(300, 128, device="cuda")
+    for i in range(300):
+        sa.stream_attn(dQ, dK, dV, 128, 1.0, out=outs[i], ws=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(outs, outs[:1].expand_as(outs)), int((outs != outs[0]).any(dim=1).sum())
+    assert_f32_parity(host(outs[0]), Oracle().streaming_serial(Q, K, V, 128))
+
+
+def test_dense_gqa_batch_repeats(sa, oracle, synth):
+    """Dense GQA decode with several sequences and groups (4 x 8 KV heads, 2
+    query heads each, T = 9000: more workgroups than CUs), repeated on one
+    workspace: outputs equal and at the fp32 bar of the oracle."""
+    B, Hq, Hkv, T, D = 4, 16, 8, 9000, 128
+    q = synth.normal(9, 1, (B, Hq, D))
+    k = synth.normal(9, 2, (B, Hkv, T, D))
+    v = synth.normal(9, 3, (B, Hkv, T, D))
+    dq, dk, dv = dev(q), dev(k), dev(v)
+    ws = torch.zeros(sa.lib().sa_decode_dense_ws_bytes(B, Hq, T, D), dtype=torch.uint8, device="cuda")
+    a = sa.decode_dense(dq, dk, dv, float(SCALE128), ws=ws)
+    for _ in range(50):
+        b = sa.decode_dense(dq, dk, dv, float(SCALE128), ws=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    assert_f32_parity(host(a), oracle.decode_gqa(q, k, v, SCALE128))
