@@ -604,7 +604,11 @@ def bench_prefill(torch, sa, synth, L: int, bf16: bool, steps: int = 5):
     sc = float(1 / np.sqrt(D))
     # The clocks settle only after about a second of MFMA load; the untimed
     # warmup runs that long so the timed launches see steady-state clocks.
-    call = lambda i: sa.prefill_causal(q, k, v, sc, out=out)
+    # fp32 short prompts pair their query tiles through a workspace
+    # (sa_prefill_causal_ws); other shapes ask for none.
+    ws_n = sa.prefill_ws_bytes(sa.SA_DTYPE_BF16 if bf16 else sa.SA_DTYPE_F32, 1, HQ, HKV, L, D)
+    ws = torch.empty(ws_n, dtype=torch.uint8, device="cuda") if ws_n else None
+    call = lambda i: sa.prefill_causal(q, k, v, sc, out=out, ws=ws)
     t_end = time.perf_counter() + 1.0
     while time.perf_counter() < t_end:
         for i in range(10):
@@ -616,7 +620,7 @@ def bench_prefill(torch, sa, synth, L: int, bf16: bool, steps: int = 5):
     tf = flops / (ms * 1e-3) / 1e12
     peak = BF16_PEAK_TFLOPS if bf16 else FP32_PEAK_TFLOPS
     res = {"L": L, "dtype": "bf16" if bf16 else "f32", "ms": round(ms, 4), "tflops": round(tf, 2),
-           "mfma_frac": round(tf / peak, 4)}
+           "mfma_frac": round(tf / peak, 4), "paired_workspace_bytes": ws_n}
     if L <= 1024:
         # A short prompt's kernel runs for less time than the ctypes call that
         # launches it takes on the host; 32 calls replayed from a HIP graph give

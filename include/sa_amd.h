@@ -308,6 +308,25 @@ sa_status sa_prefill_causal_strided(const void* q, const void* k, const void* v,
                                     const int64_t out_strides[3], float scale, float* out,
                                     sa_stream_t stream);
 
+/* The same two calls with a caller workspace.  fp32 at head_dim 128 on a grid
+ * of one round of workgroups (short prompts: 16/8 heads up to L = 2048)
+ * pairs the longest query tiles with the shortest and splits the pair's key
+ * tiles evenly between two workgroups, whose partials a second launch merges;
+ * every other shape ignores the workspace.  ws_bytes at least
+ * sa_prefill_causal_ws_bytes of the shape (0 where the shape takes no
+ * partials), else SA_ENOMEM; ws = NULL takes the single launch.  Results
+ * agree with the single launch to fp32 rounding.  Calls that overlap on one
+ * workspace race. */
+size_t sa_prefill_causal_ws_bytes(sa_dtype dtype, int batch, int n_q_heads, int n_kv_heads, int L, int D);
+sa_status sa_prefill_causal_ws(const void* q, const void* k, const void* v, sa_dtype dtype,
+                               int batch, int n_q_heads, int n_kv_heads, int L, int D,
+                               float scale, float* out, void* ws, size_t ws_bytes, sa_stream_t stream);
+sa_status sa_prefill_causal_strided_ws(const void* q, const void* k, const void* v, sa_dtype dtype,
+                                       int batch, int n_q_heads, int n_kv_heads, int L, int D,
+                                       const int64_t q_strides[3], const int64_t kv_strides[3],
+                                       const int64_t out_strides[3], float scale, float* out,
+                                       void* ws, size_t ws_bytes, sa_stream_t stream);
+
 /* ------------------------------------------------------------------------
  * Tile sizes of the attention kernels, for the whole process: the
  * counterpart of the reference's tensor_cpp::g_q_block_size and

@@ -100,6 +100,10 @@ SIGNATURES = {
                               _I, _P]),
     "sa_prefill_causal": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _P]),
     "sa_prefill_causal_strided": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _F, _P, _P]),
+    "sa_prefill_causal_ws_bytes": (_SZ, [_I, _I, _I, _I, _I, _I]),
+    "sa_prefill_causal_ws": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _P, _SZ, _P]),
+    "sa_prefill_causal_strided_ws": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _F, _P, _P, _SZ,
+                                          _P]),
     "sa_set_attention_blocks": (_I, [_I, _I]),
     "sa_get_attention_blocks": (_I, [C.POINTER(_I), C.POINTER(_I)]),
     "sa_prefill_query_tile": (_I, [_I, _I, _I, _I, _I, _I]),
@@ -448,8 +452,15 @@ def prefill_query_tile(dtype: int, batch: int, n_q_heads: int, n_kv_heads: int, 
     return r
 
 
-def prefill_causal(q, k, v, scale: float, out=None, stream=None):
-    """q [B, Hq, L, D], k/v [B, Hkv, L, D] (fp32 or bf16) -> out fp32 [B, Hq, L, D]."""
+def prefill_ws_bytes(dtype: int, batch: int, n_q_heads: int, n_kv_heads: int, L: int, D: int) -> int:
+    """Workspace bytes of a prefill launch of this shape (0: it takes none)."""
+    return int(lib().sa_prefill_causal_ws_bytes(dtype, batch, n_q_heads, n_kv_heads, L, D))
+
+
+def prefill_causal(q, k, v, scale: float, out=None, stream=None, ws=None):
+    """q [B, Hq, L, D], k/v [B, Hkv, L, D] (fp32 or bf16) -> out fp32 [B, Hq, L, D].
+    ws: a CUDA tensor of at least prefill_ws_bytes bytes (sa_prefill_causal_ws),
+    or None (sa_prefill_causal)."""
     import torch
     if q.dtype == torch.float32:
         dt = SA_DTYPE_F32
@@ -463,8 +474,12 @@ def prefill_causal(q, k, v, scale: float, out=None, stream=None):
     B, Hq, L, D = q.shape
     Hkv = k.shape[1]
     out = torch.empty(B, Hq, L, D, dtype=torch.float32, device=q.device) if out is None else out
-    check(lib().sa_prefill_causal(_ptr(q), _ptr(k), _ptr(v), dt, B, Hq, Hkv, L, D, scale, _ptr(out),
-                                  _stream(stream)))
+    if ws is None:
+        check(lib().sa_prefill_causal(_ptr(q), _ptr(k), _ptr(v), dt, B, Hq, Hkv, L, D, scale, _ptr(out),
+                                      _stream(stream)))
+    else:
+        check(lib().sa_prefill_causal_ws(_ptr(q), _ptr(k), _ptr(v), dt, B, Hq, Hkv, L, D, scale, _ptr(out),
+                                         _ptr(ws), ws.numel() * ws.element_size(), _stream(stream)))
     return out
 
 

@@ -91,9 +91,12 @@ Tensor causal_prefill(const Tensor& q, const Tensor& k, const Tensor& v, const D
             to_device(dv + bh * rows, v.data() + bh * d.Sk * d.D, rows * sizeof(float));
         }
     }
-    check(sa_prefill_causal(dq, dk, dv, SA_DTYPE_F32, (int)d.B, (int)d.Hq, (int)d.Hkv, (int)d.Sq, (int)d.D,
-                            scale, dout, nullptr),
-          "sa_prefill_causal");
+    const size_t ws_bytes = sa_prefill_causal_ws_bytes(SA_DTYPE_F32, (int)d.B, (int)d.Hq, (int)d.Hkv, (int)d.Sq,
+                                                       (int)d.D);
+    void* ws = ws_bytes ? st.ws.ensure(ws_bytes) : nullptr;
+    check(sa_prefill_causal_ws(dq, dk, dv, SA_DTYPE_F32, (int)d.B, (int)d.Hq, (int)d.Hkv, (int)d.Sq, (int)d.D,
+                               scale, dout, ws, ws_bytes, nullptr),
+          "sa_prefill_causal_ws");
     std::vector<float> out(nq);
     to_host(out.data(), dout, nq * sizeof(float));
     return Tensor(std::move(out), q.shape());

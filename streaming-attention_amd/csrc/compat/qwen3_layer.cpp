@@ -236,8 +236,10 @@ void attention_dev(const Geometry& g, const Variant& var, const float* q_norm, c
         const int64_t kvs[3] = {(int64_t)(g.S * g.kd()), (int64_t)g.D, (int64_t)g.kd()};
         const int64_t os_tok[3] = {(int64_t)(g.S * g.qd()), (int64_t)g.D, (int64_t)g.qd()};
         const int64_t os_head[3] = {(int64_t)(g.S * g.qd()), (int64_t)(g.S * g.D), (int64_t)g.D};
-        check(sa_prefill_causal_strided(q, k, v, SA_DTYPE_F32, B, Hq, Hkv, S, D, qs, kvs,
-                                        head_major ? os_head : os_tok, scale, attn, nullptr),
+        const size_t ws_bytes = sa_prefill_causal_ws_bytes(SA_DTYPE_F32, B, Hq, Hkv, S, D);
+        void* ws = ws_bytes ? b.ws.ensure(ws_bytes) : nullptr;
+        check(sa_prefill_causal_strided_ws(q, k, v, SA_DTYPE_F32, B, Hq, Hkv, S, D, qs, kvs,
+                                           head_major ? os_head : os_tok, scale, attn, ws, ws_bytes, nullptr),
               "causal prefill");
     } else {
         const size_t ws_bytes = sa_paged_decode_ws_bytes(cache->handle(), B, Hq);

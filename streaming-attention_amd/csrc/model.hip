@@ -742,7 +742,11 @@ extern "C" sa_status sa_qwen3_prefill(sa_qwen3* m, sa_kvcache* cache, const int3
     // activations of the M token rows, carved from one grow-only buffer
     const size_t f_x = M * s.H, f_q = M * s.Nq, f_k = M * s.Nk, f_act = M * s.I;
     const size_t f_part = M * part_cols;
-    const size_t floats = 2 * f_x + 2 * f_q + 2 * f_k + f_act + f_part + (size_t)batch * s.H;
+    // the attention's workspace (paired key ranges of short prompts) after
+    // the activations, at a 256-byte boundary
+    const size_t ws_attn = sa_prefill_causal_ws_bytes(SA_DTYPE_F32, batch, s.Hq, s.Hkv, L, s.D);
+    const size_t f_act_all = (2 * f_x + 2 * f_q + 2 * f_k + f_act + f_part + (size_t)batch * s.H + 63) / 64 * 64;
+    const size_t floats = f_act_all + (ws_attn + 255) / 256 * 64;
     const size_t need = floats * sizeof(float);
     if (need > m->pf_bytes) {
         if (m->pf) SA_HIP_TRY(hipFree(m->pf));
@@ -760,6 +764,7 @@ extern "C" sa_status sa_qwen3_prefill(sa_qwen3* m, sa_kvcache* cache, const int3
     float* act = v + f_k;
     float* part = act + f_act;
     float* h_last = part + f_part;
+    float* attn_ws = ws_attn ? static_cast<float*>(m->pf) + f_act_all : nullptr;
     const float eps = d.rms_eps;
     const float scale = 1.0f / sqrtf((float)d.head_dim);
     float* out_logits = logits ? logits : m->logits;
@@ -779,8 +784,8 @@ extern "C" sa_status sa_qwen3_prefill(sa_qwen3* m, sa_kvcache* cache, const int3
         // appended to the cache, q, k, v written for the attention: one launch.
         SA_TRY(qknorm_rope_append_partials(cache, l, part, g_qkv.S, batch, L, s.Hq, Ly.q_norm, Ly.k_norm, eps,
                                            m->rope_cos, m->rope_sin, d.max_pos, q, k, v, st));
-        SA_TRY(sa_prefill_causal_strided(q, k, v, SA_DTYPE_F32, batch, s.Hq, s.Hkv, L, s.D, q_str, kv_str, q_str,
-                                         scale, attn, stream));
+        SA_TRY(sa_prefill_causal_strided_ws(q, k, v, SA_DTYPE_F32, batch, s.Hq, s.Hkv, L, s.D, q_str, kv_str, q_str,
+                                            scale, attn, attn_ws, ws_attn, stream));
         SA_TRY(gemm(attn, (int)M, Ly.o, g_o, part, st));
         hipLaunchKernelGGL(residual_norm_kernel, dim3((unsigned)M), dim3(256), 0, st, part, g_o.S, (int)M, s.H, x,
                            Ly.post_norm, eps, h);

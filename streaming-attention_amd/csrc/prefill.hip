@@ -1146,7 +1146,22 @@ __device__ __forceinline__ void x3_split8(const float* x, bf16x8_t (&t)[3]) {
     for (int k = 0; k < 3; ++k) t[k] = __builtin_bit_cast(bf16x8_t, u32x4_t{w[k][0], w[k][1], w[k][2], w[k][3]});
 }
 
-template <int W>
+// Key tiles of query tile t (tiles of qtile rows) under the causal mask.
+__host__ __device__ constexpr int x3_key_tiles(int L, int qtile, int t) {
+    return ((L < (t + 1) * qtile ? L : (t + 1) * qtile) - 1) / kX3KTile + 1;
+}
+
+// Paired launches (short prompts, one round of workgroups): query tile t and
+// tile u = n_qt - 1 - t form a pair whose key tiles add up to about the same
+// count for every t.  Workgroup A computes tile t whole and the first s key
+// tiles of u; workgroup B the rest of u's; so every workgroup walks about
+// half the longest tile's keys instead of up to all of them.  u's two
+// partials meet in prefill_x3_merge_kernel.  s = 0: no split, B writes u.
+__host__ __device__ constexpr int x3_pair_split(int L, int qtile, int t, int u) {
+    return (x3_key_tiles(L, qtile, u) - x3_key_tiles(L, qtile, t)) / 2;
+}
+
+template <int W, bool PAIRED>
 __global__ void __launch_bounds__(W * 64)
 prefill_f32x3_kernel(PrefillArgs pa) {
     constexpr int NT = W * 64;
@@ -1168,9 +1183,37 @@ prefill_f32x3_kernel(PrefillArgs pa) {
     const float* V = static_cast<const float*>(pa.v) + wk.b * pa.kvs[0] + wk.kvh * pa.kvs[1];
     const long long kv_row = pa.kvs[2];
 
-    const int q0 = wk.qt * qtile + (wave % wph) * 16;   // this wave's first query
-    const int n_kt = (min(L, (wk.qt + 1) * qtile) - 1) / kX3KTile + 1;
-    const int wave_kt = q0 < L ? min(q0 + 15, L - 1) / kX3KTile + 1 : 0;   // tiles this wave computes
+    // ---- segments: (query tile, key tiles [k0, k1), output) ----
+    // part < 0: the output rows; else partial slot part of the pair.
+    int seg_qt[2] = {wk.qt, 0}, seg_k0[2] = {0, 0}, seg_k1[2] = {x3_key_tiles(L, qtile, wk.qt), 0};
+    int seg_part[2] = {-1, -1};
+    int n_seg = 1;
+    if constexpr (PAIRED) {
+        const int slot = pa.n_qt - 1 - wk.qt;     // slot 0 is dispatched first
+        const int np = pa.n_qt / 2;
+        if (slot >= 2 * np) {                     // the middle tile of an odd count
+            seg_qt[0] = np;
+            seg_k1[0] = x3_key_tiles(L, qtile, np);
+        } else {
+            const int t = slot >> 1, u = pa.n_qt - 1 - t;
+            const int s = x3_pair_split(L, qtile, t, u);
+            if (slot & 1) {                       // A: tile t whole, then u's first s key tiles
+                seg_qt[0] = t;
+                seg_k1[0] = x3_key_tiles(L, qtile, t);
+                if (s > 0) {
+                    seg_qt[1] = u;
+                    seg_k1[1] = s;
+                    seg_part[1] = 0;
+                    n_seg = 2;
+                }
+            } else {                              // B: the rest of u's key tiles
+                seg_qt[0] = u;
+                seg_k0[0] = s;
+                seg_k1[0] = x3_key_tiles(L, qtile, u);
+                seg_part[0] = s > 0 ? 1 : -1;
+            }
+        }
+    }
 
     // ---- tile staging: fp32 rows in registers, three bf16 terms in LDS ----
     f32x4_t sk[NC], sv[NC];
@@ -1205,20 +1248,6 @@ prefill_f32x3_kernel(PrefillArgs pa) {
         }
     };
 
-    // ---- this wave's queries: q' = q * scale * log2(e), three terms of the
-    // B operand per 32-wide d step (lane: query q0 + r16, d 32 ks + 8 g ..) ----
-    bf16x8_t qf[4][3];
-    {
-        const float sq = pa.scale * kLog2eP;
-        const float* qrow = Q + (long long)min(q0 + r16, L - 1) * pa.qs[2] + 8 * g;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const f32x4_t a = *reinterpret_cast<const f32x4_t*>(qrow + 32 * ks);
-            const f32x4_t b = *reinterpret_cast<const f32x4_t*>(qrow + 32 * ks + 4);
-            const float x[8] = {a[0] * sq, a[1] * sq, a[2] * sq, a[3] * sq, b[0] * sq, b[1] * sq, b[2] * sq, b[3] * sq};
-            x3_split8(x, qf[ks]);
-        }
-    }
     // K fragment rows: block kb's row r16 is tile key 8 (r16 / 4) + 4 kb + r16 % 4,
     // so score element e of block kb is key 8 g + 4 kb + e of the lane's query.
     int k_off[2][4];
@@ -1242,115 +1271,190 @@ prefill_f32x3_kernel(PrefillArgs pa) {
         }
     }
 
-    f32x4_t acc[8];
-#pragma unroll
-    for (int db = 0; db < 8; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    float ms = -INFINITY;      // running max of the lane's query (log2 domain) at the last raise
-    float b = 0.f;             // -ms once finite: the score chain's start
-    float lp = 0.f;            // the lane's part of the row sum
-    float cap = -1.f;          // kSumCap once ms is finite: the first tile always raises
+    const int segs = PAIRED ? n_seg : 1;
+#pragma unroll 1
+    for (int sg = 0; sg < segs; ++sg) {
+        const int qt = seg_qt[sg], k0 = seg_k0[sg], k1 = seg_k1[sg];
+        const int q0 = qt * qtile + (wave % wph) * 16;   // this wave's first query
+        // key tiles this wave computes: up to its last query's
+        const int wave_end = min(k1, q0 < L ? min(q0 + 15, L - 1) / kX3KTile + 1 : 0);
 
-    auto compute = [&](int kt, const lds_u8_t* sb) {
-        // ---- scores, two independent chains ----
-        f32x4_t s[2] = {f32x4_t{b, b, b, b}, f32x4_t{b, b, b, b}};
+        // ---- this wave's queries: q' = q * scale * log2(e), three terms of the
+        // B operand per 32-wide d step (lane: query q0 + r16, d 32 ks + 8 g ..) ----
+        bf16x8_t qf[4][3];
+        {
+            const float sq = pa.scale * kLog2eP;
+            const float* qrow = Q + (long long)min(q0 + r16, L - 1) * pa.qs[2] + 8 * g;
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            bf16x8_t kf[2][3];
+            for (int ks = 0; ks < 4; ++ks) {
+                const f32x4_t a = *reinterpret_cast<const f32x4_t*>(qrow + 32 * ks);
+                const f32x4_t b = *reinterpret_cast<const f32x4_t*>(qrow + 32 * ks + 4);
+                const float x[8] = {a[0] * sq, a[1] * sq, a[2] * sq, a[3] * sq,
+                                    b[0] * sq, b[1] * sq, b[2] * sq, b[3] * sq};
+                x3_split8(x, qf[ks]);
+            }
+        }
+
+        f32x4_t acc[8];
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+        for (int db = 0; db < 8; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        float ms = -INFINITY;      // running max of the lane's query (log2 domain) at the last raise
+        float b = 0.f;             // -ms once finite: the score chain's start
+        float lp = 0.f;            // the lane's part of the row sum
+        float cap = -1.f;          // kSumCap once ms is finite: the first tile always raises
+
+        auto compute = [&](int kt, const lds_u8_t* sb) {
+            // ---- scores, two independent chains ----
+            f32x4_t s[2] = {f32x4_t{b, b, b, b}, f32x4_t{b, b, b, b}};
 #pragma unroll
-                for (int t = 0; t < 3; ++t)
-                    kf[kb][t] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(
-                        sb + t * kX3TermBytes + k_off[kb][ks]);
-#pragma unroll
-            for (int pr = 0; pr < kX3Pairs; ++pr)
+            for (int ks = 0; ks < 4; ++ks) {
+                bf16x8_t kf[2][3];
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb)
-                    s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kb][x3_pair_a(pr)], qf[ks][x3_pair_b(pr)],
-                                                                    s[kb], 0, 0, 0);
-        }
-        if (kt * kX3KTile + kX3KTile - 1 > q0) {   // the diagonal: keys past the query
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+                    for (int t = 0; t < 3; ++t)
+                        kf[kb][t] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>(
+                            sb + t * kX3TermBytes + k_off[kb][ks]);
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (kt * kX3KTile + 8 * g + 4 * kb + e > q0 + r16) s[kb][e] = -INFINITY;
-        }
-        // ---- P = 2^s, its sum; raise the max when the sum left the cap ----
-        float p[8];
+                for (int pr = 0; pr < kX3Pairs; ++pr)
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) p[4 * kb + e] = __builtin_amdgcn_exp2f(s[kb][e]);
-        float rs = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
-        if (__any(!(rs <= cap))) {
-            float mt = s[0][0];
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) mt = fmaxf(mt, s[kb][e]);
-            mt = xmax16_32(mt);                       // the row: lanes r16, r16 + 16, + 32, + 48
-            const float mq = mt - b;                  // unbiased row max of this tile
-            const float m_new = fmaxf(ms, mq);
-            const float alpha = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - m_new);
-#pragma unroll
-            for (int db = 0; db < 8; ++db) acc[db] *= alpha;
-            lp *= alpha;
-            const float b_new = m_new == -INFINITY ? 0.f : -m_new;
-            const float delta = b_new - b;
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) p[4 * kb + e] = __builtin_amdgcn_exp2f(s[kb][e] + delta);
-            rs = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
-            ms = m_new;
-            b = b_new;
-            cap = m_new == -INFINITY ? -1.f : kSumCap;
-        }
-        lp += rs;
-        bf16x8_t pt[3];
-        x3_split8(p, pt);
-        // ---- O^T += V^T P^T, 8 blocks of 16 d ----
-#pragma unroll
-        for (int db = 0; db < 8; ++db) {
-            bf16x8_t vf[3];
-#pragma unroll
-            for (int t = 0; t < 3; ++t) {
-                const lds_u8_t* p0 = sb + t * kX3TermBytes + v_off[0][db];
-                const lds_u8_t* p1 = sb + t * kX3TermBytes + v_off[1][db];
-                const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p0);
-                const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p1);
-                vf[t] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                    for (int kb = 0; kb < 2; ++kb)
+                        s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kb][x3_pair_a(pr)],
+                                                                        qf[ks][x3_pair_b(pr)], s[kb], 0, 0, 0);
             }
+            if (kt * kX3KTile + kX3KTile - 1 > q0) {   // the diagonal: keys past the query
 #pragma unroll
-            for (int pr = 0; pr < kX3Pairs; ++pr)
-                acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[x3_pair_a(pr)], pt[x3_pair_b(pr)], acc[db], 0, 0, 0);
-        }
-    };
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (kt * kX3KTile + 8 * g + 4 * kb + e > q0 + r16) s[kb][e] = -INFINITY;
+            }
+            // ---- P = 2^s, its sum; raise the max when the sum left the cap ----
+            float p[8];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) p[4 * kb + e] = __builtin_amdgcn_exp2f(s[kb][e]);
+            float rs = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+            if (__any(!(rs <= cap))) {
+                float mt = s[0][0];
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) mt = fmaxf(mt, s[kb][e]);
+                mt = xmax16_32(mt);                       // the row: lanes r16, r16 + 16, + 32, + 48
+                const float mq = mt - b;                  // unbiased row max of this tile
+                const float m_new = fmaxf(ms, mq);
+                const float alpha = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - m_new);
+#pragma unroll
+                for (int db = 0; db < 8; ++db) acc[db] *= alpha;
+                lp *= alpha;
+                const float b_new = m_new == -INFINITY ? 0.f : -m_new;
+                const float delta = b_new - b;
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) p[4 * kb + e] = __builtin_amdgcn_exp2f(s[kb][e] + delta);
+                rs = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+                ms = m_new;
+                b = b_new;
+                cap = m_new == -INFINITY ? -1.f : kSumCap;
+            }
+            lp += rs;
+            bf16x8_t pt[3];
+            x3_split8(p, pt);
+            // ---- O^T += V^T P^T, 8 blocks of 16 d ----
+#pragma unroll
+            for (int db = 0; db < 8; ++db) {
+                bf16x8_t vf[3];
+#pragma unroll
+                for (int t = 0; t < 3; ++t) {
+                    const lds_u8_t* p0 = sb + t * kX3TermBytes + v_off[0][db];
+                    const lds_u8_t* p1 = sb + t * kX3TermBytes + v_off[1][db];
+                    const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p0);
+                    const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p1);
+                    vf[t] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                }
+#pragma unroll
+                for (int pr = 0; pr < kX3Pairs; ++pr)
+                    acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[x3_pair_a(pr)], pt[x3_pair_b(pr)],
+                                                                      acc[db], 0, 0, 0);
+            }
+        };
 
-    load_tile(0);
-    store_tile(0);
-    if (n_kt > 1) load_tile(1);
-    __syncthreads();
-    for (int kt = 0; kt < n_kt; ++kt) {
-        if (kt < wave_kt) compute(kt, lsm + (kt & 1) * kX3StageBytes);
-        if (kt + 1 < n_kt) {
-            store_tile((kt + 1) & 1);
-            if (kt + 2 < n_kt) load_tile(kt + 2);
-        }
+        // The previous segment's last iteration ended on a barrier: no wave
+        // still reads stage 0.
+        load_tile(k0);
+        store_tile(0);
+        if (k0 + 1 < k1) load_tile(k0 + 1);
         __syncthreads();
-    }
+        for (int kt = k0; kt < k1; ++kt) {
+            if (kt < wave_end) compute(kt, lsm + ((kt - k0) & 1) * kX3StageBytes);
+            if (kt + 1 < k1) {
+                store_tile((kt - k0 + 1) & 1);
+                if (kt + 2 < k1) load_tile(kt + 2);
+            }
+            __syncthreads();
+        }
 
-    // ---- O / l for query q0 + r16: lane holds O[q][16 db + 4 g + e] ----
-    const float l = xsum16_32(lp);
-    const int qi = q0 + r16;
-    if (qi < L) {
-        const float inv = 1.0f / l;
-        float* orow = pa.out + wk.b * pa.os[0] + h * pa.os[1] + (long long)qi * pa.os[2] + 4 * g;
+        // ---- lane holds O[q0 + r16][16 db + 4 g + e] (times l) ----
+        const float l = xsum16_32(lp);
+        const int qi = q0 + r16;
+        const int part = seg_part[sg];
+        if (qi < L && part < 0) {
+            const float inv = 1.0f / l;
+            float* orow = pa.out + wk.b * pa.os[0] + h * pa.os[1] + (long long)qi * pa.os[2] + 4 * g;
 #pragma unroll
-        for (int db = 0; db < 8; ++db)
-            *reinterpret_cast<float4*>(orow + 16 * db) =
-                make_float4(acc[db][0] * inv, acc[db][1] * inv, acc[db][2] * inv, acc[db][3] * inv);
+            for (int db = 0; db < 8; ++db)
+                *reinterpret_cast<float4*>(orow + 16 * db) =
+                    make_float4(acc[db][0] * inv, acc[db][1] * inv, acc[db][2] * inv, acc[db][3] * inv);
+        } else if (qi < L) {
+            // partial rows: [2][part_rows][128] O, then [2][part_rows] (m, l);
+            // row ((b Hq + h) n_pairs + pair) qtile + query within the tile
+            const int np = pa.n_qt / 2;
+            const long long row =
+                (((long long)wk.b * pa.Hq + h) * np + (pa.n_qt - 1 - qt)) * qtile + (qi - qt * qtile);
+            float* po = pa.part + ((long long)part * pa.part_rows + row) * 128 + 4 * g;
+#pragma unroll
+            for (int db = 0; db < 8; ++db)
+                *reinterpret_cast<float4*>(po + 16 * db) = make_float4(acc[db][0], acc[db][1], acc[db][2], acc[db][3]);
+            if (g == 0)
+                *reinterpret_cast<float2*>(pa.part + 2 * pa.part_rows * 128 + 2 * (part * pa.part_rows + row)) =
+                    make_float2(ms, l);
+        }
+    }
+}
+
+// The rows of query tiles whose key tiles the two workgroups of a pair
+// split: O = (2^(m0-M) O0 + 2^(m1-M) O1) / (2^(m0-M) l0 + 2^(m1-M) l1), M the
+// larger m, each partial's O and l taken against its own m (log2 domain).
+// One workgroup per (batch, query head, pair); pairs without a split return.
+__global__ void __launch_bounds__(256) prefill_x3_merge_kernel(PrefillArgs pa) {
+    const int np = pa.n_qt / 2;
+    const int pair = blockIdx.x % np;
+    const int bh = blockIdx.x / np;   // batch * Hq + query head
+    const int qtile = pa.q_tile;
+    const int u = pa.n_qt - 1 - pair;
+    if (x3_pair_split(pa.L, qtile, pair, u) == 0) return;
+    const int bi = bh / pa.Hq, h = bh % pa.Hq;
+    const long long row0 = ((long long)bh * np + pair) * qtile;
+    const float4* o0 = reinterpret_cast<const float4*>(pa.part + row0 * 128);
+    const float4* o1 = reinterpret_cast<const float4*>(pa.part + (pa.part_rows + row0) * 128);
+    const float2* ml0 = reinterpret_cast<const float2*>(pa.part + 2 * pa.part_rows * 128) + row0;
+    const float2* ml1 = ml0 + pa.part_rows;
+    for (int i = threadIdx.x; i < qtile * 32; i += 256) {
+        const int r = i >> 5, c = i & 31;
+        const int q = u * qtile + r;
+        if (q >= pa.L) break;
+        const float2 a = ml0[r], bb = ml1[r];
+        const float M = fmaxf(a.x, bb.x);
+        const float w0 = a.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(a.x - M);
+        const float w1 = bb.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(bb.x - M);
+        const float inv = 1.0f / (w0 * a.y + w1 * bb.y);
+        const float4 x = o0[r * 32 + c], y = o1[r * 32 + c];
+        *reinterpret_cast<float4*>(pa.out + bi * pa.os[0] + h * pa.os[1] + (long long)q * pa.os[2] + 4 * c) =
+            make_float4((w0 * x.x + w1 * y.x) * inv, (w0 * x.y + w1 * y.y) * inv, (w0 * x.z + w1 * y.z) * inv,
+                        (w0 * x.w + w1 * y.w) * inv);
     }
 }
 
@@ -1626,11 +1730,19 @@ long long bf16_grid(const PrefillArgs& pa, int B, int W) {
 }
 
 template <int W>
-sa_status launch_f32x3(const PrefillArgs& pa, dim3 grid, hipStream_t st) {
+sa_status launch_f32x3(const PrefillArgs& pa, dim3 grid, bool paired, hipStream_t st) {
     constexpr int bytes = 2 * kX3StageBytes;
-    sa_status s = opt_in_lds<&prefill_f32x3_kernel<W>>(bytes);
-    if (s == SA_OK) hipLaunchKernelGGL(prefill_f32x3_kernel<W>, grid, dim3(W * 64), bytes, st, pa);
-    return s;
+    if (paired) {
+        SA_TRY((opt_in_lds<&prefill_f32x3_kernel<W, true>>(bytes)));
+        hipLaunchKernelGGL((prefill_f32x3_kernel<W, true>), grid, dim3(W * 64), bytes, st, pa);
+        SA_CHECK_LAUNCH();
+        const long long n_merge = pa.part_rows / pa.q_tile;   // (batch, query head, pair)
+        hipLaunchKernelGGL(prefill_x3_merge_kernel, dim3(static_cast<unsigned>(n_merge)), dim3(256), 0, st, pa);
+        return SA_OK;
+    }
+    SA_TRY((opt_in_lds<&prefill_f32x3_kernel<W, false>>(bytes)));
+    hipLaunchKernelGGL((prefill_f32x3_kernel<W, false>), grid, dim3(W * 64), bytes, st, pa);
+    return SA_OK;
 }
 
 // Workgroups of the three-term fp32 kernel: W waves of 16 queries serve
@@ -1648,7 +1760,23 @@ struct PfPlan {
     int W;        // Bf: waves per workgroup (kBfWSmall or kBfW)
     int gh;       // query heads per workgroup
     int q_tile;   // query rows per workgroup and head
+    bool pair;    // F32x3: the shape takes paired key ranges when given a workspace
 };
+
+// Paired three-term launches: one round of workgroups (96 KiB of LDS each,
+// so one per CU) and at least this many query tiles per head.
+constexpr int kX3PairMinTiles = 8;
+
+// Rows of partials a paired launch of this plan writes: (batch, query head,
+// pair, query of the tile).
+long long x3_part_rows(const PrefillArgs& pa, int B, const PfPlan& plan) {
+    const int n_qt = (pa.L + plan.q_tile - 1) / plan.q_tile;
+    return (long long)B * pa.Hq * (n_qt / 2) * plan.q_tile;
+}
+
+size_t x3_ws_bytes(const PrefillArgs& pa, int B, const PfPlan& plan) {
+    return plan.pair ? (size_t)x3_part_rows(pa, B, plan) * 2 * (128 + 2) * sizeof(float) : 0;
+}
 
 PfPlan plan_prefill(const PrefillArgs& pa, int B, bool bf16, int D) {
     const int G = pa.Hq / pa.Hkv;
@@ -1661,11 +1789,11 @@ PfPlan plan_prefill(const PrefillArgs& pa, int B, bool bf16, int D) {
     // kernel of that tile takes the launch's own choice.
     const int want = attn_q_block();
     if (want > 0) {
-        if (!bf16) return {want == 32 ? PfKind::F32Split : PfKind::F32, 0, 1, want};
-        if (want == 32 && split_shape) return {PfKind::BfSplit, 0, kSplitGH, 32};
+        if (!bf16) return {want == 32 ? PfKind::F32Split : PfKind::F32, 0, 1, want, false};
+        if (want == 32 && split_shape) return {PfKind::BfSplit, 0, kSplitGH, 32, false};
         for (int W : {kBfWSmall, kBfW}) {
             const int gh = std::gcd(G, W);
-            if ((W / gh) * kBfQB * 32 == want) return {PfKind::Bf, W, gh, want};
+            if ((W / gh) * kBfQB * 32 == want) return {PfKind::Bf, W, gh, want, false};
         }
     }
     // bf16: 8-wave workgroups while they give every CU two of them; below
@@ -1685,7 +1813,7 @@ PfPlan plan_prefill(const PrefillArgs& pa, int B, bool bf16, int D) {
     const char* fsplit = std::getenv("SA_PREFILL_SPLIT");
     const bool split = split_shape && (fsplit ? std::atoi(fsplit) != 0
                                               : !forced && bf16_grid(pa, B, kBfWSmall) <= device_cu_count());
-    if (split) return {PfKind::BfSplit, 0, kSplitGH, 32};
+    if (split) return {PfKind::BfSplit, 0, kSplitGH, 32, false};
     // fp32: 32-query workgroups whose waves split each tile's keys while
     // 128-query ones would give fewer than two workgroups per CU.  Measured
     // (16/8 heads, D = 128, graph-replayed calls): L = 128 / 512 / 1024 /
@@ -1700,23 +1828,43 @@ PfPlan plan_prefill(const PrefillArgs& pa, int B, bool bf16, int D) {
     if (!bf16 && D == 128 && !fsplit && (!fx3 || std::atoi(fx3) != 0)) {
         const int W = x3_grid(pa, B, 8) >= device_cu_count() ? 8 : 4;
         const int gh = std::gcd(G, W);
-        return {PfKind::F32x3, W, gh, (W / gh) * 16};
+        const int q_tile = (W / gh) * 16;
+        // Paired key ranges where the grid is one round: the longest query
+        // tile no longer sets the launch's time (its keys are split with the
+        // shortest tile's workgroup).  SA_PREFILL_PAIR=0 / 1 turns them off /
+        // on regardless of the size rules (one round of workgroups still required).
+        const char* fpair = std::getenv("SA_PREFILL_PAIR");
+        const int n_qt = (pa.L + q_tile - 1) / q_tile;
+        const bool one_round = x3_grid(pa, B, W) <= device_cu_count();
+        const bool pair = one_round && n_qt >= 2 &&
+                          (fpair ? std::atoi(fpair) != 0 : n_qt >= kX3PairMinTiles);
+        return {PfKind::F32x3, W, gh, q_tile, pair};
     }
     if (!bf16) {
         const bool fsp = fsplit ? std::atoi(fsplit) != 0
                                 : (long long)B * pa.Hq * ((pa.L + kFQTile - 1) / kFQTile) < 2LL * device_cu_count();
-        return fsp ? PfPlan{PfKind::F32Split, 0, 1, 32} : PfPlan{PfKind::F32, 0, 1, kFQTile};
+        return fsp ? PfPlan{PfKind::F32Split, 0, 1, 32, false} : PfPlan{PfKind::F32, 0, 1, kFQTile, false};
     }
     const int W = fw == kBfW || fw == kBfWSmall ? fw
                   : bf16_grid(pa, B, kBfW) < 2LL * device_cu_count() ? kBfWSmall : kBfW;
     const int gh = std::gcd(G, W);
-    return {PfKind::Bf, W, gh, (W / gh) * kBfQB * 32};
+    return {PfKind::Bf, W, gh, (W / gh) * kBfQB * 32, false};
 }
 
-sa_status launch(PrefillArgs pa, int B, bool bf16, int D, hipStream_t st) {
+// ws / ws_bytes: the caller's workspace, or null / 0.  A paired shape (see
+// PfPlan::pair) with a workspace of at least x3_ws_bytes takes paired key
+// ranges; without one, the single launch.
+sa_status launch(PrefillArgs pa, int B, bool bf16, int D, void* ws, size_t ws_bytes, hipStream_t st) {
     const PfPlan plan = plan_prefill(pa, B, bf16, D);
     pa.gh = plan.gh;
+    pa.q_tile = plan.q_tile;
     pa.n_qt = (pa.L + plan.q_tile - 1) / plan.q_tile;
+    const bool paired = plan.pair && ws != nullptr;
+    if (paired) {
+        if (ws_bytes < x3_ws_bytes(pa, B, plan)) return fail(SA_ENOMEM, "workspace too small for prefill partials");
+        pa.part = static_cast<float*>(ws);
+        pa.part_rows = x3_part_rows(pa, B, plan);
+    }
     const int groups = B * pa.Hkv;
     pa.xcd_groups = groups % 8 == 0 ? groups / 8 : 0;
     const long long n_wg = (long long)B * (pa.Hq / pa.gh) * pa.n_qt;
@@ -1728,7 +1876,7 @@ sa_status launch(PrefillArgs pa, int B, bool bf16, int D, hipStream_t st) {
             s = launch_bf16_split(pa, grid, st);
             break;
         case PfKind::F32x3:
-            s = plan.W == 8 ? launch_f32x3<8>(pa, grid, st) : launch_f32x3<4>(pa, grid, st);
+            s = plan.W == 8 ? launch_f32x3<8>(pa, grid, paired, st) : launch_f32x3<4>(pa, grid, paired, st);
             break;
         case PfKind::F32Split:
             switch (D) {
@@ -1782,8 +1930,9 @@ sa_status launch(PrefillArgs pa, int B, bool bf16, int D, hipStream_t st) {
 
 sa_status prefill(const void* q, const void* k, const void* v, sa_dtype dtype, int batch, int n_q_heads,
                   int n_kv_heads, int L, int D, const int64_t* qs, const int64_t* kvs, const int64_t* os,
-                  float scale, float* out, hipStream_t st) {
+                  float scale, float* out, void* ws, size_t ws_bytes, hipStream_t st) {
     if (!q || !k || !v || !out || !qs || !kvs || !os) return fail(SA_EINVAL, "null pointer");
+    if (ws && !aligned16(ws)) return fail(SA_EINVAL, "workspace must be 16-byte aligned");
     if (batch <= 0 || n_q_heads <= 0 || n_kv_heads <= 0 || n_q_heads % n_kv_heads)
         return fail(SA_EINVAL, "bad head counts");
     if (dtype != SA_DTYPE_F32 && dtype != SA_DTYPE_BF16) return fail(SA_EINVAL, "dtype must be F32 or BF16");
@@ -1811,7 +1960,7 @@ sa_status prefill(const void* q, const void* k, const void* v, sa_dtype dtype, i
     pa.scale = scale;
     pa.sl2 = fabsf(scale) * kLog2eP;
     pa.q_sign = scale < 0.f ? 0x80008000u : 0u;
-    return launch(pa, batch, dtype == SA_DTYPE_BF16, D, st);
+    return launch(pa, batch, dtype == SA_DTYPE_BF16, D, ws, ws_bytes, st);
 }
 
 }  // namespace
@@ -1829,14 +1978,32 @@ extern "C" int sa_prefill_query_tile(sa_dtype dtype, int batch, int n_q_heads, i
     return sa::plan_prefill(pa, batch, dtype == SA_DTYPE_BF16, D).q_tile;
 }
 
+extern "C" size_t sa_prefill_causal_ws_bytes(sa_dtype dtype, int batch, int n_q_heads, int n_kv_heads, int L,
+                                             int D) {
+    if (dtype != SA_DTYPE_F32 && dtype != SA_DTYPE_BF16) return 0;
+    if (batch <= 0 || n_q_heads <= 0 || n_kv_heads <= 0 || n_q_heads % n_kv_heads || L <= 0) return 0;
+    if (dtype == SA_DTYPE_BF16 ? D != 64 && D != 128 : D != 16 && D != 32 && D != 64 && D != 128) return 0;
+    sa::PrefillArgs pa{};
+    pa.Hq = n_q_heads; pa.Hkv = n_kv_heads; pa.L = L;
+    const sa::PfPlan plan = sa::plan_prefill(pa, batch, dtype == SA_DTYPE_BF16, D);
+    return sa::x3_ws_bytes(pa, batch, plan);
+}
+
 extern "C" sa_status sa_prefill_causal(const void* q, const void* k, const void* v, sa_dtype dtype,
                                        int batch, int n_q_heads, int n_kv_heads, int L, int D,
                                        float scale, float* out, sa_stream_t stream) {
+    return sa_prefill_causal_ws(q, k, v, dtype, batch, n_q_heads, n_kv_heads, L, D, scale, out, nullptr, 0, stream);
+}
+
+extern "C" sa_status sa_prefill_causal_ws(const void* q, const void* k, const void* v, sa_dtype dtype,
+                                          int batch, int n_q_heads, int n_kv_heads, int L, int D,
+                                          float scale, float* out, void* ws, size_t ws_bytes,
+                                          sa_stream_t stream) {
     sa::clear_error();
     const int64_t Ld = (int64_t)L * D;
     const int64_t qs[3] = {n_q_heads * Ld, Ld, D};
     const int64_t kvs[3] = {n_kv_heads * Ld, Ld, D};
-    return sa::prefill(q, k, v, dtype, batch, n_q_heads, n_kv_heads, L, D, qs, kvs, qs, scale, out,
+    return sa::prefill(q, k, v, dtype, batch, n_q_heads, n_kv_heads, L, D, qs, kvs, qs, scale, out, ws, ws_bytes,
                        sa::as_stream(stream));
 }
 
@@ -1845,7 +2012,16 @@ extern "C" sa_status sa_prefill_causal_strided(const void* q, const void* k, con
                                                const int64_t q_strides[3], const int64_t kv_strides[3],
                                                const int64_t out_strides[3], float scale, float* out,
                                                sa_stream_t stream) {
+    return sa_prefill_causal_strided_ws(q, k, v, dtype, batch, n_q_heads, n_kv_heads, L, D, q_strides, kv_strides,
+                                        out_strides, scale, out, nullptr, 0, stream);
+}
+
+extern "C" sa_status sa_prefill_causal_strided_ws(const void* q, const void* k, const void* v, sa_dtype dtype,
+                                                  int batch, int n_q_heads, int n_kv_heads, int L, int D,
+                                                  const int64_t q_strides[3], const int64_t kv_strides[3],
+                                                  const int64_t out_strides[3], float scale, float* out, void* ws,
+                                                  size_t ws_bytes, sa_stream_t stream) {
     sa::clear_error();
     return sa::prefill(q, k, v, dtype, batch, n_q_heads, n_kv_heads, L, D, q_strides, kv_strides, out_strides,
-                       scale, out, sa::as_stream(stream));
+                       scale, out, ws, ws_bytes, sa::as_stream(stream));
 }

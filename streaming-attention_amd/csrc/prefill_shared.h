@@ -37,6 +37,9 @@ struct PrefillArgs {
     float sl2;          // |scale| * log2(e)
     uint32_t q_sign;    // 0x80008000 to negate bf16 q pairs (negative scale), else 0
     float scale;        // signed scale (fp32 kernel)
+    int q_tile;         // query rows per workgroup and head
+    float* part;        // paired three-term launches: the split tiles' partials
+    long long part_rows;
 };
 
 // Work mapping shared by both kernels.  A KV group is one (batch, kv head);

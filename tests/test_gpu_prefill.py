@@ -171,6 +171,109 @@ def test_prefill_fp32_three_term_every_row_of_a_group(sa, oracle, synth, monkeyp
     assert rel_l2(got, want) <= 1e-5
 
 
+def prefill_ws(sa, B, Hq, Hkv, L, D=128, dtype=None):
+    """A workspace of the size sa_prefill_causal_ws_bytes asks for (at least
+    16 bytes, so it is a real allocation), and that size."""
+    n = sa.prefill_ws_bytes(sa.SA_DTYPE_F32 if dtype is None else dtype, B, Hq, Hkv, L, D)
+    return torch.zeros(max(n, 16), dtype=torch.uint8, device="cuda"), n
+
+
+@pytest.mark.parametrize("B,L,Hq,Hkv,pair", [
+    (1, 1024, 16, 8, "auto"),   # 4-wave workgroups, 32 query tiles: 15 split pairs, one whole
+    (1, 2048, 16, 8, "auto"),   # 8-wave workgroups, 64-query tiles
+    (1, 1000, 16, 8, "auto"),   # a ragged last tile
+    (1, 256, 16, 8, "auto"),    # 8 query tiles, the fewest the size rule pairs
+    (2, 300, 16, 8, "auto"),    # two batches
+    (1, 777, 8, 2, "auto"),     # GQA groups of 4
+    (1, 1024, 4, 4, "auto"),    # one query head per KV head
+    (1, 77, 16, 8, "on"),       # 3 query tiles: an odd middle tile
+    (1, 33, 16, 8, "on"),       # 2 query tiles: a pair without a split
+])
+def test_prefill_fp32_paired_key_ranges(sa, oracle, synth, monkeypatch, B, L, Hq, Hkv, pair):
+    """sa_prefill_causal_ws on one round of three-term workgroups: query tile
+    t and tile n_qt-1-t share a pair of workgroups that split their key
+    tiles, and a second launch merges the split tiles' two partials.  Every
+    row of every head against the single launch (sa_prefill_causal; both at
+    fp32 rounding of the same sums, max-abs <= 1e-5), and every row of the
+    heads of the first and the last KV group at the fp32 bar (max-abs 1e-4,
+    relative L2 1e-5) against the oracle, RoPE'd q and k."""
+    f32_variant(monkeypatch, "default")
+    monkeypatch.delenv("SA_PREFILL_PAIR", raising=False)
+    if pair == "on":
+        monkeypatch.setenv("SA_PREFILL_PAIR", "1")
+    D = 128
+    q, k, v = (synth.normal(70 + L % 89, i, (B, H, L, D)) for i, H in ((1, Hq), (2, Hkv), (3, Hkv)))
+    q, k = roped(oracle, q), roped(oracle, k)
+    sc = np.float32(1 / np.sqrt(D))
+    ws, n = prefill_ws(sa, B, Hq, Hkv, L)
+    assert n > 0
+    dq, dk, dv = dev(q), dev(k), dev(v)
+    paired = host(sa.prefill_causal(dq, dk, dv, float(sc), ws=ws))
+    single = host(sa.prefill_causal(dq, dk, dv, float(sc)))
+    assert np.abs(paired - single).max() <= 1e-5
+    G = Hq // Hkv
+    for kvh in (0, Hkv - 1):
+        heads = slice(kvh * G, (kvh + 1) * G)
+        got = paired[:, heads]
+        want = oracle.prefill_blockwise(q[:, heads], k[:, kvh:kvh + 1], v[:, kvh:kvh + 1], sc, 64)
+        assert np.abs(got - want).max() <= 1e-4, kvh
+        assert rel_l2(got, want) <= 1e-5, kvh
+
+
+def test_prefill_paired_workspace_rules(sa, synth, monkeypatch):
+    """Shapes without partials ask for no workspace and ignore one (bf16; fp32
+    at L = 8192, several rounds of workgroups); a workspace one byte short
+    is refused with SA_ENOMEM, a misaligned one with SA_EINVAL, and neither
+    writes the output; a null workspace takes the single launch."""
+    f32_variant(monkeypatch, "default")
+    monkeypatch.delenv("SA_PREFILL_PAIR", raising=False)
+    assert sa.prefill_ws_bytes(sa.SA_DTYPE_BF16, 1, 16, 8, 1024, 128) == 0
+    assert sa.prefill_ws_bytes(sa.SA_DTYPE_F32, 1, 16, 8, 8192, 128) == 0
+    assert sa.prefill_ws_bytes(sa.SA_DTYPE_F32, 1, 16, 8, 128, 128) == 0
+    assert sa.prefill_ws_bytes(sa.SA_DTYPE_F32, 1, 16, 8, 1024, 64) == 0
+    L = 512
+    q, k, v = (dev(x) for x in inputs(synth, L, seed=71))
+    ws, n = prefill_ws(sa, 1, 16, 8, L)
+    # partial rows: 16 heads x 8 pairs x 32 queries, two partials of 128 + 2 floats
+    assert n == 16 * 8 * 32 * 2 * 130 * 4
+    out = torch.full((1, 16, L, 128), 7.0, device="cuda")
+    with pytest.raises(sa.SaError) as e:
+        sa.prefill_causal(q, k, v, 0.1, out=out, ws=ws[:n - 1])
+    assert e.value.status == sa.SA_ENOMEM
+    with pytest.raises(sa.SaError) as e:
+        sa.prefill_causal(q, k, v, 0.1, out=out, ws=ws[4:])
+    assert e.value.status == sa.SA_EINVAL
+    assert bool((out == 7.0).all())
+    bq, bk, bv = (x.to(torch.bfloat16) for x in (q, k, v))
+    a = host(sa.prefill_causal(bq, bk, bv, 0.1, ws=ws))
+    b = host(sa.prefill_causal(bq, bk, bv, 0.1))
+    assert np.array_equal(a, b)
+
+
+def test_prefill_paired_graph_replay(sa, synth, monkeypatch):
+    """The paired launch (both kernels) captured in a HIP graph and replayed
+    three times, with eager calls between the replays: every replay equals
+    the eager paired call bit for bit (the merge reads only partials the
+    same replay wrote)."""
+    f32_variant(monkeypatch, "default")
+    monkeypatch.delenv("SA_PREFILL_PAIR", raising=False)
+    L = 1024
+    q, k, v = (dev(x) for x in inputs(synth, L, seed=72))
+    ws, _ = prefill_ws(sa, 1, 16, 8, L)
+    want = host(sa.prefill_causal(q, k, v, 0.08838834764831845, ws=ws))
+    out = torch.empty(1, 16, L, 128, device="cuda")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        sa.prefill_causal(q, k, v, 0.08838834764831845, out=out, ws=ws,
+                          stream=torch.cuda.current_stream().cuda_stream)
+    for i in range(3):
+        out.fill_(float("nan"))
+        g.replay()
+        assert np.array_equal(host(out), want), i
+        other = host(sa.prefill_causal(k.repeat(1, 2, 1, 1).contiguous(), k, v, 0.05, ws=ws))
+        assert np.isfinite(other).all()
+
+
 def test_prefill_fp32_8192_rows(sa, oracle, synth):
     L = 8192
     q, k, v = inputs(synth, L)
