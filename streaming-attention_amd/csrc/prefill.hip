@@ -1429,6 +1429,10 @@ prefill_f32x3_kernel(PrefillArgs pa) {
 // split: O = (2^(m0-M) O0 + 2^(m1-M) O1) / (2^(m0-M) l0 + 2^(m1-M) l1), M the
 // larger m, each partial's O and l taken against its own m (log2 domain).
 // One workgroup per (batch, query head, pair); pairs without a split return.
+// A thread takes float4 column c of rows r, r + 8, ... (qtile <= 64 rows:
+// at most 8); every load is issued before the first use (rows past L load
+// the tile's first row and store nothing).
+constexpr int kX3MergeRows = 8;
 __global__ void __launch_bounds__(256) prefill_x3_merge_kernel(PrefillArgs pa) {
     const int np = pa.n_qt / 2;
     const int pair = blockIdx.x % np;
@@ -1442,19 +1446,31 @@ __global__ void __launch_bounds__(256) prefill_x3_merge_kernel(PrefillArgs pa) {
     const float4* o1 = reinterpret_cast<const float4*>(pa.part + (pa.part_rows + row0) * 128);
     const float2* ml0 = reinterpret_cast<const float2*>(pa.part + 2 * pa.part_rows * 128) + row0;
     const float2* ml1 = ml0 + pa.part_rows;
-    for (int i = threadIdx.x; i < qtile * 32; i += 256) {
-        const int r = i >> 5, c = i & 31;
-        const int q = u * qtile + r;
-        if (q >= pa.L) break;
-        const float2 a = ml0[r], bb = ml1[r];
-        const float M = fmaxf(a.x, bb.x);
-        const float w0 = a.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(a.x - M);
-        const float w1 = bb.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(bb.x - M);
-        const float inv = 1.0f / (w0 * a.y + w1 * bb.y);
-        const float4 x = o0[r * 32 + c], y = o1[r * 32 + c];
-        *reinterpret_cast<float4*>(pa.out + bi * pa.os[0] + h * pa.os[1] + (long long)q * pa.os[2] + 4 * c) =
-            make_float4((w0 * x.x + w1 * y.x) * inv, (w0 * x.y + w1 * y.y) * inv, (w0 * x.z + w1 * y.z) * inv,
-                        (w0 * x.w + w1 * y.w) * inv);
+    const int c = threadIdx.x & 31, r0 = threadIdx.x >> 5;
+    const int rows = min(qtile, pa.L - u * qtile);   // rows of the tile below L
+    float4 x[kX3MergeRows], y[kX3MergeRows];
+    float2 a[kX3MergeRows], b[kX3MergeRows];
+#pragma unroll
+    for (int i = 0; i < kX3MergeRows; ++i) {
+        const int r = r0 + 8 * i < rows ? r0 + 8 * i : 0;
+        a[i] = ml0[r];
+        b[i] = ml1[r];
+        x[i] = o0[r * 32 + c];
+        y[i] = o1[r * 32 + c];
+    }
+    float* out = pa.out + bi * pa.os[0] + h * pa.os[1] + (long long)u * qtile * pa.os[2] + 4 * c;
+#pragma unroll
+    for (int i = 0; i < kX3MergeRows; ++i) {
+        const int r = r0 + 8 * i;
+        if (r < rows) {
+            const float M = fmaxf(a[i].x, b[i].x);
+            const float w0 = a[i].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(a[i].x - M);
+            const float w1 = b[i].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(b[i].x - M);
+            const float inv = 1.0f / (w0 * a[i].y + w1 * b[i].y);
+            *reinterpret_cast<float4*>(out + (long long)r * pa.os[2]) =
+                make_float4((w0 * x[i].x + w1 * y[i].x) * inv, (w0 * x[i].y + w1 * y[i].y) * inv,
+                            (w0 * x[i].z + w1 * y[i].z) * inv, (w0 * x[i].w + w1 * y[i].w) * inv);
+        }
     }
 }
 
@@ -1836,7 +1852,7 @@ PfPlan plan_prefill(const PrefillArgs& pa, int B, bool bf16, int D) {
         const char* fpair = std::getenv("SA_PREFILL_PAIR");
         const int n_qt = (pa.L + q_tile - 1) / q_tile;
         const bool one_round = x3_grid(pa, B, W) <= device_cu_count();
-        const bool pair = one_round && n_qt >= 2 &&
+        const bool pair = one_round && n_qt >= 2 && q_tile <= 8 * kX3MergeRows &&
                           (fpair ? std::atoi(fpair) != 0 : n_qt >= kX3PairMinTiles);
         return {PfKind::F32x3, W, gh, q_tile, pair};
     }
