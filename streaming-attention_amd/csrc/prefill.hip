@@ -1146,21 +1146,6 @@ __device__ __forceinline__ void x3_split8(const float* x, bf16x8_t (&t)[3]) {
     for (int k = 0; k < 3; ++k) t[k] = __builtin_bit_cast(bf16x8_t, u32x4_t{w[k][0], w[k][1], w[k][2], w[k][3]});
 }
 
-// Key tiles of query tile t (tiles of qtile rows) under the causal mask.
-__host__ __device__ constexpr int x3_key_tiles(int L, int qtile, int t) {
-    return ((L < (t + 1) * qtile ? L : (t + 1) * qtile) - 1) / kX3KTile + 1;
-}
-
-// Paired launches (short prompts, one round of workgroups): query tile t and
-// tile u = n_qt - 1 - t form a pair whose key tiles add up to about the same
-// count for every t.  Workgroup A computes tile t whole and the first s key
-// tiles of u; workgroup B the rest of u's; so every workgroup walks about
-// half the longest tile's keys instead of up to all of them.  u's two
-// partials meet in prefill_x3_merge_kernel.  s = 0: no split, B writes u.
-__host__ __device__ constexpr int x3_pair_split(int L, int qtile, int t, int u) {
-    return (x3_key_tiles(L, qtile, u) - x3_key_tiles(L, qtile, t)) / 2;
-}
-
 template <int W, bool PAIRED>
 __global__ void __launch_bounds__(W * 64)
 prefill_f32x3_kernel(PrefillArgs pa) {
@@ -1184,36 +1169,9 @@ prefill_f32x3_kernel(PrefillArgs pa) {
     const long long kv_row = pa.kvs[2];
 
     // ---- segments: (query tile, key tiles [k0, k1), output) ----
-    // part < 0: the output rows; else partial slot part of the pair.
-    int seg_qt[2] = {wk.qt, 0}, seg_k0[2] = {0, 0}, seg_k1[2] = {x3_key_tiles(L, qtile, wk.qt), 0};
-    int seg_part[2] = {-1, -1};
-    int n_seg = 1;
-    if constexpr (PAIRED) {
-        const int slot = pa.n_qt - 1 - wk.qt;     // slot 0 is dispatched first
-        const int np = pa.n_qt / 2;
-        if (slot >= 2 * np) {                     // the middle tile of an odd count
-            seg_qt[0] = np;
-            seg_k1[0] = x3_key_tiles(L, qtile, np);
-        } else {
-            const int t = slot >> 1, u = pa.n_qt - 1 - t;
-            const int s = x3_pair_split(L, qtile, t, u);
-            if (slot & 1) {                       // A: tile t whole, then u's first s key tiles
-                seg_qt[0] = t;
-                seg_k1[0] = x3_key_tiles(L, qtile, t);
-                if (s > 0) {
-                    seg_qt[1] = u;
-                    seg_k1[1] = s;
-                    seg_part[1] = 0;
-                    n_seg = 2;
-                }
-            } else {                              // B: the rest of u's key tiles
-                seg_qt[0] = u;
-                seg_k0[0] = s;
-                seg_k1[0] = x3_key_tiles(L, qtile, u);
-                seg_part[0] = s > 0 ? 1 : -1;
-            }
-        }
-    }
+    const PairSegs sg = PAIRED ? pair_segments(pa, wk.qt, qtile, kX3KTile)
+                               : PairSegs{1, {wk.qt, 0}, {0, 0}, {pair_key_tiles(L, qtile, kX3KTile, wk.qt), 0},
+                                          {-1, -1}};
 
     // ---- tile staging: fp32 rows in registers, three bf16 terms in LDS ----
     f32x4_t sk[NC], sv[NC];
@@ -1271,10 +1229,10 @@ prefill_f32x3_kernel(PrefillArgs pa) {
         }
     }
 
-    const int segs = PAIRED ? n_seg : 1;
+    const int segs = PAIRED ? sg.n : 1;
 #pragma unroll 1
-    for (int sg = 0; sg < segs; ++sg) {
-        const int qt = seg_qt[sg], k0 = seg_k0[sg], k1 = seg_k1[sg];
+    for (int si = 0; si < segs; ++si) {
+        const int qt = si ? sg.qt[1] : sg.qt[0], k0 = si ? sg.k0[1] : sg.k0[0], k1 = si ? sg.k1[1] : sg.k1[0];
         const int q0 = qt * qtile + (wave % wph) * 16;   // this wave's first query
         // key tiles this wave computes: up to its last query's
         const int wave_end = min(k1, q0 < L ? min(q0 + 15, L - 1) / kX3KTile + 1 : 0);
@@ -1400,7 +1358,7 @@ prefill_f32x3_kernel(PrefillArgs pa) {
         // ---- lane holds O[q0 + r16][16 db + 4 g + e] (times l) ----
         const float l = xsum16_32(lp);
         const int qi = q0 + r16;
-        const int part = seg_part[sg];
+        const int part = si ? sg.part[1] : sg.part[0];
         if (qi < L && part < 0) {
             const float inv = 1.0f / l;
             float* orow = pa.out + wk.b * pa.os[0] + h * pa.os[1] + (long long)qi * pa.os[2] + 4 * g;
@@ -1409,11 +1367,7 @@ prefill_f32x3_kernel(PrefillArgs pa) {
                 *reinterpret_cast<float4*>(orow + 16 * db) =
                     make_float4(acc[db][0] * inv, acc[db][1] * inv, acc[db][2] * inv, acc[db][3] * inv);
         } else if (qi < L) {
-            // partial rows: [2][part_rows][128] O, then [2][part_rows] (m, l);
-            // row ((b Hq + h) n_pairs + pair) qtile + query within the tile
-            const int np = pa.n_qt / 2;
-            const long long row =
-                (((long long)wk.b * pa.Hq + h) * np + (pa.n_qt - 1 - qt)) * qtile + (qi - qt * qtile);
+            const long long row = pair_row(pa, wk.b, h, qt, qi);
             float* po = pa.part + ((long long)part * pa.part_rows + row) * 128 + 4 * g;
 #pragma unroll
             for (int db = 0; db < 8; ++db)
@@ -1425,21 +1379,21 @@ prefill_f32x3_kernel(PrefillArgs pa) {
     }
 }
 
-// The rows of query tiles whose key tiles the two workgroups of a pair
-// split: O = (2^(m0-M) O0 + 2^(m1-M) O1) / (2^(m0-M) l0 + 2^(m1-M) l1), M the
+// The second launch of a paired three-term launch: the rows of query tiles
+// whose key tiles the two workgroups of a pair split: O = (2^(m0-M) O0 + 2^(m1-M) O1) / (2^(m0-M) l0 + 2^(m1-M) l1), M the
 // larger m, each partial's O and l taken against its own m (log2 domain).
 // One workgroup per (batch, query head, pair); pairs without a split return.
 // A thread takes float4 column c of rows r, r + 8, ... (qtile <= 64 rows:
 // at most 8); every load is issued before the first use (rows past L load
 // the tile's first row and store nothing).
-constexpr int kX3MergeRows = 8;
-__global__ void __launch_bounds__(256) prefill_x3_merge_kernel(PrefillArgs pa) {
+constexpr int kPairMergeRows = 8;
+__global__ void __launch_bounds__(256) prefill_pair_merge_kernel(PrefillArgs pa) {
     const int np = pa.n_qt / 2;
     const int pair = blockIdx.x % np;
     const int bh = blockIdx.x / np;   // batch * Hq + query head
     const int qtile = pa.q_tile;
     const int u = pa.n_qt - 1 - pair;
-    if (x3_pair_split(pa.L, qtile, pair, u) == 0) return;
+    if (pair_split(pa.L, qtile, pa.k_tile, pair, u) == 0) return;
     const int bi = bh / pa.Hq, h = bh % pa.Hq;
     const long long row0 = ((long long)bh * np + pair) * qtile;
     const float4* o0 = reinterpret_cast<const float4*>(pa.part + row0 * 128);
@@ -1448,10 +1402,10 @@ __global__ void __launch_bounds__(256) prefill_x3_merge_kernel(PrefillArgs pa) {
     const float2* ml1 = ml0 + pa.part_rows;
     const int c = threadIdx.x & 31, r0 = threadIdx.x >> 5;
     const int rows = min(qtile, pa.L - u * qtile);   // rows of the tile below L
-    float4 x[kX3MergeRows], y[kX3MergeRows];
-    float2 a[kX3MergeRows], b[kX3MergeRows];
+    float4 x[kPairMergeRows], y[kPairMergeRows];
+    float2 a[kPairMergeRows], b[kPairMergeRows];
 #pragma unroll
-    for (int i = 0; i < kX3MergeRows; ++i) {
+    for (int i = 0; i < kPairMergeRows; ++i) {
         const int r = r0 + 8 * i < rows ? r0 + 8 * i : 0;
         a[i] = ml0[r];
         b[i] = ml1[r];
@@ -1460,7 +1414,7 @@ __global__ void __launch_bounds__(256) prefill_x3_merge_kernel(PrefillArgs pa) {
     }
     float* out = pa.out + bi * pa.os[0] + h * pa.os[1] + (long long)u * qtile * pa.os[2] + 4 * c;
 #pragma unroll
-    for (int i = 0; i < kX3MergeRows; ++i) {
+    for (int i = 0; i < kPairMergeRows; ++i) {
         const int r = r0 + 8 * i;
         if (r < rows) {
             const float M = fmaxf(a[i].x, b[i].x);
@@ -1710,6 +1664,13 @@ sa_status launch_bf16_dma(const PrefillArgs& pa, dim3 grid, hipStream_t st) {
 constexpr int kSplitKS = 2;
 constexpr int kSplitGH = 2;
 
+// The second launch of a paired launch: one workgroup per (batch, query
+// head, pair).
+void launch_pair_merge(const PrefillArgs& pa, hipStream_t st) {
+    const long long n_merge = pa.part_rows / pa.q_tile;
+    hipLaunchKernelGGL(prefill_pair_merge_kernel, dim3(static_cast<unsigned>(n_merge)), dim3(256), 0, st, pa);
+}
+
 sa_status launch_bf16_split(const PrefillArgs& pa, dim3 grid, hipStream_t st) {
     constexpr int bytes = 2 * kSplitKS * kDmaStageBytes;
     sa_status s = opt_in_lds<&prefill_bf16_split_kernel<kSplitKS, kSplitGH>>(bytes);
@@ -1752,8 +1713,7 @@ sa_status launch_f32x3(const PrefillArgs& pa, dim3 grid, bool paired, hipStream_
         SA_TRY((opt_in_lds<&prefill_f32x3_kernel<W, true>>(bytes)));
         hipLaunchKernelGGL((prefill_f32x3_kernel<W, true>), grid, dim3(W * 64), bytes, st, pa);
         SA_CHECK_LAUNCH();
-        const long long n_merge = pa.part_rows / pa.q_tile;   // (batch, query head, pair)
-        hipLaunchKernelGGL(prefill_x3_merge_kernel, dim3(static_cast<unsigned>(n_merge)), dim3(256), 0, st, pa);
+        launch_pair_merge(pa, st);
         return SA_OK;
     }
     SA_TRY((opt_in_lds<&prefill_f32x3_kernel<W, false>>(bytes)));
@@ -1781,17 +1741,17 @@ struct PfPlan {
 
 // Paired three-term launches: one round of workgroups (96 KiB of LDS each,
 // so one per CU) and at least this many query tiles per head.
-constexpr int kX3PairMinTiles = 8;
+constexpr int kPairMinTiles = 8;
 
 // Rows of partials a paired launch of this plan writes: (batch, query head,
 // pair, query of the tile).
-long long x3_part_rows(const PrefillArgs& pa, int B, const PfPlan& plan) {
+long long pair_part_rows(const PrefillArgs& pa, int B, const PfPlan& plan) {
     const int n_qt = (pa.L + plan.q_tile - 1) / plan.q_tile;
     return (long long)B * pa.Hq * (n_qt / 2) * plan.q_tile;
 }
 
-size_t x3_ws_bytes(const PrefillArgs& pa, int B, const PfPlan& plan) {
-    return plan.pair ? (size_t)x3_part_rows(pa, B, plan) * 2 * (128 + 2) * sizeof(float) : 0;
+size_t pair_ws_bytes(const PrefillArgs& pa, int B, const PfPlan& plan) {
+    return plan.pair ? (size_t)pair_part_rows(pa, B, plan) * 2 * (128 + 2) * sizeof(float) : 0;
 }
 
 PfPlan plan_prefill(const PrefillArgs& pa, int B, bool bf16, int D) {
@@ -1829,6 +1789,11 @@ PfPlan plan_prefill(const PrefillArgs& pa, int B, bool bf16, int D) {
     const char* fsplit = std::getenv("SA_PREFILL_SPLIT");
     const bool split = split_shape && (fsplit ? std::atoi(fsplit) != 0
                                               : !forced && bf16_grid(pa, B, kBfWSmall) <= device_cu_count());
+    // Paired key ranges (see the three-term kernel below) measured slower
+    // here: at ~1.45 us per step of two 64-key tiles, the second segment's
+    // prologue and epilogue in workgroup A and the merge launch cost more
+    // than the steps they save (16/8 heads, graph-replayed: L = 1024 17.9
+    // against 23.5 us, L = 256 9.3 against 15.5 us).
     if (split) return {PfKind::BfSplit, 0, kSplitGH, 32, false};
     // fp32: 32-query workgroups whose waves split each tile's keys while
     // 128-query ones would give fewer than two workgroups per CU.  Measured
@@ -1852,8 +1817,8 @@ PfPlan plan_prefill(const PrefillArgs& pa, int B, bool bf16, int D) {
         const char* fpair = std::getenv("SA_PREFILL_PAIR");
         const int n_qt = (pa.L + q_tile - 1) / q_tile;
         const bool one_round = x3_grid(pa, B, W) <= device_cu_count();
-        const bool pair = one_round && n_qt >= 2 && q_tile <= 8 * kX3MergeRows &&
-                          (fpair ? std::atoi(fpair) != 0 : n_qt >= kX3PairMinTiles);
+        const bool pair = one_round && n_qt >= 2 && q_tile <= 8 * kPairMergeRows &&
+                          (fpair ? std::atoi(fpair) != 0 : n_qt >= kPairMinTiles);
         return {PfKind::F32x3, W, gh, q_tile, pair};
     }
     if (!bf16) {
@@ -1868,18 +1833,19 @@ PfPlan plan_prefill(const PrefillArgs& pa, int B, bool bf16, int D) {
 }
 
 // ws / ws_bytes: the caller's workspace, or null / 0.  A paired shape (see
-// PfPlan::pair) with a workspace of at least x3_ws_bytes takes paired key
+// PfPlan::pair) with a workspace of at least pair_ws_bytes takes paired key
 // ranges; without one, the single launch.
 sa_status launch(PrefillArgs pa, int B, bool bf16, int D, void* ws, size_t ws_bytes, hipStream_t st) {
     const PfPlan plan = plan_prefill(pa, B, bf16, D);
     pa.gh = plan.gh;
     pa.q_tile = plan.q_tile;
     pa.n_qt = (pa.L + plan.q_tile - 1) / plan.q_tile;
+    pa.k_tile = plan.kind == PfKind::F32x3 ? kX3KTile : kKTile;
     const bool paired = plan.pair && ws != nullptr;
     if (paired) {
-        if (ws_bytes < x3_ws_bytes(pa, B, plan)) return fail(SA_ENOMEM, "workspace too small for prefill partials");
+        if (ws_bytes < pair_ws_bytes(pa, B, plan)) return fail(SA_ENOMEM, "workspace too small for prefill partials");
         pa.part = static_cast<float*>(ws);
-        pa.part_rows = x3_part_rows(pa, B, plan);
+        pa.part_rows = pair_part_rows(pa, B, plan);
     }
     const int groups = B * pa.Hkv;
     pa.xcd_groups = groups % 8 == 0 ? groups / 8 : 0;
@@ -2002,7 +1968,7 @@ extern "C" size_t sa_prefill_causal_ws_bytes(sa_dtype dtype, int batch, int n_q_
     sa::PrefillArgs pa{};
     pa.Hq = n_q_heads; pa.Hkv = n_kv_heads; pa.L = L;
     const sa::PfPlan plan = sa::plan_prefill(pa, batch, dtype == SA_DTYPE_BF16, D);
-    return sa::x3_ws_bytes(pa, batch, plan);
+    return sa::pair_ws_bytes(pa, batch, plan);
 }
 
 extern "C" sa_status sa_prefill_causal(const void* q, const void* k, const void* v, sa_dtype dtype,

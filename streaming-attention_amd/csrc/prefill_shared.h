@@ -38,7 +38,8 @@ struct PrefillArgs {
     uint32_t q_sign;    // 0x80008000 to negate bf16 q pairs (negative scale), else 0
     float scale;        // signed scale (fp32 kernel)
     int q_tile;         // query rows per workgroup and head
-    float* part;        // paired three-term launches: the split tiles' partials
+    int k_tile;         // keys per tile of the kernel's loop (paired launches)
+    float* part;        // paired launches: the split tiles' partials
     long long part_rows;
 };
 
@@ -64,6 +65,67 @@ __device__ __forceinline__ Work map_work(const PrefillArgs& pa, int i) {
     w.kvh = group % pa.Hkv;
     w.h0 = w.kvh * G + (rem % HS) * pa.gh;
     return w;
+}
+
+// Paired launches (short prompts, one round of workgroups): query tile t and
+// tile u = n_qt - 1 - t form a pair whose key tiles add up to about the same
+// count for every t.  Workgroup A computes tile t whole and the first s key
+// tiles of u; workgroup B the rest of u's; so every workgroup walks about
+// half the longest tile's keys instead of up to all of them.  u's two
+// partials meet in the merge launch.  s = 0: no split, B writes u.
+
+// Key tiles (ktile keys each) of query tile t (qtile rows) under the causal mask.
+__host__ __device__ constexpr int pair_key_tiles(int L, int qtile, int ktile, int t) {
+    return ((L < (t + 1) * qtile ? L : (t + 1) * qtile) - 1) / ktile + 1;
+}
+__host__ __device__ constexpr int pair_split(int L, int qtile, int ktile, int t, int u) {
+    return (pair_key_tiles(L, qtile, ktile, u) - pair_key_tiles(L, qtile, ktile, t)) / 2;
+}
+
+// A workgroup's segments: query tile qt[i], key tiles [k0[i], k1[i]); part[i]
+// < 0 writes the output rows, else partial slot part[i] of the pair.
+struct PairSegs {
+    int n;
+    int qt[2], k0[2], k1[2], part[2];
+};
+
+// The segments of the workgroup map_work gave query tile slot wk_qt (slot
+// n_qt - 1 - wk_qt is dispatched in that order: B of each pair, then A).
+__device__ __forceinline__ PairSegs pair_segments(const PrefillArgs& pa, int wk_qt, int qtile, int ktile) {
+    const int L = pa.L;
+    const int slot = pa.n_qt - 1 - wk_qt;
+    const int np = pa.n_qt / 2;
+    PairSegs sg{1, {0, 0}, {0, 0}, {0, 0}, {-1, -1}};
+    if (slot >= 2 * np) {                     // the middle tile of an odd count
+        sg.qt[0] = np;
+        sg.k1[0] = pair_key_tiles(L, qtile, ktile, np);
+        return sg;
+    }
+    const int t = slot >> 1, u = pa.n_qt - 1 - t;
+    const int s = pair_split(L, qtile, ktile, t, u);
+    if (slot & 1) {                           // A: tile t whole, then u's first s key tiles
+        sg.qt[0] = t;
+        sg.k1[0] = pair_key_tiles(L, qtile, ktile, t);
+        if (s > 0) {
+            sg.qt[1] = u;
+            sg.k1[1] = s;
+            sg.part[1] = 0;
+            sg.n = 2;
+        }
+    } else {                                  // B: the rest of u's key tiles
+        sg.qt[0] = u;
+        sg.k0[0] = s;
+        sg.k1[0] = pair_key_tiles(L, qtile, ktile, u);
+        sg.part[0] = s > 0 ? 1 : -1;
+    }
+    return sg;
+}
+
+// Partial rows of a paired launch: [2][part_rows][128] O, then [2][part_rows]
+// (m, l); row ((b Hq + h) n_pairs + pair) qtile + query within the tile,
+// pair = n_qt - 1 - (the long tile).
+__device__ __forceinline__ long long pair_row(const PrefillArgs& pa, int b, int h, int qt, int qi) {
+    return (((long long)b * pa.Hq + h) * (pa.n_qt / 2) + (pa.n_qt - 1 - qt)) * pa.q_tile + (qi - qt * pa.q_tile);
 }
 
 // The K rows a lane feeds to the score MFMA are permuted within each 32-key

@@ -221,13 +221,15 @@ def test_prefill_fp32_paired_key_ranges(sa, oracle, synth, monkeypatch, B, L, Hq
 
 
 def test_prefill_paired_workspace_rules(sa, synth, monkeypatch):
-    """Shapes without partials ask for no workspace and ignore one (bf16; fp32
-    at L = 8192, several rounds of workgroups); a workspace one byte short
-    is refused with SA_ENOMEM, a misaligned one with SA_EINVAL, and neither
-    writes the output; a null workspace takes the single launch."""
+    """Shapes without partials ask for no workspace and ignore one (bf16;
+    fp32 at L = 8192, several rounds of workgroups, at L = 128, too few
+    query tiles, and at head_dim 64); a workspace one byte short is refused
+    with SA_ENOMEM, a misaligned one with SA_EINVAL, and neither writes the
+    output; a null workspace takes the single launch."""
     f32_variant(monkeypatch, "default")
     monkeypatch.delenv("SA_PREFILL_PAIR", raising=False)
     assert sa.prefill_ws_bytes(sa.SA_DTYPE_BF16, 1, 16, 8, 1024, 128) == 0
+    assert sa.prefill_ws_bytes(sa.SA_DTYPE_BF16, 1, 16, 8, 8192, 128) == 0
     assert sa.prefill_ws_bytes(sa.SA_DTYPE_F32, 1, 16, 8, 8192, 128) == 0
     assert sa.prefill_ws_bytes(sa.SA_DTYPE_F32, 1, 16, 8, 128, 128) == 0
     assert sa.prefill_ws_bytes(sa.SA_DTYPE_F32, 1, 16, 8, 1024, 64) == 0
