@@ -56,7 +56,9 @@ typedef enum sa_qwen3_tensor {
 } sa_qwen3_tensor;
 
 /* Allocate the weights (uninitialised), RoPE tables and the activations of a
- * batch of up to max_batch sequences (max_batch <= 64).  Requirements:
+ * batch of up to max_batch sequences (max_batch <= 1024; the projections
+ * tile rows by 64, the fused attention launches 64 sequences at a time).
+ * Requirements:
  * hidden, Hq*D, (Hq+2Hkv)*D, 2*intermediate and vocab multiples of 64;
  * hidden, Hq*D and intermediate multiples of 32; D in {64, 128}. */
 sa_status sa_qwen3_create(const sa_qwen3_desc* desc, int max_batch, sa_qwen3** out);

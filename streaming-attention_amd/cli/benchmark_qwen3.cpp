@@ -178,8 +178,8 @@ Config parse(int argc, char** argv) {
         }
     }
     if (c.attention == "streaming") c.attention_algo = "online_softmax";
-    if (c.batch_size < 1 || c.batch_size > 64) {
-        std::cerr << "error: --batch-size must be in [1, 64]\n";
+    if (c.batch_size < 1 || c.batch_size > 1024) {
+        std::cerr << "error: --batch-size must be in [1, 1024]\n";
         std::exit(1);
     }
     if (c.prompt_len < 1 || c.gen_len < 1 || c.iters < 1) {

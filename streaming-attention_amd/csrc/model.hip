@@ -8,7 +8,7 @@
 // sa_qknorm_rope_append + the causal prefill kernel (prompt), both reading
 // q, k and v straight from the qkv projection's split-K partials.
 //
-// Layout: the batch of B <= 64 token rows stays fp32 in a residual stream
+// Layout: the batch of B <= kMaxBatch token rows stays fp32 in a residual stream
 // x[B][hidden]; every projection is one GEMM Y = X W^T with bf16 weights in
 // nn.Linear layout [out][in] and fp32 accumulation, split over K into
 // fixed-order partial sums when the output is narrow, so results do not
@@ -75,7 +75,8 @@ namespace {
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kMaxRows = 64;     // batch rows one GEMM tile covers
+constexpr int kMaxRows = 64;     // batch rows one GEMM tile covers (more rows: more tiles)
+constexpr int kMaxBatch = 1024;  // decode batch rows per model (activations and logits sized for them)
 constexpr int kGN = 64;          // GEMM output columns per workgroup
 constexpr int kGK = 32;          // GEMM k chunk
 constexpr int kArgBlocks = 64;   // argmax workgroups per row
@@ -475,7 +476,7 @@ Shapes shapes_of(const sa_qwen3_desc& d, int cus) {
     s.H = d.hidden; s.I = d.intermediate; s.V = d.vocab;
     s.Hq = d.n_q_heads; s.Hkv = d.n_kv_heads; s.D = d.head_dim;
     s.Nq = s.Hq * s.D; s.Nk = s.Hkv * s.D; s.Nqkv = s.Nq + 2 * s.Nk;
-    // Decode-step projections (up to 64 rows): splits of at least 8 k-steps,
+    // Decode-step projections (64 rows per tile): splits of at least 8 k-steps,
     // 4 for the 1024-column o and down projections (16 column blocks: 256
     // workgroups instead of 128).  Measured on the 28-layer B = 64 step:
     // 20.79 ms against 20.98 ms with 2-step splits everywhere (the partials'
@@ -567,7 +568,7 @@ extern "C" sa_status sa_qwen3_create(const sa_qwen3_desc* desc, int max_batch, s
         d.hidden % kGK || nq % kGK || d.intermediate % kGK)
         return fail(SA_EINVAL, "projection sizes must be multiples of 64 (outputs) and 32 (inputs)");
     if (d.hidden > 4096) return fail(SA_EINVAL, "hidden must be at most 4096");
-    if (max_batch < 1 || max_batch > kMaxRows) return fail(SA_ERANGE, "max_batch must be in [1, 64]");
+    if (max_batch < 1 || max_batch > kMaxBatch) return fail(SA_ERANGE, "max_batch must be in [1, 1024]");
     sa_qwen3* m = new sa_qwen3();
     m->d = d;
     m->max_batch = max_batch;

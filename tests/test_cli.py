@@ -39,7 +39,7 @@ def test_help_and_bad_options():
     assert r.returncode == 1 and "unknown option" in r.stderr
     r = run("--prompt-len", "abc")
     assert r.returncode == 1
-    r = run("--batch-size", "65")
+    r = run("--batch-size", "1025")
     assert r.returncode == 1
     r = run("--phase", "prefill")          # neither --model nor --synthetic
     assert r.returncode == 1

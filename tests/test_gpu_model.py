@@ -145,6 +145,34 @@ def test_model_decode_qwen3_shape_bf16_kv(sa, oracle, synth, interleave):
     print(f"lens {lens}: worst logits rel-L2 {max(worst):.2e}")
 
 
+def test_model_decode_beyond_64_rows(sa, oracle, synth, interleave):
+    """A decode batch above one 64-row projection tile: 150 sequences of 1 ..
+    300 cached tokens (three row tiles of every projection; the fused
+    attention in launches of 64 sequences; interleaved, two half-batches of
+    more than 64 each), small model, fp32 KV, 3 greedy steps at the fp32 bar
+    against the oracle decoder."""
+    B = 150
+    lens = [1 + int(x * 299) for x in synth.uniform(90, 1, B)]
+    first = [int(x) for x in (synth.uniform(90, 2, B) * SMALL["vocab"]).astype(np.int64)]
+
+    def check(t, got, want):
+        assert np.abs(got - want).max() <= 1e-4, f"step {t}"
+        assert rel_l2(got, want) <= 1e-5, f"step {t}"
+
+    run_parity(sa, oracle, synth, SMALL, 0.1, lens, 3, sa.SA_DTYPE_F32, 33, first, check)
+
+
+def test_model_batch_limit(sa):
+    """max_batch 1 .. 1024 is accepted, 0 and 1025 refused with SA_ERANGE."""
+    import ctypes as C
+    d = sa.Qwen3Desc(1, 256, 512, 1024, 4, 2, 64, 64, 1e-6, 1e6)
+    for n, want in ((0, sa.SA_ERANGE), (1025, sa.SA_ERANGE)):
+        h = C.c_void_p()
+        assert sa.lib().sa_qwen3_create(C.byref(d), n, C.byref(h)) == want
+    model = sa.Qwen3(1024, 64, **{k: SMALL[k] for k in SHAPE_KEYS})
+    model.close()
+
+
 def test_model_rejects_bad_calls(sa):
     import ctypes as C
     model = sa.Qwen3(2, 64, **{k: SMALL[k] for k in SHAPE_KEYS})
