@@ -41,7 +41,10 @@ Dims check_qkv(const Tensor& q, const Tensor& k, const Tensor& v) {
 }
 
 // out[b, h, i, :] = softmax(scale q[b, h, i] k[b, h/rep]^T) v for every query
-// row i (no mask), through the dense decode kernel, one query row per call.
+// row i (no mask), through the dense decode kernel: q goes up once as
+// [Sq][B][Hq][D], one decode call per query row runs on the device without a
+// host round trip between calls (they share the workspace in stream order),
+// and the outputs come back once.
 Tensor decode_rows(const Tensor& q, const Tensor& k, const Tensor& v, const Dims& d, float scale) {
     auto& st = staging();
     const size_t kv = k.size();
@@ -49,24 +52,25 @@ Tensor decode_rows(const Tensor& q, const Tensor& k, const Tensor& v, const Dims
     float* dv = st.in[2].as<float>(kv);
     to_device(dk, k.data(), kv * sizeof(float));
     to_device(dv, v.data(), kv * sizeof(float));
-    const size_t nq = d.B * d.Hq * d.D;
-    float* dq = st.in[0].as<float>(nq);
-    float* dout = st.out.as<float>(nq);
+    const size_t nq = d.B * d.Hq * d.D;   // one query row of every (batch, head)
+    float* dq = st.in[0].as<float>(nq * d.Sq);
+    float* dout = st.out.as<float>(nq * d.Sq);
     const size_t ws_bytes = sa_decode_dense_ws_bytes((int)d.B, (int)d.Hq, (int)d.Sk, (int)d.D);
     void* ws = ws_bytes ? st.ws.ensure(ws_bytes) : nullptr;
-    std::vector<float> out(q.size());
-    std::vector<float> qrow(nq), orow(nq);
-    for (size_t i = 0; i < d.Sq; ++i) {
+    std::vector<float> rows(nq * d.Sq);
+    for (size_t i = 0; i < d.Sq; ++i)
         for (size_t bh = 0; bh < d.B * d.Hq; ++bh)
-            for (size_t x = 0; x < d.D; ++x) qrow[bh * d.D + x] = q[(bh * d.Sq + i) * d.D + x];
-        to_device(dq, qrow.data(), nq * sizeof(float));
-        check(sa_decode_dense_f32(dq, dk, dv, (int)d.B, (int)d.Hq, (int)d.Hkv, (int)d.Sk, (int)d.D, scale, dout,
-                                  ws, ws_bytes, nullptr),
+            for (size_t x = 0; x < d.D; ++x) rows[(i * d.B * d.Hq + bh) * d.D + x] = q[(bh * d.Sq + i) * d.D + x];
+    to_device(dq, rows.data(), rows.size() * sizeof(float));
+    for (size_t i = 0; i < d.Sq; ++i)
+        check(sa_decode_dense_f32(dq + i * nq, dk, dv, (int)d.B, (int)d.Hq, (int)d.Hkv, (int)d.Sk, (int)d.D, scale,
+                                  dout + i * nq, ws, ws_bytes, nullptr),
               "sa_decode_dense_f32");
-        to_host(orow.data(), dout, nq * sizeof(float));
+    to_host(rows.data(), dout, rows.size() * sizeof(float));
+    std::vector<float> out(q.size());
+    for (size_t i = 0; i < d.Sq; ++i)
         for (size_t bh = 0; bh < d.B * d.Hq; ++bh)
-            for (size_t x = 0; x < d.D; ++x) out[(bh * d.Sq + i) * d.D + x] = orow[bh * d.D + x];
-    }
+            for (size_t x = 0; x < d.D; ++x) out[(bh * d.Sq + i) * d.D + x] = rows[(i * d.B * d.Hq + bh) * d.D + x];
     return Tensor(std::move(out), q.shape());
 }
 
