@@ -49,15 +49,24 @@ def run(sa, cfg, model, tokens, prompt, kv_dtype):
     return np.stack(out), np.stack(toks), cache
 
 
-@pytest.mark.parametrize("B,prompt,steps", [(1, 1, 3), (2, 7, 4), (3, 130, 3), (1, 300, 2)])
-def test_prefill_then_decode_matches_reference(sa, ref, B, prompt, steps):
+# head_dim 128: the prompt's attention runs on the three-term kernel, and
+# prompts of 8 or more 32-query tiles take its paired key ranges (the model
+# passes the workspace).
+CFG128 = dict(CFG, hidden=256, head_dim=128)
+
+
+@pytest.mark.parametrize("B,prompt,steps,cfg", [(1, 1, 3, CFG), (2, 7, 4, CFG), (3, 130, 3, CFG), (1, 300, 2, CFG),
+                                                (2, 300, 2, CFG128), (1, 77, 2, CFG128)])
+def test_prefill_then_decode_matches_reference(sa, ref, B, prompt, steps, cfg):
     max_pos = prompt + steps + 1
-    model = sa.Qwen3(B, max_pos, **{k: CFG[k] for k in SHAPE_KEYS})
+    model = sa.Qwen3(B, max_pos, **{k: cfg[k] for k in SHAPE_KEYS})
     model.init_random(11 + prompt, 0.1)
-    w = host_weights(sa, model, CFG)
-    tokens = ((np.arange(B * (prompt + steps)).reshape(B, -1) * 41 + 5 * prompt) % CFG["vocab"]).astype(np.int32)
-    want = ref.qwen3_forward(w, dict(CFG, max_pos=max_pos), tokens, prompt)
-    got, toks, cache = run(sa, CFG, model, tokens, prompt, sa.SA_DTYPE_F32)
+    w = host_weights(sa, model, cfg)
+    if cfg is CFG128 and prompt >= 256:
+        assert sa.prefill_ws_bytes(sa.SA_DTYPE_F32, B, cfg["n_q_heads"], cfg["n_kv_heads"], prompt, 128) > 0
+    tokens = ((np.arange(B * (prompt + steps)).reshape(B, -1) * 41 + 5 * prompt) % cfg["vocab"]).astype(np.int32)
+    want = ref.qwen3_forward(w, dict(cfg, max_pos=max_pos), tokens, prompt)
+    got, toks, cache = run(sa, cfg, model, tokens, prompt, sa.SA_DTYPE_F32)
     cache.close()
     model.close()
     assert np.abs(got - want).max() <= 1e-4
