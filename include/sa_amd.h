@@ -308,7 +308,10 @@ sa_status sa_prefill_causal_strided(const void* q, const void* k, const void* v,
                                     const int64_t out_strides[3], float scale, float* out,
                                     sa_stream_t stream);
 
-/* The same two calls with a caller workspace.  fp32 at head_dim 128 on a grid
+/* The same two calls with a caller workspace (they replace the same
+ * reference functions, ops.cpp:1027-1112 and :1383-1599, whose per-call
+ * std::vector state, :1040-1041 and :1075, the workspace stands for).
+ * fp32 at head_dim 128 on a grid
  * of one round of workgroups (short prompts: 16/8 heads up to L = 2048)
  * pairs the longest query tiles with the shortest and splits the pair's key
  * tiles evenly between two workgroups, whose partials a second launch merges;
