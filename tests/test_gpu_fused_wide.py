@@ -21,7 +21,9 @@ tensor_cpp/src/ops.cpp:514-641) on the K/V the cache holds.
 Lengths span 0 .. 4,095 cached tokens (1 to 16 chunks of the default 256
 tokens; up to 32 forced chunks of 128 and 64 of 64, where bf16 workgroups
 have waves without a tile), on shuffled pages, called in a shuffled row
-order.
+order.  The fused launch's grid covers only the chunks that hold tokens;
+SA_DECODE_COMPACT=0 runs the full (KV head, chunk, sequence) grid, and both
+are held to the same bit-equality.
 """
 from __future__ import annotations
 
@@ -113,10 +115,19 @@ def compare(sa, oracle, synth, a, b, lens, order, out_a, qa, out_b, qb, commit, 
         assert err <= 1e-4 and rel <= 1e-5, (s, lens[s], err, rel)
 
 
+@pytest.fixture(params=["compact", "full"])
+def grid_env(request, monkeypatch):
+    if request.param == "full":
+        monkeypatch.setenv("SA_DECODE_COMPACT", "0")
+    else:
+        monkeypatch.delenv("SA_DECODE_COMPACT", raising=False)
+    return request.param
+
+
 @pytest.mark.parametrize("chunk_env", [None, 128, 64], indirect=True)
 @pytest.mark.parametrize("n_seq,commit", [(40, True), (72, True), (72, False)])
 @pytest.mark.parametrize("kv", ["f32", "bf16"])
-def test_fused_wide_grid_equals_three_calls(sa, oracle, synth, chunk_env, n_seq, commit, kv):
+def test_fused_wide_grid_equals_three_calls(sa, oracle, synth, chunk_env, n_seq, commit, kv, grid_env):
     assert HKV * min(n_seq, 64) > torch.cuda.get_device_properties(0).multi_processor_count
     dt = sa.SA_DTYPE_F32 if kv == "f32" else sa.SA_DTYPE_BF16
     seed = 300 + n_seq + (chunk_env or 0)
