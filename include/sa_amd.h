@@ -235,7 +235,10 @@ sa_status sa_qk_norm_rope_ex(const float* x, int n_rows, int D, const int32_t* p
  * step).  seq_ids: host array [n_seq] of cache rows, or NULL for
  * 0..n_seq-1; every row must have pages for seq_len + n_pending tokens
  * (SA_ERANGE otherwise).  A sequence of length 0 gets a zero output.
- * q [n_seq][n_q_heads][D] fp32, out likewise.
+ * seq_len is the cache's committed length as the library's calls have set
+ * it (the host copy the launch is sized from, published to the device in
+ * stream order); lengths written into sa_kvcache_seq_lens by other code are
+ * not read.  q [n_seq][n_q_heads][D] fp32, out likewise.
  * ws must hold sa_paged_decode_ws_bytes(...) bytes.
  * ------------------------------------------------------------------------ */
 size_t sa_paged_decode_ws_bytes(const sa_kvcache* cache, int n_seq, int n_q_heads);

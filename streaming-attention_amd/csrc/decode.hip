@@ -99,10 +99,13 @@ struct DecodeArgs {
     float eps;
     int rope_max_pos;
     int commit;
-    // Compact grid (FUSED only): blockIdx.y runs over the chunks that hold
-    // tokens, sequence i's at cstart[i] .. cstart[i + 1] - 1 (entries past
-    // the launch's sequences hold INT_MAX), and blockIdx.z is 0.
+    // Compact grid (paged launches): blockIdx.y runs over the chunks that
+    // hold tokens, sequence i's at cstart[i] .. cstart[i + 1] - 1 (entries
+    // past the launch's sequences hold INT_MAX), and blockIdx.z is 0.
     int compact;
+    // Paged, not FUSED: the committed lengths come from pos (host values)
+    // instead of seq_lens.
+    int host_lens;
     int32_t cstart[kRowsPerLaunch + 1];
 };
 
@@ -266,7 +269,7 @@ split_kv_decode_kernel(DecodeArgs a) {
     const int g = blockIdx.x;      // kv head
     int split = blockIdx.y;
     int seq = blockIdx.z;          // batch row
-    if constexpr (FUSED) {
+    if constexpr (PAGED) {
         if (a.compact) {
             // the last sequence whose first chunk is at or before blockIdx.y
             int lo = 0, hi = kRowsPerLaunch;
@@ -295,7 +298,8 @@ split_kv_decode_kernel(DecodeArgs a) {
             pos = a.pos.row[seq];
             len = min(min(pos + 1, a.max_pages * 64), a.n_split * a.chunk);
         } else {
-            len = min(min(a.seq_lens[cache_row] + a.n_pending, a.max_pages * 64), a.n_split * a.chunk);
+            const int committed = a.host_lens ? a.pos.row[seq] : a.seq_lens[cache_row];
+            len = min(min(committed + a.n_pending, a.max_pages * 64), a.n_split * a.chunk);
         }
         if (len <= 0) {
             // An empty sequence attends to nothing: its output is zero.
@@ -623,7 +627,8 @@ lse_merge_kernel(DecodeArgs a) {
         len = min(min(a.pos.row[seq] + 1, a.max_pages * 64), a.n_split * a.chunk);
     } else if constexpr (PAGED) {
         const int row = a.rows.row[seq];
-        len = min(min(a.seq_lens[row] + a.n_pending, a.max_pages * 64), a.n_split * a.chunk);
+        const int committed = a.host_lens ? a.pos.row[seq] : a.seq_lens[row];
+        len = min(min(committed + a.n_pending, a.max_pages * 64), a.n_split * a.chunk);
     } else {
         len = a.T;
     }
@@ -771,7 +776,7 @@ template <int D, int NREP, bool BF16, bool PAGED, bool FUSED>
 sa_status launch_decode(const DecodeArgs& a, int n_seq, hipStream_t st) {
     constexpr int W = waves_for<D, NREP>();
     dim3 grid(a.n_kv, a.n_split, n_seq);
-    if (FUSED && a.compact) grid = dim3(a.n_kv, a.cstart[n_seq], 1);
+    if (PAGED && a.compact) grid = dim3(a.n_kv, a.cstart[n_seq], 1);
     if constexpr (NREP == 1 && !PAGED) {
         if ((long long)a.n_split * a.n_kv * n_seq <= device_cu_count()) {
             hipLaunchKernelGGL((split_kv_decode_kernel<D, NREP, BF16, PAGED, kWavesOneRound>), grid,
@@ -907,8 +912,8 @@ size_t paged_ws(int n_seq, int n_q, int n_kv, int d, int max_pages) {
 }
 
 sa_status decode_paged(const PagedView& c, const float* q, int n_seq, const int32_t* seq_ids,
-                       int n_q, int n_pending, int max_len, long long total_len, float scale,
-                       float* out, void* ws, size_t ws_bytes, hipStream_t st) {
+                       const int32_t* lens, int n_q, int n_pending, int max_len, long long total_len,
+                       float scale, float* out, void* ws, size_t ws_bytes, hipStream_t st) {
     if (!q || !out) return fail(SA_EINVAL, "null pointer");
     if (n_seq <= 0 || n_q <= 0 || n_q % c.n_kv) return fail(SA_EINVAL, "bad head counts");
     if (!aligned16(q) || !aligned16(out)) return fail(SA_EINVAL, "q and out must be 16-byte aligned");
@@ -934,6 +939,17 @@ sa_status decode_paged(const PagedView& c, const float* q, int n_seq, const int3
     for (int i0 = 0; i0 < n_seq; i0 += kRowsPerLaunch) {
         const int m = std::min(kRowsPerLaunch, n_seq - i0);
         for (int i = 0; i < m; ++i) a.rows.row[i] = seq_ids ? seq_ids[i0 + i] : i0 + i;
+        if (lens) {
+            a.host_lens = 1;
+            a.cstart[0] = 0;
+            for (int i = 0; i < m; ++i) {
+                a.pos.row[i] = lens[i0 + i];
+                const int len = std::min(std::min(lens[i0 + i] + n_pending, c.max_pages * 64), a.n_split * a.chunk);
+                a.cstart[i + 1] = a.cstart[i] + std::max(1, (len + a.chunk - 1) / a.chunk);
+            }
+            for (int i = m; i < kRowsPerLaunch; ++i) a.cstart[i + 1] = 0x7fffffff;
+            a.compact = env_int("SA_DECODE_COMPACT", 1) != 0 && a.cstart[m] <= 65535 ? 1 : 0;
+        }
         a.q = q + (size_t)i0 * n_q * c.d;
         a.out = out + (size_t)i0 * n_q * c.d;
         if (c.bf16) {

@@ -551,7 +551,9 @@ extern "C" sa_status sa_paged_decode(const sa_kvcache* c, int layer, const float
     pv.n_kv = c->desc.num_kv_heads; pv.d = c->desc.head_dim;
     pv.max_pages = c->desc.max_pages_per_seq; pv.num_pages = c->desc.num_pages;
     pv.bf16 = c->desc.kv_dtype == SA_DTYPE_BF16;
-    return decode_paged(pv, q, n_seq, seq_ids, n_q_heads, n_pending, max_len, total, scale, out, ws,
+    std::vector<int32_t> lens(n_seq);
+    for (int i = 0; i < n_seq; ++i) lens[i] = c->pt.len(seq_ids ? seq_ids[i] : i);
+    return decode_paged(pv, q, n_seq, seq_ids, lens.data(), n_q_heads, n_pending, max_len, total, scale, out, ws,
                         ws_bytes, as_stream(stream));
 }
 

@@ -270,9 +270,12 @@ sa_status append_decode_partials(sa_kvcache* c, int layer, const float* part, in
 
 size_t paged_ws(int n_seq, int n_q, int n_kv, int d, int max_pages);
 // seq_ids: host array of cache rows (NULL: 0 .. n_seq-1), already checked.
+// lens: the rows' committed lengths (host array in call order, the page
+// table's mirror): the launches read them instead of the device lengths and
+// size their grids to the chunks that hold tokens.
 sa_status decode_paged(const PagedView& c, const float* q, int n_seq, const int32_t* seq_ids,
-                       int n_q, int n_pending, int max_len, long long total_len, float scale,
-                       float* out, void* ws, size_t ws_bytes, hipStream_t st);
+                       const int32_t* lens, int n_q, int n_pending, int max_len, long long total_len,
+                       float scale, float* out, void* ws, size_t ws_bytes, hipStream_t st);
 
 // The append half of a fused decode step: the new token of every sequence
 // (raw q [n_seq][n_q][D] is decode_paged's q; k, v [n_seq][n_kv][D]), its
