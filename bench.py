@@ -314,6 +314,38 @@ def cpu_prefill(L: int):
                       f"{warm} warmup call(s), median of {reps} timed calls: {med:.4f} s"}
 
 
+def cpu_prefill_sequence(L: int):
+    """Causal prefill on the CPU along the reference's `mpi+avx2
+    --parallel-strategy sequence` path at one rank: the oracle's restatement of
+    attention_sequence_online_softmax_avx2's loop (AVX2/FMA, one thread: the
+    reference's OpenMP loop runs over the batch of 1).  Timing only: that path's
+    numerics are wrong (its weights multiply s_j v_j), so nothing is checked."""
+    from oracle import Oracle
+    oracle = Oracle()
+    HQ, HKV, D = 16, 8, 128
+    rng = np.random.default_rng(61)       # timing inputs only: N(0,1), results unchecked
+    q = rng.standard_normal((1, HQ, L, D), dtype=np.float32)
+    k, v = (rng.standard_normal((1, HKV, L, D), dtype=np.float32) for _ in range(2))
+    sc = float(1 / np.sqrt(D))
+    # Every head does the same work, so above L = 1024 one head of the 16 is
+    # timed and the call time scaled by 16 (a few seconds of CPU per call).
+    heads = HQ if L <= 1024 else 1
+    warm, reps = (2, 10) if L <= 1024 else (1, 3)
+    for _ in range(warm):
+        oracle.sequence_np1(q, k, v, sc, heads=(0, heads))
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        oracle.sequence_np1(q, k, v, sc, heads=(0, heads))
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times) * HQ / heads
+    tf = 2.0 * HQ * D * L * (L + 1) / med / 1e12
+    return {"value": round(tf, 5), "unit": "TFLOP/s", "cores": 1, "kind": "port", "host": host_cpu(),
+            "sample": f"np=1 sequence-parallel online-softmax loop (mpi+avx2 --parallel-strategy sequence), "
+                      f"L={L}, {heads} of 16 heads timed, {warm} warmup call(s), median of {reps} timed calls, "
+                      f"scaled to 16 heads: {med:.4f} s per call; timing only (the path's numerics are wrong)"}
+
+
 def cpu_model_decode(sum_len: int, B: int = 64, layers: int = 28, steps: int = 3):
     """The 28-layer batched decode on the CPU, extrapolated: one reference decoder layer
     (qwen3_decoder_layer_avx_with_cache, STREAMING, Qwen3-0.6B shapes) on one
@@ -727,6 +759,9 @@ def main() -> int:
             if cpu_extra:
                 log(f"[bench] CPU: reference blockwise AVX2 prefill L={L}")
                 extra[f"prefill_L{L}_cpu_baseline"] = cpu_prefill(L)
+            if args.cpu_budget >= 1.0:
+                log(f"[bench] CPU: np=1 sequence-parallel prefill loop L={L} (timing only)")
+                extra[f"prefill_L{L}_cpu_sequence_np1"] = cpu_prefill_sequence(L)
     if run("model"):
         torch.cuda.empty_cache()
         log("[bench] 28-layer Qwen3-0.6B-shape greedy decode, 64 sequences, bf16 KV")

@@ -34,6 +34,7 @@ _ORACLE_SIGS = {
     "or_decode_streaming_compat": (None, [_P, _P, _P, _I, _I, _I, _I, _F, _I, _P]),
     "or_prefill_blockwise": (None, [_P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _P, _I, _P]),
     "or_sdpa_f64": (None, [_P, _P, _P, _I, _I, _I, _D, _I, _I, _P]),
+    "or_sequence_np1": (None, [_P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _P]),
 }
 
 _REF_SIGS = {
@@ -173,6 +174,22 @@ class Oracle:
         L = k.shape[0]
         out = np.empty((nq, D), np.float64)
         self.lib.or_sdpa_f64(_p(q), _p(k), _p(v), nq, L, D, float(scale), int(causal), pos0, _p(out))
+        return out
+
+
+    def sequence_np1(self, q, k, v, scale, heads=None):
+        """TIMING ONLY: the np = 1 loop of the reference's MPI sequence-parallel
+        prefill (numerically wrong there and here).  q [B, Hq, L, D], k/v
+        [B, Hkv, L, D]; heads (first, count) limits the work to a head range
+        (the other heads' rows stay zero)."""
+        q, k, v = _f32(q), _f32(k), _f32(v)
+        B, Hq, L, D = q.shape
+        Hkv = k.shape[1]
+        h0, nh = (0, Hq) if heads is None else heads
+        if not (0 <= h0 and nh >= 0 and h0 + nh <= Hq):
+            raise ValueError("head range outside [0, Hq)")
+        out = np.zeros_like(q)
+        self.lib.or_sequence_np1(_p(q), _p(k), _p(v), B, Hq, Hkv, L, D, scale, h0, nh, _p(out))
         return out
 
 

@@ -17,6 +17,8 @@
  *   each is checked against the reference compiled from its own sources
  *   (oracle/_ref) on committed golden vectors, and against the fp64 forms
  *   and closed-form invariants.
+ *   or_sequence_np1 (timing only: the reference's MPI path cannot be built
+ *   here, mpi.h is absent) is checked against its closed form in fp64.
  */
 #include <math.h>
 #include <stdlib.h>
@@ -328,4 +330,125 @@ void or_sdpa_f64(const float* q, const float* k, const float* v, int nq, int L, 
         }
         free(s);
     }
+}
+
+/* TIMING ONLY, never a checker.  The np = 1 loop of the MPI sequence-parallel
+ * prefill attention (reference tensor_cpp/src/ops_mpi.cpp:1216-1454,
+ * attention_sequence_online_softmax_avx2, the `mpi+avx2
+ * --parallel-strategy sequence` path) for query heads [h0, h0 + nh) of every
+ * batch row: the same per-query work in the same order, AVX2/FMA like the
+ * reference's build, one thread (the reference's OpenMP loop runs over the
+ * batch, which is 1 in the prefill benchmark).  Per query i (q scaled
+ * first, :1257-1270) and per 64-key block holding a key j <= i (:1274-1290):
+ * fresh zeroed block buffers (:1293-1294); for each such key the score
+ * s_j = q'.k_j (8-lane FMA then a horizontal sum, :1303-1320) and s_j v_j
+ * (:1325-1339); the block max over every slot, the masked ones holding 0
+ * (:1343-1345); e_j = exp(s_j - m) over the valid keys (:1348-1360); the
+ * running sum and the O row rescaled by exp(m_old - m) (:1363-1381), then
+ * O += e_j (s_j v_j) (:1384-1407).  With one rank the Allreduce is skipped
+ * and the correction factor is exp(0) = 1 (:1414-1438): out = O / l.
+ *
+ * Its numerics are the reference's, which are wrong: the weights multiply
+ * s_j v_j, not v_j, so out_i = sum_{j<=i} e^{s_j} s_j v_j / sum_{j<=i} e^{s_j}
+ * (the maxima cancel).  tests/test_oracle.py pins it to that closed form in
+ * fp64.  q [B][Hq][L][D], k/v [B][Hkv][L][D], out [B][Hq][L][D] (heads
+ * outside the range untouched). */
+#include <immintrin.h>
+
+__attribute__((target("avx2,fma"))) static float or_hsum8(__m256 x) {
+    const __m128 s4 = _mm_add_ps(_mm256_castps256_ps128(x), _mm256_extractf128_ps(x, 1));
+    const __m128 s2 = _mm_add_ps(s4, _mm_movehl_ps(s4, s4));
+    return _mm_cvtss_f32(_mm_add_ss(s2, _mm_shuffle_ps(s2, s2, 1)));
+}
+
+__attribute__((target("avx2,fma"))) void or_sequence_np1(const float* q, const float* k, const float* v, int B,
+                                                         int Hq, int Hkv, int L, int D, float scale, int h0,
+                                                         int nh, float* out) {
+    const int rep = Hq / Hkv;
+    const int KB = 64;
+    const size_t nstat = (size_t)B * Hq * L;
+    float* m_all = (float*)malloc(sizeof(float) * nstat);
+    float* l_all = (float*)malloc(sizeof(float) * nstat);
+    for (size_t i = 0; i < nstat; ++i) { m_all[i] = -INFINITY; l_all[i] = 0.0f; }
+    for (int b = 0; b < B; ++b)
+        for (int h = h0; h < h0 + nh; ++h) {
+            const float* kb = k + ((size_t)b * Hkv + h / rep) * (size_t)L * D;
+            const float* vb = v + ((size_t)b * Hkv + h / rep) * (size_t)L * D;
+            for (int i = 0; i < L; ++i) {
+                const size_t row = ((size_t)b * Hq + h) * L + i;
+                float* o = out + row * D;
+                memset(o, 0, sizeof(float) * (size_t)D);
+                float* qs = (float*)malloc(sizeof(float) * (size_t)D);
+                const float* qr = q + row * D;
+                const __m256 vs = _mm256_set1_ps(scale);
+                int d = 0;
+                for (; d + 8 <= D; d += 8) _mm256_storeu_ps(qs + d, _mm256_mul_ps(_mm256_loadu_ps(qr + d), vs));
+                for (; d < D; ++d) qs[d] = qr[d] * scale;
+                for (int j0 = 0; j0 < L; j0 += KB) {
+                    const int j1 = j0 + KB < L ? j0 + KB : L;
+                    int any = 0;                   /* a key of the block is <= i */
+                    for (int j = j0; j < j1; ++j)
+                        if (j <= i) { any = 1; break; }
+                    if (!any) continue;
+                    const int n = j1 - j0;
+                    float* sc = (float*)calloc((size_t)n, sizeof(float));
+                    float* wv = (float*)calloc((size_t)n * D, sizeof(float));
+                    for (int j = j0; j < j1 && j <= i; ++j) {
+                        const float* kr = kb + (size_t)j * D;
+                        __m256 acc = _mm256_setzero_ps();
+                        d = 0;
+                        for (; d + 8 <= D; d += 8)
+                            acc = _mm256_fmadd_ps(_mm256_loadu_ps(qs + d), _mm256_loadu_ps(kr + d), acc);
+                        float s = d > 0 ? or_hsum8(acc) : 0.0f;
+                        for (; d < D; ++d) s += qs[d] * kr[d];
+                        sc[j - j0] = s;
+                        const float* vr = vb + (size_t)j * D;
+                        float* w = wv + (size_t)(j - j0) * D;
+                        const __m256 sv = _mm256_set1_ps(s);
+                        d = 0;
+                        for (; d + 8 <= D; d += 8) _mm256_storeu_ps(w + d, _mm256_mul_ps(sv, _mm256_loadu_ps(vr + d)));
+                        for (; d < D; ++d) w[d] = s * vr[d];
+                    }
+                    float bm = sc[0];
+                    for (int t = 1; t < n; ++t) bm = sc[t] > bm ? sc[t] : bm;
+                    const float m_old = m_all[row];
+                    const float m_new = m_old > bm ? m_old : bm;
+                    m_all[row] = m_new;
+                    float* e = (float*)calloc((size_t)n, sizeof(float));
+                    float esum = 0.0f;
+                    for (int j = j0; j < j1 && j <= i; ++j) {
+                        e[j - j0] = expf(sc[j - j0] - m_new);
+                        esum += e[j - j0];
+                    }
+                    const float f = expf(m_old - m_new);
+                    l_all[row] = l_all[row] * f + esum;
+                    const __m256 vf = _mm256_set1_ps(f);
+                    d = 0;
+                    for (; d + 8 <= D; d += 8) _mm256_storeu_ps(o + d, _mm256_mul_ps(_mm256_loadu_ps(o + d), vf));
+                    for (; d < D; ++d) o[d] *= f;
+                    for (int j = j0; j < j1 && j <= i; ++j) {
+                        const float* w = wv + (size_t)(j - j0) * D;
+                        const __m256 ve = _mm256_set1_ps(e[j - j0]);
+                        d = 0;
+                        for (; d + 8 <= D; d += 8)
+                            _mm256_storeu_ps(o + d, _mm256_fmadd_ps(ve, _mm256_loadu_ps(w + d), _mm256_loadu_ps(o + d)));
+                        for (; d < D; ++d) o[d] += e[j - j0] * w[d];
+                    }
+                    free(e);
+                    free(wv);
+                    free(sc);
+                }
+                free(qs);
+            }
+        }
+    /* the normalisation pass; with one rank the global statistics are the local ones */
+    for (int b = 0; b < B; ++b)
+        for (int h = h0; h < h0 + nh; ++h)
+            for (int i = 0; i < L; ++i) {
+                const size_t row = ((size_t)b * Hq + h) * L + i;
+                const float corr = expf(m_all[row] - m_all[row]);
+                for (int d = 0; d < D; ++d) out[row * D + d] = out[row * D + d] * corr / l_all[row];
+            }
+    free(l_all);
+    free(m_all);
 }

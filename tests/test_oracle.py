@@ -297,6 +297,49 @@ def test_prefill_rows_are_prefix_attention(oracle, synth):
     np.testing.assert_allclose(out[0, :, L - 1], dec[0], atol=2e-6)
 
 
+def _sequence_np1_closed_form(q, k, v, sc):
+    """fp64: out_i = sum_{j<=i} e^{s_j} s_j v_j / sum_{j<=i} e^{s_j}, s_j = (q_i sc).k_j,
+    the value the np = 1 sequence-parallel loop computes (its weights multiply
+    s_j v_j)."""
+    B, Hq, L, D = q.shape
+    rep = Hq // k.shape[1]
+    qs = (q * np.float32(sc)).astype(np.float32).astype(np.float64)
+    out = np.zeros(q.shape)
+    for b in range(B):
+        for h in range(Hq):
+            kk = k[b, h // rep].astype(np.float64)
+            vv = v[b, h // rep].astype(np.float64)
+            s = qs[b, h] @ kk.T
+            for i in range(L):
+                si = s[i, : i + 1]
+                e = np.exp(si - si.max())
+                out[b, h, i] = (e[:, None] * si[:, None] * vv[: i + 1]).sum(0) / e.sum()
+    return out
+
+
+@pytest.mark.parametrize("D", [32, 36])
+def test_sequence_np1_closed_form(oracle, synth, D):
+    """The timing-only restatement of the np = 1 sequence-parallel loop
+    (reference ops_mpi.cpp:1216-1454) against its closed form in fp64, at a
+    ragged length (150 keys: blocks of 64, 64, 22), GQA 2, a head size with and
+    without a scalar tail, batch 2; a head range leaves the other heads zero."""
+    B, Hq, Hkv, L = 2, 4, 2, 150
+    q = synth.normal(71, 1, (B, Hq, L, D))
+    k = synth.normal(71, 2, (B, Hkv, L, D))
+    v = synth.normal(71, 3, (B, Hkv, L, D))
+    sc = float(1 / np.sqrt(D))
+    want = _sequence_np1_closed_form(q, k, v, sc)
+    got = oracle.sequence_np1(q, k, v, sc)
+    assert rel_l2(got, want) < 1e-5
+    assert np.abs(got - want).max() < 1e-4
+    part = oracle.sequence_np1(q, k, v, sc, heads=(1, 2))
+    np.testing.assert_array_equal(part[:, 1:3], got[:, 1:3])
+    assert not part[:, 0].any() and not part[:, 3].any()
+    # the path's known-wrong numerics: it is not causal attention
+    true = oracle.prefill_blockwise(q, k, v, np.float32(sc), 64)
+    assert rel_l2(got, true) > 0.5
+
+
 # ------------------------------------------------------------------ the checks catch mistakes
 
 def test_mistake_hf_rope_convention_is_caught(oracle):
