@@ -264,9 +264,12 @@ extern "C" sa_status sa_kvcache_create(const sa_kv_desc* d, sa_kvcache** out) {
         return fail(SA_EINVAL, "head_dim must be 8, 16, 32, 64, 128 or 256");
     if (d->kv_dtype != SA_DTYPE_F32 && d->kv_dtype != SA_DTYPE_BF16)
         return fail(SA_EINVAL, "kv_dtype must be F32 or BF16");
+    int device = 0;
+    const hipError_t de = hipGetDevice(&device);
+    if (de != hipSuccess) return hip_fail(de, "hipGetDevice");
     auto* c = new sa_kvcache();
     c->desc = *d;
-    hipGetDevice(&c->device);
+    c->device = device;
     c->elem_bytes = d->kv_dtype == SA_DTYPE_BF16 ? 2 : 4;
     c->page_bytes = (size_t)d->num_kv_heads * 64 * d->head_dim * c->elem_bytes;
     c->layer_bytes = 2 * c->page_bytes * (size_t)d->num_pages;
@@ -280,7 +283,9 @@ extern "C" sa_status sa_kvcache_create(const sa_kv_desc* d, sa_kvcache** out) {
     e = hipMalloc(&c->d_table, n_table * sizeof(int32_t));
     if (e == hipSuccess) e = hipMalloc(&c->d_lens, (size_t)d->max_seqs * sizeof(int32_t));
     if (e != hipSuccess) {
-        hipFree(c->pool); hipFree(c->d_table); hipFree(c->d_lens);
+        (void)hipFree(c->pool);
+        (void)hipFree(c->d_table);
+        (void)hipFree(c->d_lens);
         delete c;
         return fail(SA_ENOMEM, "KV table allocation failed");
     }
@@ -301,10 +306,12 @@ extern "C" sa_status sa_kvcache_create(const sa_kv_desc* d, sa_kvcache** out) {
 extern "C" sa_status sa_kvcache_destroy(sa_kvcache* c) {
     clear_error();
     if (!c) return SA_OK;
-    hipDeviceSynchronize();
-    hipFree(c->pool);
-    hipFree(c->d_table);
-    hipFree(c->d_lens);
+    // Best effort: work still queued on the cache must finish before its
+    // memory goes; a failure here leaves nothing else to do.
+    (void)hipDeviceSynchronize();
+    (void)hipFree(c->pool);
+    (void)hipFree(c->d_table);
+    (void)hipFree(c->d_lens);
     delete c;
     return SA_OK;
 }

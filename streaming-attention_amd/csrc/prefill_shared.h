@@ -156,7 +156,10 @@ typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 // of them (vmcnt(0)), which would drain the tile prefetched NS - 1 tiles ahead
 // in the middle of each tile.  The kernel waits for these loads itself
 // (s_waitcnt vmcnt before each tile barrier).  m0 holds the LDS address; the
-// s_nop covers the m0-write-to-load-to-LDS hazard.
+// s_nop covers the m0-write-to-load-to-LDS hazard.  hipcc warns that m0 in a
+// clobber list is reserved; no code it generates for these kernels reads or
+// writes m0 (every m0 access in their ISA is this block's), so nothing it
+// holds there is lost.
 __device__ __forceinline__ void dma16(const uint16_t* g, lds_u8_t* dst) {
     const uint32_t m = static_cast<uint32_t>(reinterpret_cast<size_t>(dst));
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m) : "memory", "m0");
