@@ -252,10 +252,10 @@ __device__ __forceinline__ void consume(const TileRegs<Geo<D, BF16>::R>& regs, i
 // from the launch arguments, so no workgroup reads the device length another
 // one writes.
 // PF: each wave keeps the next tile's loads in flight while it reduces the
-// current one (two register tiles).  Dense single-head launches whose waves
-// walk at most two tiles take PF = false: one register tile (100 VGPRs
-// against 199 at fp32 d = 128), bit-identical, graph-replayed T = 65536
-// 16.21 against 16.50 us per call, T = 8192 8.34 against 8.65 us; at
+// current one (two register tiles).  One-round launches whose waves walk at
+// most two tiles take PF = false: one register tile (100 VGPRs against 199
+// at fp32 d = 128), bit-identical; dense single-head calls graph-replayed
+// T = 65536 16.21 against 16.50 us, T = 8192 8.34 against 8.65 us; at
 // T = 262144 (eight tiles per wave) the prefetch keeps 45.1 against 46.1 us.
 template <int D, int NREP, bool BF16, bool PAGED, int W, bool FUSED = false, bool PF = true>
 __global__ void __launch_bounds__(W * kWave)
@@ -799,8 +799,15 @@ sa_status launch_decode(const DecodeArgs& a, int n_seq, hipStream_t st) {
         // decode step of a few rows) use eight waves: half the tiles per
         // wave, so fewer dependent load round trips.
         if ((long long)a.n_split * a.n_kv * n_seq <= device_cu_count()) {
-            hipLaunchKernelGGL((split_kv_decode_kernel<D, NREP, BF16, PAGED, kWavesOneRound, FUSED>), grid,
-                               dim3(kWavesOneRound * kWave), 0, st, a);
+            // One register tile when every wave walks at most two tiles
+            // (config-3 loop, graph-replayed: fp32 fused step 7.31-7.36 ->
+            // 6.51-6.54 us, bf16 6.71-6.76 -> 6.60 us, same box).
+            if (a.chunk <= 2 * kWavesOneRound * Geo<D, BF16>::TILE)
+                hipLaunchKernelGGL((split_kv_decode_kernel<D, NREP, BF16, PAGED, kWavesOneRound, FUSED, false>), grid,
+                                   dim3(kWavesOneRound * kWave), 0, st, a);
+            else
+                hipLaunchKernelGGL((split_kv_decode_kernel<D, NREP, BF16, PAGED, kWavesOneRound, FUSED>), grid,
+                                   dim3(kWavesOneRound * kWave), 0, st, a);
         } else {
             hipLaunchKernelGGL((split_kv_decode_kernel<D, NREP, BF16, PAGED, W, FUSED>), grid, dim3(W * kWave), 0, st,
                                a);
