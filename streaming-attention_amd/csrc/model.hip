@@ -932,20 +932,27 @@ extern "C" sa_status sa_qwen3_decode_step(sa_qwen3* m, sa_kvcache* cache, const 
         hipEvent_t fork = m->events[0], join = m->events[1], a_first = m->events[2];
         SA_HIP_TRY(hipEventRecord(fork, st));
         SA_HIP_TRY(hipStreamWaitEvent(m->side, fork, 0));
-        SA_TRY(qkv(a, 0));
-        SA_TRY(qkv(b, 0));
-        for (int l = 0; l < d.num_layers; ++l) {
-            SA_TRY(attention(a, l));
-            if (l == 0) SA_HIP_TRY(hipEventRecord(a_first, st));
-            SA_TRY(rest(a, l));
-            if (l + 1 < d.num_layers) SA_TRY(qkv(a, l + 1));
-            if (l == 0) SA_HIP_TRY(hipStreamWaitEvent(m->side, a_first, 0));
-            SA_TRY(attention(b, l));
-            SA_TRY(rest(b, l));
-            if (l + 1 < d.num_layers) SA_TRY(qkv(b, l + 1));
-        }
+        auto layers = [&]() -> sa_status {
+            SA_TRY(qkv(a, 0));
+            SA_TRY(qkv(b, 0));
+            for (int l = 0; l < d.num_layers; ++l) {
+                SA_TRY(attention(a, l));
+                if (l == 0) SA_HIP_TRY(hipEventRecord(a_first, st));
+                SA_TRY(rest(a, l));
+                if (l + 1 < d.num_layers) SA_TRY(qkv(a, l + 1));
+                if (l == 0) SA_HIP_TRY(hipStreamWaitEvent(m->side, a_first, 0));
+                SA_TRY(attention(b, l));
+                SA_TRY(rest(b, l));
+                if (l + 1 < d.num_layers) SA_TRY(qkv(b, l + 1));
+            }
+            return SA_OK;
+        };
+        const sa_status ls = layers();
+        // Joined on failure too, so the caller's stream orders after whatever
+        // the side stream was given.
         SA_HIP_TRY(hipEventRecord(join, m->side));
         SA_HIP_TRY(hipStreamWaitEvent(st, join, 0));
+        if (ls != SA_OK) return ls;
     }
     // ---- final norm (folded above), lm_head, greedy argmax ----
     SA_TRY(gemm(m->h, M, m->lm_head, s.lm, out_logits, st));
